@@ -1,0 +1,280 @@
+#!/usr/bin/env python3
+"""bench.py -- INT4 GEMV HBM GB/s at the Llama-3-8B decode shapes (plus the FP8
+E4M3 per-token quantizer's GB/s) on one MI355X.
+
+A step is one Llama-3-8B decode layer's four INT4 GEMVs (M = 1, group size
+128, bf16 activation and output, fp32 accumulation): fused QKV (K 4096,
+N 6144), O (4096, 4096), fused gate/up (4096, 28672), down (14336, 4096).
+`value` is algorithmic bytes per step (packed weights + fp32 scales + zero
+nibbles + x + y: 116 858 880 B) times steps over the wall-clock time of the
+timed steps, bracketed by torch.cuda.synchronize().  Inputs are resident in
+HBM and rotate over enough copies (> 1 GiB) that the 256 MB Infinity Cache
+cannot hold them; each step replays a HIP graph of the four launches.
+
+`roofline` is for the dominant kernel (the gate/up GEMV): its algorithmic
+bytes per launch over its average duration, timed with HIP events on the
+launch stream; `cpu_baseline` times the CPU oracle's scalar GEMV on the same
+inputs on one host thread.  `fp8_quant` reports the per-token quantizer on
+BASELINE cfg1 (X fp32 [4096, 4096]).
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "kernel-craft_amd" / "python", ROOT / "oracle"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "INT4 GEMV HBM GB/s (% of peak) at M=1 8B shapes; FP8 quant GB/s"
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, AMD published
+GS = 128
+LLAMA = [("qkv", 6144, 4096), ("o_proj", 4096, 4096), ("gate_up", 28672, 4096),
+         ("down", 4096, 14336)]                        # (name, N, K)
+DOMINANT = 2                                           # gate/up
+ROTATE_BYTES = 1 << 30
+
+
+def gemv_bytes(n: int, k: int, gs: int = GS, xb: int = 2, yb: int = 2) -> int:
+    g = k // gs
+    return n * k // 2 + n * g * 4 + n * g // 2 + k * xb + n * yb
+
+
+def fp8_bytes(rows: int, cols: int) -> int:
+    return rows * cols * 4 + rows * cols + rows * 4
+
+
+def log(*a) -> None:
+    print(*a, file=sys.stderr, flush=True)
+
+
+def enqueue_backlog(torch, filler, ms: float = 20.0) -> None:
+    """Queue ~`ms` of GPU work so the launches that follow are issued ahead of
+    the GPU and run back to back (events then time kernels, not the host)."""
+    for _ in range(max(1, int(ms / 0.25))):
+        filler.fill_(1)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="bound on the CPU-baseline sample (0 skips it)")
+    ap.add_argument("--no-graph", action="store_true", help="eager launches instead of HIP graphs")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build runs on one GPU only (the quantized GEMV/FP8 path has no "
+              "multi-GPU code); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    import kernel_craft_torch_ops as ops
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    lib = ops._get_lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"# {lib.kc_version().decode()} on {torch.cuda.get_device_name(dev)}")
+
+    # ---- inputs (BASELINE cfg2 distributions), rotated over > 1 GiB --------
+    layer_bytes = sum(gemv_bytes(n, k) for _, n, k in LLAMA)
+    w_bytes = sum(n * k // 2 + n * (k // GS) * 4 + n * (k // GS) // 2 for _, n, k in LLAMA)
+    copies = max(2, math.ceil(ROTATE_BYTES / w_bytes))
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2024)
+    layers = []
+    for _ in range(copies):
+        layer = []
+        for _, n, k in LLAMA:
+            g = k // GS
+            packed = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=dev, generator=gen)
+            scales = torch.empty(n, g, device=dev).uniform_(0.005, 0.02, generator=gen)
+            zeros = torch.randint(0, 256, (n, g // 2), dtype=torch.uint8, device=dev, generator=gen)
+            layer.append((packed, scales, zeros))
+        layers.append(layer)
+    xs = [torch.randn(k, device=dev, generator=gen).to(torch.bfloat16) for _, _, k in LLAMA]
+    ys = [torch.empty(n, dtype=torch.bfloat16, device=dev) for _, n, _ in LLAMA]
+    fn = lib.kc_gemv_int4_bf16
+
+    def launch(r: int, i: int) -> None:
+        _, n, k = LLAMA[i]
+        p, s, z = layers[r][i]
+        st = fn(p.data_ptr(), s.data_ptr(), z.data_ptr(), xs[i].data_ptr(), ys[i].data_ptr(),
+                n, k, GS, torch.cuda.current_stream().cuda_stream)
+        if st:
+            raise RuntimeError(f"kc_gemv_int4_bf16 failed: {lib.kc_last_error_string().decode()}")
+
+    # ---- parity guard: every shape against an fp32 reference --------------
+    for i, (name, n, k) in enumerate(LLAMA):
+        launch(0, i)
+        p, s, z = layers[0][i]
+        W = torch.empty(n, k, dtype=torch.float32, device=dev)
+        lib.launch_dequantize_int4(p.data_ptr(), s.data_ptr(), z.data_ptr(), W.data_ptr(),
+                                   n, k, GS, torch.cuda.current_stream().cuda_stream)
+        ref = W @ xs[i].float()
+        err = (ys[i].float() - ref).norm() / ref.norm()
+        del W
+        if not err < 1e-2:
+            print(f"bench.py: parity guard failed for {name}: rel L2 {err:.3e}", file=sys.stderr)
+            return 1
+        log(f"# parity {name}: rel L2 {err:.2e}")
+
+    # ---- one HIP graph per rotation copy (the four launches of a layer) ----
+    graphs = None
+    if not args.no_graph:
+        try:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            graphs = []
+            with torch.cuda.stream(side):
+                for r in range(copies):
+                    gph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(gph, stream=side):
+                        for i in range(len(LLAMA)):
+                            launch(r, i)
+                    graphs.append(gph)
+            torch.cuda.current_stream().wait_stream(side)
+        except Exception as e:  # pragma: no cover - depends on the runtime
+            log(f"# graph capture unavailable ({e}); eager launches")
+            graphs = None
+
+    def step(j: int) -> None:
+        r = j % copies
+        if graphs is not None:
+            graphs[r].replay()
+        else:
+            for i in range(len(LLAMA)):
+                launch(r, i)
+
+    torch.cuda.synchronize()
+    for j in range(args.warmup):
+        step(j)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for j in range(args.steps):
+        step(args.warmup + j)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    value = layer_bytes * args.steps / elapsed / 1e9
+    log(f"# timed {args.steps} steps in {elapsed * 1e3:.3f} ms -> {value:.1f} GB/s "
+        f"({'graph' if graphs is not None else 'eager'})")
+
+    # ---- per-kernel durations with HIP events (launch stream, backlogged) ---
+    filler = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    reps = 100
+    kernel_us = {}
+    for i, (name, n, k) in enumerate(LLAMA):
+        enqueue_backlog(torch, filler)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for j in range(reps):
+            launch(j % copies, i)
+        e1.record()
+        torch.cuda.synchronize()
+        kernel_us[name] = e0.elapsed_time(e1) * 1e3 / reps
+        log(f"# {name:8s} N={n:6d} K={k:6d}: {kernel_us[name]:7.2f} us/launch, "
+            f"{gemv_bytes(n, k) / kernel_us[name] / 1e3:7.1f} GB/s")
+    dom_name, dom_n, dom_k = LLAMA[DOMINANT]
+    dom_bytes = gemv_bytes(dom_n, dom_k)
+    achieved = dom_bytes / (kernel_us[dom_name] * 1e-6) / 1e9
+    traffic = None
+    tfile = ROOT / "profiles" / "gemv_int4_bf16_gate_up_traffic.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+        except Exception:
+            traffic = None
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
+                "kernel": f"gemv_int4_fast_kernel bf16 gate/up N={dom_n} K={dom_k}",
+                "bytes_per_launch": dom_bytes, "avg_us": round(kernel_us[dom_name], 3)}
+
+    # ---- FP8 E4M3 per-token quantizer (BASELINE cfg1) ----------------------
+    frows = fcols = 4096
+    fcopies = max(2, math.ceil(ROTATE_BYTES / (frows * fcols * 4)))
+    fx = [torch.randn(frows, fcols, device=dev, generator=gen) for _ in range(fcopies)]
+    fq = torch.empty(frows, fcols, dtype=torch.int8, device=dev)
+    fs = torch.empty(frows, dtype=torch.float32, device=dev)
+    qfn = lib.kc_quantize_fp8_per_token_f32
+    for j in range(3):
+        qfn(fx[j % fcopies].data_ptr(), fq.data_ptr(), fs.data_ptr(), frows, fcols,
+            torch.cuda.current_stream().cuda_stream)
+    enqueue_backlog(torch, filler)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for j in range(reps):
+        qfn(fx[j % fcopies].data_ptr(), fq.data_ptr(), fs.data_ptr(), frows, fcols,
+            torch.cuda.current_stream().cuda_stream)
+    e1.record()
+    torch.cuda.synchronize()
+    fp8_us = e0.elapsed_time(e1) * 1e3 / reps
+    fp8_gbs = fp8_bytes(frows, fcols) / (fp8_us * 1e-6) / 1e9
+    log(f"# fp8 per-token [{frows}x{fcols}] fp32: {fp8_us:.2f} us, {fp8_gbs:.1f} GB/s")
+    del fx, filler
+
+    # ---- CPU baseline: the oracle's scalar GEMV, one host thread ----------
+    cpu = None
+    if args.cpu_seconds > 0:
+        import kc_oracle
+        host = []
+        for i, (_, n, k) in enumerate(LLAMA):
+            p, s, z = layers[0][i]
+            host.append((p.cpu().numpy(), s.cpu().numpy(), z.cpu().numpy(),
+                         xs[i].view(torch.int16).cpu().numpy().view(np.uint16), n, k))
+        kc_oracle.gemv_int4_bf16_f32(*host[1][:4], host[1][4], host[1][5], GS)   # warm
+        nlayers = 0
+        t0 = time.perf_counter()
+        while True:
+            for p, s, z, xb, n, k in host:
+                kc_oracle.gemv_int4_bf16_f32(p, s, z, xb, n, k, GS)
+            nlayers += 1
+            if time.perf_counter() - t0 >= args.cpu_seconds:
+                break
+        cpu_s = time.perf_counter() - t0
+        cpu = {"value": round(nlayers * layer_bytes / cpu_s / 1e9, 3), "unit": "GB/s",
+               "cores": 1, "kind": "port",
+               "sample": f"{nlayers} x one decode layer (the same 4 GEMVs, "
+                         f"{layer_bytes} B) in {cpu_s:.1f} s, oracle scalar C loop"}
+        log(f"# cpu baseline: {cpu['value']} GB/s ({nlayers} layers, {cpu_s:.1f} s)")
+
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / args.steps, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int4w-bf16a-f32acc",
+        "data": "synthetic",
+        "config": {"workload": "int4_gemv_llama3_8b_decode_layer",
+                   "shapes_NK": [[n, k] for _, n, k in LLAMA], "group_size": GS, "M": 1,
+                   "bytes_per_step": layer_bytes, "rotation_copies": copies,
+                   "launch": "hip_graph" if graphs is not None else "eager"},
+        "pct_of_peak": round(100.0 * value / PEAK_HBM_GBS, 2),
+        "roofline": roofline,
+        "kernel_us": {k: round(v, 3) for k, v in kernel_us.items()},
+        "fp8_quant": {"value": round(fp8_gbs, 1), "unit": "GB/s",
+                      "config": "per-token X fp32 [4096,4096]", "bytes_per_launch":
+                      fp8_bytes(frows, fcols), "avg_us": round(fp8_us, 3),
+                      "frac": round(fp8_gbs / PEAK_HBM_GBS, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

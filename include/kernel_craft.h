@@ -1,0 +1,222 @@
+/*
+ * kernel_craft.h -- C ABI of libkernels.so, the MI355X (gfx950) build of
+ * kernel-craft's quantized-inference path.
+ *
+ * Every pointer is a device pointer owned by the caller unless stated
+ * otherwise; the library allocates nothing.  `rows` is N (weight output
+ * features, or tokens), `cols` is K.  The stream argument is a hipStream_t
+ * (an opaque pointer, ABI-identical to the reference's cudaStream_t); 0 is
+ * the null stream.
+ *
+ * Part 1 keeps the reference launchers' names and signatures so that
+ * ctypes.CDLL / pybind11 callers of the reference load this library
+ * unchanged.  Like the reference they return void and synchronize their
+ * stream before returning.  Unlike the reference they validate their
+ * arguments: an invalid call launches nothing and records an error that
+ * kc_get_last_error() reports (part 2).
+ *
+ * Part 3 adds entry points that have no reference counterpart (bf16
+ * activations, the M>1 MFMA path, fused SmoothQuant, non-blocking variants).
+ * They are stream-ordered (they do not synchronize) and return a kc_status.
+ *
+ * Part 4 exports the reference's out-of-scope launchers as stubs so that the
+ * reference's loaders bind every symbol they expect; each stub prints
+ * "[kernel-craft-hip stub] <name> not implemented" to stderr and records
+ * KC_ERR_NOT_IMPLEMENTED.
+ */
+#ifndef KERNEL_CRAFT_H
+#define KERNEL_CRAFT_H
+
+#include <stdbool.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* kc_stream_t; /* == hipStream_t */
+
+/* ======================================================================
+ * Part 1 -- reference launchers (blocking; void)
+ * ==================================================================== */
+
+/* W[n,k] = (float)(sext4(nibble) - zero) * scale.
+ * packed [rows, cols/2] u8 (low nibble = even k), scales [rows, cols/gs]
+ * fp32, zeros [rows, (cols/gs)/2] u8 (even group -> low nibble, unsigned).
+ * Requires cols even and group_size dividing cols.
+ * Replaces quant_int4.cu:193-206. */
+void launch_dequantize_int4(const uint8_t* d_packed, const float* d_scales,
+                            const uint8_t* d_zeros, float* d_output, int rows,
+                            int cols, int group_size, kc_stream_t stream);
+
+/* y[n] = sum_k W[n,k] * x[k], dequantizing on the fly; fp32 x and y.
+ * Replaces quant_int4.cu:221-234. */
+void launch_gemv_int4(const uint8_t* d_packed, const float* d_scales,
+                      const uint8_t* d_zeros, const float* d_x, float* d_y,
+                      int rows, int cols, int group_size, kc_stream_t stream);
+
+/* FP8 E4M3 (OCP) quantization of fp32 [rows, cols]; codes are int8 bit
+ * patterns.  per_token: scales[r] = absmax_r/448 (1 for an all-zero row),
+ * written by the call.  Otherwise per-tensor: the call reads the scale from
+ * d_scales[0].  q = E4M3_rne(clamp(x / scale, +-448)).
+ * Replaces fp8_quant.cu:201-226. */
+void launch_quantize_fp8(const float* d_input, int8_t* d_output,
+                         float* d_scales, int rows, int cols, bool per_token,
+                         kc_stream_t stream);
+
+/* x = decode(code) * scale[row] (per_token) or * scale[0].
+ * Replaces fp8_quant.cu:239-253. */
+void launch_dequantize_fp8(const int8_t* d_input, const float* d_scales,
+                           float* d_output, int rows, int cols, bool per_token,
+                           kc_stream_t stream);
+
+/* out[r,c] = in[r,c] / smooth[c].  Replaces fp8_quant.cu:265-278. */
+void launch_smoothquant_scale(const float* d_input,
+                              const float* d_smooth_scales, float* d_output,
+                              int rows, int cols, kc_stream_t stream);
+
+/* ======================================================================
+ * Part 2 -- error channel (no reference counterpart: the reference's
+ * launchers report nothing, quant_int4.cu:205,233, fp8_quant.cu:225)
+ * ==================================================================== */
+
+typedef enum kc_status {
+    KC_SUCCESS = 0,
+    KC_ERR_INVALID_ARGUMENT = 1,
+    KC_ERR_NOT_IMPLEMENTED = 2,
+    KC_ERR_HIP = 3,
+    KC_ERR_UNSUPPORTED_DEVICE = 4
+} kc_status;
+
+/* Last error recorded on the calling thread; get_ clears it, peek_ keeps it. */
+int kc_get_last_error(void);
+int kc_peek_last_error(void);
+/* Message of the last error on the calling thread ("" when none). */
+const char* kc_last_error_string(void);
+/* Library version string. */
+const char* kc_version(void);
+
+/* ======================================================================
+ * Part 3 -- extensions (stream-ordered, return kc_status)
+ * ==================================================================== */
+
+/* Non-blocking launch_gemv_int4: identical arguments and results, no sync. */
+int kc_gemv_int4_f32_async(const uint8_t* d_packed, const float* d_scales,
+                           const uint8_t* d_zeros, const float* d_x, float* d_y,
+                           int rows, int cols, int group_size,
+                           kc_stream_t stream);
+
+/* INT4 GEMV with bf16 activation and bf16 output, fp32 accumulation
+ * (Llama-3-8B decode shapes).  x [cols] bf16, y [rows] bf16 (RNE). */
+int kc_gemv_int4_bf16(const uint8_t* d_packed, const float* d_scales,
+                      const uint8_t* d_zeros, const uint16_t* d_x,
+                      uint16_t* d_y, int rows, int cols, int group_size,
+                      kc_stream_t stream);
+
+/* Small-batch INT4 GEMM on MFMA: Y[m, n] = sum_k X[m,k] W[n,k].
+ * X [m, cols] bf16 row-major, Y [m, rows] bf16 row-major, 1 <= m <= 64. */
+int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
+                      const uint8_t* d_zeros, const uint16_t* d_x,
+                      uint16_t* d_y, int m, int rows, int cols, int group_size,
+                      kc_stream_t stream);
+
+/* Non-blocking FP8 quantizers (same arithmetic as launch_quantize_fp8). */
+int kc_quantize_fp8_per_token_f32(const float* d_input, int8_t* d_output,
+                                  float* d_scales, int64_t rows, int64_t cols,
+                                  kc_stream_t stream);
+int kc_quantize_fp8_per_tensor_f32(const float* d_input, int8_t* d_output,
+                                   const float* d_scale, int64_t rows,
+                                   int64_t cols, kc_stream_t stream);
+/* bf16 input, per row (per token for activations, per output channel for a
+ * weight matrix [N, K]). */
+int kc_quantize_fp8_per_token_bf16(const uint16_t* d_input, int8_t* d_output,
+                                   float* d_scales, int64_t rows, int64_t cols,
+                                   kc_stream_t stream);
+
+/* SmoothQuant (alpha = 0.5).  Column absmax of a [rows, cols] tensor;
+ * d_amax [cols] is overwritten (the call clears it first). */
+int kc_col_absmax_bf16(const uint16_t* d_input, float* d_amax, int64_t rows,
+                       int64_t cols, kc_stream_t stream);
+int kc_col_absmax_f32(const float* d_input, float* d_amax, int64_t rows,
+                      int64_t cols, kc_stream_t stream);
+/* s[c] = max(sqrt(amax_x[c]) / sqrt(max(amax_w[c], 1e-5)), 1e-5) */
+int kc_smooth_factors(const float* d_amax_x, const float* d_amax_w,
+                      float* d_smooth, int64_t cols, kc_stream_t stream);
+/* One pass: X / s, per-row absmax, scale, E4M3.  Bit-identical to
+ * launch_smoothquant_scale followed by launch_quantize_fp8(per_token). */
+int kc_quantize_fp8_smooth_div_f32(const float* d_input, const float* d_smooth,
+                                   int8_t* d_output, float* d_scales,
+                                   int64_t rows, int64_t cols,
+                                   kc_stream_t stream);
+int kc_quantize_fp8_smooth_div_bf16(const uint16_t* d_input,
+                                    const float* d_smooth, int8_t* d_output,
+                                    float* d_scales, int64_t rows,
+                                    int64_t cols, kc_stream_t stream);
+/* One pass: W * s (fp32 multiply), per-output-channel absmax, E4M3. */
+int kc_quantize_fp8_smooth_mul_bf16(const uint16_t* d_input,
+                                    const float* d_smooth, int8_t* d_output,
+                                    float* d_scales, int64_t rows,
+                                    int64_t cols, kc_stream_t stream);
+
+/* ======================================================================
+ * Part 4 -- out-of-scope reference symbols (stubs).  Signatures from the
+ * reference files cited; bound by kernel_craft_torch_ops.py:101-168 and
+ * pybind_transformer.cpp:36-122.
+ * ==================================================================== */
+
+/* flash_attention.cu:177-180 */
+void launch_flash_attention(const float* Q, const float* K, const float* V,
+                            float* O, int B, int H, int H_kv, int N, int d,
+                            bool causal, kc_stream_t stream);
+/* paged_attention.cu:135-142 */
+void launch_paged_attention(const float* Q, const int* block_table,
+                            const float* K_pool, const float* V_pool, float* O,
+                            const int* seq_lens, int B, int H, int H_kv, int d,
+                            int block_size, int max_blocks, kc_stream_t stream);
+/* speculative_decoding.cu:176-186 */
+void launch_verify_draft_tokens(const float* d_draft_probs,
+                                const float* d_target_probs,
+                                const int* d_draft_tokens,
+                                const float* d_rand_vals,
+                                const float* d_rand_vals2, int* d_accepted,
+                                int* d_corrected, int num_tokens,
+                                int vocab_size, kc_stream_t stream);
+/* speculative_decoding.cu:205-209 */
+void launch_compute_prefix_length(const int* d_accepted, int* d_prefix_len,
+                                  int num_tokens, kc_stream_t stream);
+/* tensor_parallel.cu:93-97, :258-263, :209-211, :235-237 */
+void launch_ring_allreduce(float** d_bufs, int count, int num_ranks,
+                           kc_stream_t stream);
+void launch_allgather(float** d_chunks, float* d_output, int chunk_size,
+                      int num_ranks, kc_stream_t stream);
+void launch_col_parallel_linear(const float* d_x, const float* d_W, float* d_y,
+                                int M, int N_rank, int K, kc_stream_t stream);
+void launch_row_parallel_linear(const float* d_x_rank, const float* d_W,
+                                float* d_out, int M, int N, int K_rank,
+                                kc_stream_t stream);
+/* selective_scan.cu:104-109, depthwise_conv1d.cu:84-87, rmsnorm.cu:83-85 */
+void launch_selective_scan(const float* d_u, const float* d_A_log,
+                           const float* d_B, const float* d_C,
+                           const float* d_delta, float* d_y, int B_, int L,
+                           int D, int N_state, kc_stream_t stream);
+void launch_depthwise_conv1d(const float* d_x, const float* d_w,
+                             const float* d_bias, float* d_y, int B_, int D,
+                             int L, int d_conv, kc_stream_t stream);
+void launch_rmsnorm(const float* d_x, const float* d_g, float* d_y, int rows,
+                    int D, float eps, kc_stream_t stream);
+/* tensor_parallel_nccl.cu:171-198 (the reference's own no-NCCL stubs) */
+void nccl_comm_init_all(void** comms, int num_comms, const int* devs);
+void nccl_comm_destroy(void* comm);
+void nccl_group_start(void);
+void nccl_group_end(void);
+void launch_ring_allreduce_nccl(void* comm, float* d_buf, int count,
+                                kc_stream_t stream);
+void launch_allgather_nccl(void* comm, const float* d_sendbuf,
+                           float* d_recvbuf, int sendcount, kc_stream_t stream);
+int nccl_comm_count(void* comm);     /* returns 0 */
+int nccl_comm_user_rank(void* comm); /* returns -1 */
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KERNEL_CRAFT_H */

@@ -1,0 +1,571 @@
+// fp8_quant.hip -- FP8 E4M3 (OCP) quantization for gfx950 (MI355X).
+//
+// Arithmetic (fp8_quant.cu:62-75, 89-131, 145-160, 174-184), reproduced
+// bit for bit:
+//   absmax_r = max over the row of |x| (fmaxf from 0: NaN never wins)
+//   scale_r  = absmax_r > 0 ? absmax_r / 448 : 1        (IEEE divide)
+//   code     = E4M3_rne(fmaxf(-448, fminf(448, x / scale_r)))
+// The divide is the compiler's correctly rounded fp32 division (HIP's default;
+// this library is never built with fast-math or denormal flushing), and the
+// clamp maps NaN to +448 exactly as CUDA's fmaxf/fminf do.  E4M3 encoding is
+// gfx950's v_cvt_pk_fp8_f32, which produces OCP E4M3 with round-to-nearest-
+// even; after the clamp every input is finite and within +-448.
+//
+// Per-token kernels read a row once: each thread keeps its slice of the row in
+// registers across the absmax reduction, then converts and stores it.
+#include <algorithm>
+
+#include "kc_common.hpp"
+
+namespace {
+
+using kc::kWave;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads = 256;
+constexpr float kE4M3Max = 448.0f;  // fp8_quant.cu:31
+
+__device__ __forceinline__ float clamp448(float v) { return fmaxf(-kE4M3Max, fminf(kE4M3Max, v)); }
+
+// 4 fp32 -> 4 E4M3 codes, byte i of the result holds input i.
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+    int v = __builtin_amdgcn_cvt_pk_fp8_f32(clamp448(a), clamp448(b), 0, false);
+    v = __builtin_amdgcn_cvt_pk_fp8_f32(clamp448(c), clamp448(d), v, true);
+    return static_cast<uint32_t>(v);
+}
+
+__device__ __forceinline__ uint8_t e4m3x1(float a) {
+    return static_cast<uint8_t>(__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(a), 0.0f, 0, false) & 0xFF);
+}
+
+__device__ __forceinline__ float row_scale(float amax) {
+    return amax > 0.0f ? amax / kE4M3Max : 1.0f;  // fp8_quant.cu:121
+}
+
+__device__ __forceinline__ float absmax4(float m, f32x4 v) {
+    return fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+}
+
+// Block-wide max for 256 threads; every thread gets the result.
+__device__ __forceinline__ float block_max(float m, float* red) {
+    m = kc::wave_max(m);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & (kWave - 1)) == 0) red[wave] = m;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__device__ __forceinline__ f32x4 bf16x4_to_f32(uint32_t a, uint32_t b) {
+    return f32x4{__uint_as_float(a << 16), __uint_as_float(a & 0xFFFF0000u),
+                 __uint_as_float(b << 16), __uint_as_float(b & 0xFFFF0000u)};
+}
+
+// Elementwise pre-transform applied before the absmax (SmoothQuant).
+enum class Smooth { kNone, kDiv, kMul };
+
+template <Smooth S>
+__device__ __forceinline__ f32x4 apply_smooth(f32x4 v, const float* __restrict__ s, int64_t col) {
+    if constexpr (S == Smooth::kNone) {
+        return v;
+    } else {
+        const f32x4 f = *reinterpret_cast<const f32x4*>(s + col);
+        if constexpr (S == Smooth::kDiv)
+            return f32x4{v.x / f.x, v.y / f.y, v.z / f.z, v.w / f.w};  // fp8_quant.cu:183
+        else
+            return f32x4{v.x * f.x, v.y * f.y, v.z * f.z, v.w * f.w};
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Per-row quantizer, fast path.  One 256-thread workgroup per row; thread t
+// holds float4 slots t, t+256, ... (NV of them) of the row in registers.
+// Requires cols % 4 == 0 (fp32) / cols % 8 == 0 (bf16), 16-byte aligned rows
+// and cols <= 1024*NV (fp32) / 2048*NV (bf16).
+// ---------------------------------------------------------------------------
+template <int NV, Smooth S>
+__global__ __launch_bounds__(kThreads) void quant_rows_f32_kernel(
+    const float* __restrict__ in, const float* __restrict__ smooth, int8_t* __restrict__ out,
+    float* __restrict__ scales, int64_t cols) {
+    __shared__ float red[kThreads / kWave];
+    const int64_t row = blockIdx.x;
+    const f32x4* src = reinterpret_cast<const f32x4*>(in + row * cols);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(out + row * cols);
+    const int n4 = static_cast<int>(cols >> 2);
+    f32x4 v[NV];
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        if (i < n4) {
+            v[j] = apply_smooth<S>(__builtin_nontemporal_load(src + i), smooth, 4 * int64_t{i});
+            m = absmax4(m, v[j]);
+        }
+    }
+    const float scale = row_scale(block_max(m, red));
+    if (threadIdx.x == 0) scales[row] = scale;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        if (i < n4) {
+            const f32x4 q = v[j];
+            __builtin_nontemporal_store(e4m3x4(q.x / scale, q.y / scale, q.z / scale, q.w / scale),
+                                        dst + i);
+        }
+    }
+}
+
+template <int NV, Smooth S>
+__global__ __launch_bounds__(kThreads) void quant_rows_bf16_kernel(
+    const uint16_t* __restrict__ in, const float* __restrict__ smooth, int8_t* __restrict__ out,
+    float* __restrict__ scales, int64_t cols) {
+    __shared__ float red[kThreads / kWave];
+    const int64_t row = blockIdx.x;
+    const u32x4* src = reinterpret_cast<const u32x4*>(in + row * cols);  // 8 bf16 per u32x4
+    u32x2* dst = reinterpret_cast<u32x2*>(out + row * cols);
+    const int n8 = static_cast<int>(cols >> 3);
+    f32x4 lo[NV], hi[NV];
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        if (i < n8) {
+            const u32x4 d = __builtin_nontemporal_load(src + i);
+            lo[j] = apply_smooth<S>(bf16x4_to_f32(d.x, d.y), smooth, 8 * int64_t{i});
+            hi[j] = apply_smooth<S>(bf16x4_to_f32(d.z, d.w), smooth, 8 * int64_t{i} + 4);
+            m = absmax4(absmax4(m, lo[j]), hi[j]);
+        }
+    }
+    const float scale = row_scale(block_max(m, red));
+    if (threadIdx.x == 0) scales[row] = scale;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        if (i < n8) {
+            const f32x4 a = lo[j], b = hi[j];
+            u32x2 o;
+            o.x = e4m3x4(a.x / scale, a.y / scale, a.z / scale, a.w / scale);
+            o.y = e4m3x4(b.x / scale, b.y / scale, b.z / scale, b.w / scale);
+            __builtin_nontemporal_store(o, dst + i);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Per-row quantizer, generic path: any cols >= 1, any alignment.  Two passes
+// over the row (absmax, then quantize), scalar accesses.
+// ---------------------------------------------------------------------------
+template <bool BF16, Smooth S>
+__device__ __forceinline__ float load_elem(const void* in, const float* smooth, int64_t row,
+                                           int64_t cols, int64_t c) {
+    float v;
+    if constexpr (BF16) v = kc::bf16_to_f32(static_cast<const uint16_t*>(in)[row * cols + c]);
+    else v = static_cast<const float*>(in)[row * cols + c];
+    if constexpr (S == Smooth::kDiv) v = v / smooth[c];
+    if constexpr (S == Smooth::kMul) v = v * smooth[c];
+    return v;
+}
+
+template <bool BF16, Smooth S>
+__global__ __launch_bounds__(kThreads) void quant_rows_generic_kernel(
+    const void* __restrict__ in, const float* __restrict__ smooth, int8_t* __restrict__ out,
+    float* __restrict__ scales, int64_t cols) {
+    __shared__ float red[kThreads / kWave];
+    const int64_t row = blockIdx.x;
+    float m = 0.0f;
+    for (int64_t c = threadIdx.x; c < cols; c += kThreads)
+        m = fmaxf(m, fabsf(load_elem<BF16, S>(in, smooth, row, cols, c)));
+    const float scale = row_scale(block_max(m, red));
+    if (threadIdx.x == 0) scales[row] = scale;
+    for (int64_t c = threadIdx.x; c < cols; c += kThreads)
+        out[row * cols + c] =
+            static_cast<int8_t>(e4m3x1(load_elem<BF16, S>(in, smooth, row, cols, c) / scale));
+}
+
+// ---------------------------------------------------------------------------
+// Per-tensor quantizer (fp8_quant.cu:62-75).  The scale is read on the device
+// from d_scale[0]; the reference copies the same word to the host first
+// (fp8_quant.cu:215-219) and passes it by value.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void quant_tensor_f32_kernel(
+    const float* __restrict__ in, const float* __restrict__ d_scale, int8_t* __restrict__ out,
+    int64_t count, bool vec) {
+    const float scale = *d_scale;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    const int64_t tid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    int64_t done = 0;
+    if (vec) {
+        const int64_t n4 = count >> 2;
+        const f32x4* src = reinterpret_cast<const f32x4*>(in);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(out);
+        for (int64_t i = tid; i < n4; i += stride) {
+            const f32x4 q = __builtin_nontemporal_load(src + i);
+            __builtin_nontemporal_store(e4m3x4(q.x / scale, q.y / scale, q.z / scale, q.w / scale),
+                                        dst + i);
+        }
+        done = n4 << 2;
+    }
+    for (int64_t i = done + tid; i < count; i += stride)
+        out[i] = static_cast<int8_t>(e4m3x1(in[i] / scale));
+}
+
+// ---------------------------------------------------------------------------
+// Dequantization (fp8_quant.cu:145-160): exact E4M3 decode
+// (v_cvt_pk_f32_fp8), times the row's (or the tensor's) scale.
+// Grid: one block per (row, 1024-column tile); the row index is uniform.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void dequant_fp8_kernel(
+    const int8_t* __restrict__ in, const float* __restrict__ scales, float* __restrict__ out,
+    int64_t cols, int64_t tiles_per_row, bool per_token, bool vec) {
+    const int64_t row = blockIdx.x / tiles_per_row;
+    const int64_t tile = blockIdx.x - row * tiles_per_row;
+    const float s = per_token ? scales[row] : scales[0];
+    const int64_t c = tile * 1024 + 4 * static_cast<int64_t>(threadIdx.x);
+    const int8_t* src = in + row * cols;
+    float* dst = out + row * cols;
+    if (vec && c + 4 <= cols) {
+        const uint32_t q = *reinterpret_cast<const uint32_t*>(src + c);
+        const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(q), false);
+        const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(q), true);
+        __builtin_nontemporal_store(f32x4{a.x * s, a.y * s, b.x * s, b.y * s},
+                                    reinterpret_cast<f32x4*>(dst + c));
+    } else {
+        for (int64_t k = c; k < std::min(c + 4, cols); ++k) {
+            const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(static_cast<uint8_t>(src[k])), false);
+            dst[k] = a.x * s;
+        }
+    }
+}
+
+// SmoothQuant divide (fp8_quant.cu:174-184): out = in / s[col].
+__global__ __launch_bounds__(kThreads) void smooth_div_kernel(
+    const float* __restrict__ in, const float* __restrict__ s, float* __restrict__ out,
+    int64_t cols, int64_t tiles_per_row, bool vec) {
+    const int64_t row = blockIdx.x / tiles_per_row;
+    const int64_t tile = blockIdx.x - row * tiles_per_row;
+    const int64_t c = tile * 1024 + 4 * static_cast<int64_t>(threadIdx.x);
+    const float* src = in + row * cols;
+    float* dst = out + row * cols;
+    if (vec && c + 4 <= cols) {
+        const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + c));
+        const f32x4 f = *reinterpret_cast<const f32x4*>(s + c);
+        __builtin_nontemporal_store(f32x4{v.x / f.x, v.y / f.y, v.z / f.z, v.w / f.w},
+                                    reinterpret_cast<f32x4*>(dst + c));
+    } else {
+        for (int64_t k = c; k < std::min(c + 4, cols); ++k) dst[k] = src[k] / s[k];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// SmoothQuant statistics: column absmax.  Each block reduces a 64-row band of
+// 1024 columns in registers and folds it into d_amax with an integer atomic
+// max (non-negative fp32 values order like their bit patterns; fmaxf from 0
+// keeps NaN out).  d_amax is cleared by a fill kernel first.
+// ---------------------------------------------------------------------------
+constexpr int kAbsmaxRowsPerBlock = 64;
+
+__global__ __launch_bounds__(kThreads) void fill_zero_kernel(float* __restrict__ p, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kThreads)
+        p[i] = 0.0f;
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(kThreads) void col_absmax_kernel(const void* __restrict__ in,
+                                                              float* __restrict__ amax,
+                                                              int64_t rows, int64_t cols,
+                                                              int64_t tiles_per_row, bool vec) {
+    const int64_t band = blockIdx.x / tiles_per_row;
+    const int64_t tile = blockIdx.x - band * tiles_per_row;
+    const int64_t c = tile * 1024 + 4 * static_cast<int64_t>(threadIdx.x);
+    const int64_t r0 = band * kAbsmaxRowsPerBlock;
+    const int64_t r1 = std::min(r0 + kAbsmaxRowsPerBlock, rows);
+    float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f;
+    if (vec && c + 4 <= cols) {
+        for (int64_t r = r0; r < r1; ++r) {
+            f32x4 v;
+            if constexpr (BF16) {
+                const u32x2 d = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(in) + r * cols + c));
+                v = bf16x4_to_f32(d.x, d.y);
+            } else {
+                v = __builtin_nontemporal_load(
+                    reinterpret_cast<const f32x4*>(static_cast<const float*>(in) + r * cols + c));
+            }
+            m0 = fmaxf(m0, fabsf(v.x));
+            m1 = fmaxf(m1, fabsf(v.y));
+            m2 = fmaxf(m2, fabsf(v.z));
+            m3 = fmaxf(m3, fabsf(v.w));
+        }
+        atomicMax(reinterpret_cast<unsigned int*>(amax) + c, __float_as_uint(m0));
+        atomicMax(reinterpret_cast<unsigned int*>(amax) + c + 1, __float_as_uint(m1));
+        atomicMax(reinterpret_cast<unsigned int*>(amax) + c + 2, __float_as_uint(m2));
+        atomicMax(reinterpret_cast<unsigned int*>(amax) + c + 3, __float_as_uint(m3));
+    } else {
+        for (int64_t k = c; k < std::min(c + 4, cols); ++k) {
+            float m = 0.f;
+            for (int64_t r = r0; r < r1; ++r) {
+                float v;
+                if constexpr (BF16) v = kc::bf16_to_f32(static_cast<const uint16_t*>(in)[r * cols + k]);
+                else v = static_cast<const float*>(in)[r * cols + k];
+                m = fmaxf(m, fabsf(v));
+            }
+            atomicMax(reinterpret_cast<unsigned int*>(amax) + k, __float_as_uint(m));
+        }
+    }
+}
+
+// s = max(sqrt(ax) / sqrt(max(aw, 1e-5)), 1e-5); sqrtf and / correctly rounded.
+__global__ __launch_bounds__(kThreads) void smooth_factor_kernel(const float* __restrict__ ax,
+                                                                 const float* __restrict__ aw,
+                                                                 float* __restrict__ s,
+                                                                 int64_t cols) {
+    for (int64_t c = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; c < cols;
+         c += static_cast<int64_t>(gridDim.x) * kThreads)
+        s[c] = fmaxf(sqrtf(ax[c]) / sqrtf(fmaxf(aw[c], 1e-5f)), 1e-5f);
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+int check_rows(const char* fn, const void* in, const void* out, const void* scales, int64_t rows,
+               int64_t cols) {
+    if (rows < 0 || cols < 0)
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: negative shape rows=%lld cols=%lld",
+                             fn, (long long)rows, (long long)cols);
+    if (rows > INT32_MAX)
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: rows=%lld exceeds 2^31-1", fn,
+                             (long long)rows);
+    if (rows > 0 && cols > 0 && (!scales || !in || !out))
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: null device pointer", fn);
+    return KC_SUCCESS;
+}
+
+template <Smooth S>
+int quant_rows_f32(const char* fn, const float* in, const float* smooth, int8_t* out,
+                   float* scales, int64_t rows, int64_t cols, hipStream_t stream) {
+    int st = check_rows(fn, in, out, scales, rows, cols);
+    if (st != KC_SUCCESS) return st;
+    if (S != Smooth::kNone && rows > 0 && cols > 0 && !smooth)
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: null smoothing vector", fn);
+    if (rows == 0 || cols == 0) return KC_SUCCESS;
+    const unsigned grid = static_cast<unsigned>(rows);
+    const bool vec = cols > 0 && cols % 4 == 0 && kc::aligned(in, 16) && kc::aligned(out, 4) &&
+                     (S == Smooth::kNone || kc::aligned(smooth, 16));
+    const int64_t nv = (cols + 1023) / 1024;
+    if (vec && nv <= 1)
+        quant_rows_f32_kernel<1, S><<<grid, kThreads, 0, stream>>>(in, smooth, out, scales, cols);
+    else if (vec && nv <= 2)
+        quant_rows_f32_kernel<2, S><<<grid, kThreads, 0, stream>>>(in, smooth, out, scales, cols);
+    else if (vec && nv <= 4)
+        quant_rows_f32_kernel<4, S><<<grid, kThreads, 0, stream>>>(in, smooth, out, scales, cols);
+    else if (vec && nv <= 8)
+        quant_rows_f32_kernel<8, S><<<grid, kThreads, 0, stream>>>(in, smooth, out, scales, cols);
+    else
+        quant_rows_generic_kernel<false, S><<<grid, kThreads, 0, stream>>>(in, smooth, out, scales,
+                                                                           cols);
+    return kc::check_launch(fn);
+}
+
+template <Smooth S>
+int quant_rows_bf16(const char* fn, const uint16_t* in, const float* smooth, int8_t* out,
+                    float* scales, int64_t rows, int64_t cols, hipStream_t stream) {
+    int st = check_rows(fn, in, out, scales, rows, cols);
+    if (st != KC_SUCCESS) return st;
+    if (S != Smooth::kNone && rows > 0 && cols > 0 && !smooth)
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: null smoothing vector", fn);
+    if (rows == 0 || cols == 0) return KC_SUCCESS;
+    const unsigned grid = static_cast<unsigned>(rows);
+    const bool vec = cols > 0 && cols % 8 == 0 && kc::aligned(in, 16) && kc::aligned(out, 8) &&
+                     (S == Smooth::kNone || kc::aligned(smooth, 16));
+    const int64_t nv = (cols + 2047) / 2048;
+    if (vec && nv <= 1)
+        quant_rows_bf16_kernel<1, S><<<grid, kThreads, 0, stream>>>(in, smooth, out, scales, cols);
+    else if (vec && nv <= 2)
+        quant_rows_bf16_kernel<2, S><<<grid, kThreads, 0, stream>>>(in, smooth, out, scales, cols);
+    else if (vec && nv <= 4)
+        quant_rows_bf16_kernel<4, S><<<grid, kThreads, 0, stream>>>(in, smooth, out, scales, cols);
+    else if (vec && nv <= 8)
+        quant_rows_bf16_kernel<8, S><<<grid, kThreads, 0, stream>>>(in, smooth, out, scales, cols);
+    else
+        quant_rows_generic_kernel<true, S><<<grid, kThreads, 0, stream>>>(in, smooth, out, scales,
+                                                                          cols);
+    return kc::check_launch(fn);
+}
+
+int quant_tensor_f32(const char* fn, const float* in, int8_t* out, const float* d_scale,
+                     int64_t rows, int64_t cols, hipStream_t stream) {
+    int st = check_rows(fn, in, out, d_scale, rows, cols);
+    if (st != KC_SUCCESS) return st;
+    const int64_t count = rows * cols;
+    if (count == 0) return KC_SUCCESS;
+    const bool vec = kc::aligned(in, 16) && kc::aligned(out, 4);
+    const int64_t work = vec ? (count + 3) / 4 : count;
+    const int64_t blocks = std::min<int64_t>((work + kThreads - 1) / kThreads, 256 * 32);
+    quant_tensor_f32_kernel<<<static_cast<unsigned>(blocks), kThreads, 0, stream>>>(
+        in, d_scale, out, count, vec);
+    return kc::check_launch(fn);
+}
+
+int row_tiles(const char* fn, int64_t rows, int64_t cols, int64_t* tiles, unsigned* grid) {
+    *tiles = (cols + 1023) / 1024;
+    const int64_t g = rows * *tiles;
+    if (g > INT32_MAX)
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: tensor too large (rows=%lld cols=%lld)",
+                             fn, (long long)rows, (long long)cols);
+    *grid = static_cast<unsigned>(g);
+    return KC_SUCCESS;
+}
+
+int dequant_fp8(const char* fn, const int8_t* in, const float* scales, float* out, int64_t rows,
+                int64_t cols, bool per_token, hipStream_t stream) {
+    int st = check_rows(fn, in, out, scales, rows, cols);
+    if (st != KC_SUCCESS) return st;
+    if (rows == 0 || cols == 0) return KC_SUCCESS;
+    int64_t tiles;
+    unsigned grid;
+    if ((st = row_tiles(fn, rows, cols, &tiles, &grid)) != KC_SUCCESS) return st;
+    const bool vec = cols % 4 == 0 && kc::aligned(in, 4) && kc::aligned(out, 16);
+    dequant_fp8_kernel<<<grid, kThreads, 0, stream>>>(in, scales, out, cols, tiles, per_token, vec);
+    return kc::check_launch(fn);
+}
+
+int smooth_div(const char* fn, const float* in, const float* s, float* out, int64_t rows,
+               int64_t cols, hipStream_t stream) {
+    int st = check_rows(fn, in, out, s, rows, cols);
+    if (st != KC_SUCCESS) return st;
+    if (rows == 0 || cols == 0) return KC_SUCCESS;
+    int64_t tiles;
+    unsigned grid;
+    if ((st = row_tiles(fn, rows, cols, &tiles, &grid)) != KC_SUCCESS) return st;
+    const bool vec = cols % 4 == 0 && kc::aligned(in, 16) && kc::aligned(out, 16) &&
+                     kc::aligned(s, 16);
+    smooth_div_kernel<<<grid, kThreads, 0, stream>>>(in, s, out, cols, tiles, vec);
+    return kc::check_launch(fn);
+}
+
+template <bool BF16>
+int col_absmax(const char* fn, const void* in, float* amax, int64_t rows, int64_t cols,
+               hipStream_t stream) {
+    int st = check_rows(fn, in, amax, amax, rows, cols);
+    if (st != KC_SUCCESS) return st;
+    if (cols == 0) return KC_SUCCESS;
+    if (!amax) return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: null device pointer", fn);
+    const int64_t fill_blocks = std::min<int64_t>((cols + kThreads - 1) / kThreads, 1024);
+    fill_zero_kernel<<<static_cast<unsigned>(fill_blocks), kThreads, 0, stream>>>(amax, cols);
+    if ((st = kc::check_launch(fn)) != KC_SUCCESS) return st;
+    if (rows == 0) return KC_SUCCESS;
+    const int64_t tiles = (cols + 1023) / 1024;
+    const int64_t bands = (rows + kAbsmaxRowsPerBlock - 1) / kAbsmaxRowsPerBlock;
+    if (bands * tiles > INT32_MAX)
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: tensor too large", fn);
+    const bool vec = cols % 4 == 0 && (BF16 ? kc::aligned(in, 8) : kc::aligned(in, 16));
+    col_absmax_kernel<BF16><<<static_cast<unsigned>(bands * tiles), kThreads, 0, stream>>>(
+        in, amax, rows, cols, tiles, vec);
+    return kc::check_launch(fn);
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI -- reference launchers (blocking)
+// ===========================================================================
+
+extern "C" void launch_quantize_fp8(const float* d_input, int8_t* d_output, float* d_scales,
+                                    int rows, int cols, bool per_token, kc_stream_t stream) {
+    const char* fn = "launch_quantize_fp8";
+    const int st = per_token ? quant_rows_f32<Smooth::kNone>(fn, d_input, nullptr, d_output,
+                                                             d_scales, rows, cols, stream)
+                             : quant_tensor_f32(fn, d_input, d_output, d_scales, rows, cols, stream);
+    if (st == KC_SUCCESS) kc::sync_stream(stream, fn);
+}
+
+extern "C" void launch_dequantize_fp8(const int8_t* d_input, const float* d_scales,
+                                      float* d_output, int rows, int cols, bool per_token,
+                                      kc_stream_t stream) {
+    const char* fn = "launch_dequantize_fp8";
+    if (dequant_fp8(fn, d_input, d_scales, d_output, rows, cols, per_token, stream) == KC_SUCCESS)
+        kc::sync_stream(stream, fn);
+}
+
+extern "C" void launch_smoothquant_scale(const float* d_input, const float* d_smooth_scales,
+                                         float* d_output, int rows, int cols,
+                                         kc_stream_t stream) {
+    const char* fn = "launch_smoothquant_scale";
+    if (smooth_div(fn, d_input, d_smooth_scales, d_output, rows, cols, stream) == KC_SUCCESS)
+        kc::sync_stream(stream, fn);
+}
+
+// ===========================================================================
+// C ABI -- extensions (stream-ordered)
+// ===========================================================================
+
+extern "C" int kc_quantize_fp8_per_token_f32(const float* d_input, int8_t* d_output,
+                                             float* d_scales, int64_t rows, int64_t cols,
+                                             kc_stream_t stream) {
+    return quant_rows_f32<Smooth::kNone>("kc_quantize_fp8_per_token_f32", d_input, nullptr,
+                                         d_output, d_scales, rows, cols, stream);
+}
+
+extern "C" int kc_quantize_fp8_per_tensor_f32(const float* d_input, int8_t* d_output,
+                                              const float* d_scale, int64_t rows, int64_t cols,
+                                              kc_stream_t stream) {
+    return quant_tensor_f32("kc_quantize_fp8_per_tensor_f32", d_input, d_output, d_scale, rows,
+                            cols, stream);
+}
+
+extern "C" int kc_quantize_fp8_per_token_bf16(const uint16_t* d_input, int8_t* d_output,
+                                              float* d_scales, int64_t rows, int64_t cols,
+                                              kc_stream_t stream) {
+    return quant_rows_bf16<Smooth::kNone>("kc_quantize_fp8_per_token_bf16", d_input, nullptr,
+                                          d_output, d_scales, rows, cols, stream);
+}
+
+extern "C" int kc_col_absmax_bf16(const uint16_t* d_input, float* d_amax, int64_t rows,
+                                  int64_t cols, kc_stream_t stream) {
+    return col_absmax<true>("kc_col_absmax_bf16", d_input, d_amax, rows, cols, stream);
+}
+
+extern "C" int kc_col_absmax_f32(const float* d_input, float* d_amax, int64_t rows, int64_t cols,
+                                 kc_stream_t stream) {
+    return col_absmax<false>("kc_col_absmax_f32", d_input, d_amax, rows, cols, stream);
+}
+
+extern "C" int kc_smooth_factors(const float* d_amax_x, const float* d_amax_w, float* d_smooth,
+                                 int64_t cols, kc_stream_t stream) {
+    const char* fn = "kc_smooth_factors";
+    if (cols < 0)
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: negative cols", fn);
+    if (cols == 0) return KC_SUCCESS;
+    if (!d_amax_x || !d_amax_w || !d_smooth)
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: null device pointer", fn);
+    const int64_t blocks = std::min<int64_t>((cols + kThreads - 1) / kThreads, 1024);
+    smooth_factor_kernel<<<static_cast<unsigned>(blocks), kThreads, 0, stream>>>(d_amax_x, d_amax_w,
+                                                                                d_smooth, cols);
+    return kc::check_launch(fn);
+}
+
+extern "C" int kc_quantize_fp8_smooth_div_f32(const float* d_input, const float* d_smooth,
+                                              int8_t* d_output, float* d_scales, int64_t rows,
+                                              int64_t cols, kc_stream_t stream) {
+    return quant_rows_f32<Smooth::kDiv>("kc_quantize_fp8_smooth_div_f32", d_input, d_smooth,
+                                        d_output, d_scales, rows, cols, stream);
+}
+
+extern "C" int kc_quantize_fp8_smooth_div_bf16(const uint16_t* d_input, const float* d_smooth,
+                                               int8_t* d_output, float* d_scales, int64_t rows,
+                                               int64_t cols, kc_stream_t stream) {
+    return quant_rows_bf16<Smooth::kDiv>("kc_quantize_fp8_smooth_div_bf16", d_input, d_smooth,
+                                         d_output, d_scales, rows, cols, stream);
+}
+
+extern "C" int kc_quantize_fp8_smooth_mul_bf16(const uint16_t* d_input, const float* d_smooth,
+                                               int8_t* d_output, float* d_scales, int64_t rows,
+                                               int64_t cols, kc_stream_t stream) {
+    return quant_rows_bf16<Smooth::kMul>("kc_quantize_fp8_smooth_mul_bf16", d_input, d_smooth,
+                                         d_output, d_scales, rows, cols, stream);
+}

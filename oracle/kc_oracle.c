@@ -1,0 +1,366 @@
+/*
+ * kc_oracle.c -- CPU restatement of kernel-craft's quantized-inference path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP kernels, never the thing
+ * measured or shipped (bench.py's cpu_baseline leg times it as the CPU
+ * baseline).  Built with gcc -O2 -ffp-contract=off and no fast-math, so every
+ * fp32 operation below is one IEEE-754 operation with round-to-nearest-even,
+ * as nvcc's defaults give the reference (no --use_fast_math anywhere in the
+ * reference's CMakeLists.txt).
+ *
+ * Reference paths are relative to the kernel-craft repository root.
+ *
+ * How each function is pinned (see tests/test_oracle.py):
+ *   kco_sext4, kco_dequantize_int4   reference KATs tests/test_quant_int4.cpp:35-88
+ *                                    and :148-199, test_transformer_bindings.py:185-196
+ *                                    (golden fixtures), closed-form invariants.
+ *   kco_gemv_int4_*                  reference KATs test_quant_int4.cpp:90-146 and
+ *                                    test_triton_kernels.py:76-119 (golden fixtures),
+ *                                    numpy float64 matmul, linearity, brute force.
+ *   kco_e4m3_encode / _decode        torch.float8_e4m3fn over every fp32 in the
+ *                                    clamped domain and the full decode table, plus
+ *                                    OCP special cases.
+ *   kco_quantize_fp8_*               reference round-trip bounds
+ *                                    (test_fp8_quant.cpp:34-71,137-174), zero rows,
+ *                                    NaN/inf rows, numpy restatement of the scale.
+ *   kco_smoothquant_scale            KAT test_fp8_quant.cpp:99-135, numpy divide.
+ *   extensions                       composition identities with the pinned
+ *                                    functions above (fused == two-step).
+ */
+#include "kc_oracle.h"
+
+#include <math.h>
+#include <string.h>
+
+#define E4M3_MAX 448.0f /* fp8_quant.cu:31 */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* quant_int4.cu:34-48: bits 3:0 (or 7:4) sign-extended from 4 bits. */
+int kco_sext4(unsigned nibble) {
+    nibble &= 0xFu;
+    return (nibble & 0x8u) ? (int)nibble - 16 : (int)nibble;
+}
+
+/* OCP OFP8 v1.0 E4M3 ("FN"): bias 7, 3 mantissa bits, no infinities,
+ * S.1111.111 is NaN, max finite 448 (S.1111.110), min subnormal 2^-9.
+ * Round-to-nearest-even; magnitudes above 448 saturate to 448 (satfinite).
+ * This is the conversion fp8_quant.cu:73,128 requests from __nv_fp8_e4m3;
+ * it is written from the OCP specification, not from any CUDA header. */
+uint8_t kco_e4m3_encode(float f) {
+    uint32_t u = f2u(f);
+    uint8_t sign = (uint8_t)((u >> 24) & 0x80u);
+    uint32_t a = u & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return (uint8_t)(sign | 0x7Fu);       /* NaN */
+    if (a >= 0x43E00000u) return (uint8_t)(sign | 0x7Eu);      /* >= 448 */
+    int e = (int)(a >> 23) - 127;
+    if (e < -6) {
+        /* E4M3 subnormal range: result = RNE(|x| * 2^9) units of 2^-9 */
+        if ((a >> 23) == 0) return sign;                        /* fp32 denormal/0 */
+        uint32_t m = (a & 0x7FFFFFu) | 0x800000u;               /* |x| = m*2^(e-23) */
+        int shift = 14 - e;                                     /* >= 21 */
+        if (shift > 24) return sign;                            /* < 0.5 unit */
+        uint32_t half = 1u << (shift - 1);
+        uint32_t q = (m + half - 1u + ((m >> shift) & 1u)) >> shift;
+        return (uint8_t)(sign | q);            /* q == 8 encodes 2^-6 (E=1,M=0) */
+    }
+    uint32_t r = a + 0x7FFFFu + ((a >> 20) & 1u);               /* RNE at bit 20 */
+    int E = (int)(r >> 23) - 120;                               /* -127 + 7 */
+    uint32_t m3 = (r >> 20) & 7u;
+    if (E > 15 || (E == 15 && m3 == 7u)) return (uint8_t)(sign | 0x7Eu);
+    return (uint8_t)(sign | ((uint32_t)E << 3) | m3);
+}
+
+float kco_e4m3_decode(uint8_t c) {
+    int E = (c >> 3) & 0xF, M = c & 7;
+    float v;
+    if (E == 15 && M == 7) v = NAN;
+    else if (E == 0) v = ldexpf((float)M, -9);
+    else v = ldexpf(1.0f + (float)M / 8.0f, E - 7);
+    return (c & 0x80) ? -v : v;
+}
+
+float kco_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+uint16_t kco_f32_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+/* fp8_quant.cu:126-129: clamp to +-448 (fmaxf/fminf drop NaN in favour of the
+ * bound, so NaN becomes +448), then convert. */
+static inline uint8_t clamp_encode(float q) {
+    q = fmaxf(-E4M3_MAX, fminf(E4M3_MAX, q));
+    return kco_e4m3_encode(q);
+}
+
+uint64_t kco_e4m3_sweep_mismatches(uint32_t start, uint64_t count,
+                                   const uint8_t* codes, uint32_t* first_bad) {
+    uint64_t bad = 0;
+    uint32_t first = 0;
+    for (uint64_t i = 0; i < count; ++i) {
+        uint32_t bits = start + (uint32_t)i;
+        if (clamp_encode(u2f(bits)) != codes[i]) {
+            if (bad == 0) first = bits;
+            ++bad;
+        }
+    }
+    if (first_bad) *first_bad = first;
+    return bad;
+}
+
+/* ---- INT4 ------------------------------------------------------------- */
+
+/* Zero-point of group g of a row: byte zeros[row*(G/2) + g/2] (floor stride),
+ * even g -> low nibble, odd g -> high nibble, read unsigned 0..15
+ * (quant_int4.cu:93-96 and :152-156). */
+static inline int zero_point(const uint8_t* zeros, int64_t row, int64_t G,
+                             int64_t g) {
+    uint8_t zb = zeros[row * (G / 2) + g / 2];
+    return (g % 2 == 0) ? (zb & 0x0F) : (zb >> 4);
+}
+
+/* quant_int4.cu:68-105: W[n,k] = (float)(sext4(q) - z) * s, one fp32 rounding. */
+void kco_dequantize_int4(const uint8_t* packed, const float* scales,
+                         const uint8_t* zeros, float* out,
+                         int64_t rows, int64_t cols, int64_t gs) {
+    int64_t G = cols / gs;
+    for (int64_t r = 0; r < rows; ++r) {
+        for (int64_t b = 0; 2 * b < cols; ++b) {
+            int64_t c0 = 2 * b, c1 = c0 + 1;
+            uint8_t p = packed[r * (cols / 2) + b];
+            int64_t g0 = c0 / gs, g1 = c1 / gs;
+            float s0 = scales[r * G + g0], s1 = scales[r * G + g1];
+            int z0 = zero_point(zeros, r, G, g0), z1 = zero_point(zeros, r, G, g1);
+            out[r * cols + c0] = (float)(kco_sext4(p) - z0) * s0;
+            if (c1 < cols) out[r * cols + c1] = (float)(kco_sext4(p >> 4) - z1) * s1;
+        }
+    }
+}
+
+/* One dequantized weight exactly as quant_int4.cu:158-159 forms it. */
+static inline float wq(const uint8_t* packed, const float* scales,
+                       const uint8_t* zeros, int64_t r, int64_t k,
+                       int64_t cols, int64_t gs) {
+    int64_t G = cols / gs, g = k / gs;
+    uint8_t p = packed[r * (cols / 2) + k / 2];
+    int q = (k & 1) ? kco_sext4(p >> 4) : kco_sext4(p);
+    return (float)(q - zero_point(zeros, r, G, g)) * scales[r * G + g];
+}
+
+void kco_gemv_int4_f64(const uint8_t* packed, const float* scales,
+                       const uint8_t* zeros, const float* x, double* y,
+                       int64_t rows, int64_t cols, int64_t gs) {
+    for (int64_t r = 0; r < rows; ++r) {
+        double acc = 0.0;
+        for (int64_t k = 0; k < cols; ++k)
+            acc += (double)wq(packed, scales, zeros, r, k, cols, gs) * (double)x[k];
+        y[r] = acc;
+    }
+}
+
+/* quant_int4.cu:140-174 with nvcc's default FMA contraction of
+ * `partial += w * x` (fmaf), 256 strided partials, then the shared tree. */
+void kco_gemv_int4_refkernel_f32(const uint8_t* packed, const float* scales,
+                                 const uint8_t* zeros, const float* x, float* y,
+                                 int64_t rows, int64_t cols, int64_t gs) {
+    enum { BLOCK = 256 };
+    float part[BLOCK];
+    int64_t nbytes = cols / 2;
+    for (int64_t r = 0; r < rows; ++r) {
+        for (int t = 0; t < BLOCK; ++t) {
+            float acc = 0.0f;
+            for (int64_t b = t; b < nbytes; b += BLOCK) {
+                int64_t c0 = 2 * b;
+                float w0 = wq(packed, scales, zeros, r, c0, cols, gs);
+                acc = fmaf(w0, x[c0], acc);
+                if (c0 + 1 < cols) {
+                    float w1 = wq(packed, scales, zeros, r, c0 + 1, cols, gs);
+                    acc = fmaf(w1, x[c0 + 1], acc);
+                }
+            }
+            part[t] = acc;
+        }
+        for (int stride = BLOCK / 2; stride >= 1; stride >>= 1)
+            for (int t = 0; t < stride; ++t) part[t] += part[t + stride];
+        y[r] = part[0];
+    }
+}
+
+void kco_gemm_int4_bf16_f64(const uint8_t* packed, const float* scales,
+                            const uint8_t* zeros, const uint16_t* x, double* y,
+                            int64_t m, int64_t rows, int64_t cols, int64_t gs) {
+    for (int64_t r = 0; r < rows; ++r) {
+        for (int64_t i = 0; i < m; ++i) y[i * rows + r] = 0.0;
+        for (int64_t k = 0; k < cols; ++k) {
+            double w = (double)wq(packed, scales, zeros, r, k, cols, gs);
+            for (int64_t i = 0; i < m; ++i)
+                y[i * rows + r] += w * (double)kco_bf16_to_f32(x[i * cols + k]);
+        }
+    }
+}
+
+void kco_gemv_int4_bf16_f32(const uint8_t* packed, const float* scales,
+                            const uint8_t* zeros, const uint16_t* x, float* y,
+                            int64_t rows, int64_t cols, int64_t gs) {
+    int64_t G = cols / gs;
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint8_t* pr = packed + r * (cols / 2);
+        float acc = 0.0f;
+        for (int64_t k = 0; k < cols; k += 2) {
+            int64_t g = k / gs;
+            float s = scales[r * G + g];
+            int z = zero_point(zeros, r, G, g);
+            uint8_t p = pr[k / 2];
+            acc += (float)(kco_sext4(p) - z) * s * kco_bf16_to_f32(x[k]);
+            acc += (float)(kco_sext4(p >> 4) - z) * s * kco_bf16_to_f32(x[k + 1]);
+        }
+        y[r] = acc;
+    }
+}
+
+/* ---- FP8 -------------------------------------------------------------- */
+
+/* fp8_quant.cu:103-107,120-121: absmax over the row with fmaxf from 0 (NaN is
+ * dropped by fmaxf), scale = absmax/448 with an IEEE divide, 1 for an all-zero
+ * (or all-NaN) row. */
+static inline float row_scale(float amax) {
+    return (amax > 0.0f) ? (amax / E4M3_MAX) : 1.0f;
+}
+
+/* fp8_quant.cu:89-131 */
+void kco_quantize_fp8_per_token(const float* in, int8_t* out, float* scales,
+                                int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* x = in + r * cols;
+        float amax = 0.0f;
+        for (int64_t c = 0; c < cols; ++c) amax = fmaxf(amax, fabsf(x[c]));
+        float s = row_scale(amax);
+        scales[r] = s;
+        for (int64_t c = 0; c < cols; ++c)
+            out[r * cols + c] = (int8_t)clamp_encode(x[c] / s);
+    }
+}
+
+/* fp8_quant.cu:62-75 (scale supplied by the caller, fp8_quant.cu:215-223) */
+void kco_quantize_fp8_per_tensor(const float* in, int8_t* out, float scale,
+                                 int64_t count) {
+    for (int64_t i = 0; i < count; ++i)
+        out[i] = (int8_t)clamp_encode(in[i] / scale);
+}
+
+/* fp8_quant.cu:145-160: exact decode times the scale (one fp32 rounding). */
+void kco_dequantize_fp8(const int8_t* in, const float* scales, float* out,
+                        int64_t rows, int64_t cols, int per_token) {
+    for (int64_t r = 0; r < rows; ++r) {
+        float s = per_token ? scales[r] : scales[0];
+        for (int64_t c = 0; c < cols; ++c)
+            out[r * cols + c] = kco_e4m3_decode((uint8_t)in[r * cols + c]) * s;
+    }
+}
+
+/* fp8_quant.cu:174-184 */
+void kco_smoothquant_scale(const float* in, const float* smooth, float* out,
+                           int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c)
+            out[r * cols + c] = in[r * cols + c] / smooth[c];
+}
+
+/* ---- extensions ------------------------------------------------------- */
+
+/* Per-token quantization of bf16 activations: widen exactly, then
+ * fp8_quant.cu:89-131 unchanged. */
+void kco_quantize_fp8_per_token_bf16(const uint16_t* in, int8_t* out,
+                                     float* scales, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint16_t* x = in + r * cols;
+        float amax = 0.0f;
+        for (int64_t c = 0; c < cols; ++c)
+            amax = fmaxf(amax, fabsf(kco_bf16_to_f32(x[c])));
+        float s = row_scale(amax);
+        scales[r] = s;
+        for (int64_t c = 0; c < cols; ++c)
+            out[r * cols + c] = (int8_t)clamp_encode(kco_bf16_to_f32(x[c]) / s);
+    }
+}
+
+void kco_col_absmax_f32(const float* in, float* amax, int64_t rows, int64_t cols) {
+    for (int64_t c = 0; c < cols; ++c) amax[c] = 0.0f;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c)
+            amax[c] = fmaxf(amax[c], fabsf(in[r * cols + c]));
+}
+
+void kco_col_absmax_bf16(const uint16_t* in, float* amax, int64_t rows,
+                         int64_t cols) {
+    for (int64_t c = 0; c < cols; ++c) amax[c] = 0.0f;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c)
+            amax[c] = fmaxf(amax[c], fabsf(kco_bf16_to_f32(in[r * cols + c])));
+}
+
+/* SmoothQuant factor with alpha = 0.5 (Xiao et al. 2023, eq. 4):
+ * s_j = sqrt(max|X_j|) / sqrt(max(max|W_j|, 1e-5)), then s_j = max(s_j, 1e-5),
+ * the clamps of the SmoothQuant authors' smooth_lm().  sqrtf and / are the
+ * correctly rounded IEEE operations. */
+void kco_smooth_factors(const float* amax_x, const float* amax_w, float* s,
+                        int64_t cols) {
+    for (int64_t c = 0; c < cols; ++c) {
+        float v = sqrtf(amax_x[c]) / sqrtf(fmaxf(amax_w[c], 1e-5f));
+        s[c] = fmaxf(v, 1e-5f);
+    }
+}
+
+/* X/s (fp8_quant.cu:183) then per-token quantization (fp8_quant.cu:89-131):
+ * the reference's two-launch pipeline, fused. */
+void kco_quantize_fp8_smooth_div_f32(const float* in, const float* s,
+                                     int8_t* out, float* scales,
+                                     int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* x = in + r * cols;
+        float amax = 0.0f;
+        for (int64_t c = 0; c < cols; ++c) amax = fmaxf(amax, fabsf(x[c] / s[c]));
+        float sc = row_scale(amax);
+        scales[r] = sc;
+        for (int64_t c = 0; c < cols; ++c)
+            out[r * cols + c] = (int8_t)clamp_encode((x[c] / s[c]) / sc);
+    }
+}
+
+void kco_quantize_fp8_smooth_div_bf16(const uint16_t* in, const float* s,
+                                      int8_t* out, float* scales,
+                                      int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint16_t* x = in + r * cols;
+        float amax = 0.0f;
+        for (int64_t c = 0; c < cols; ++c)
+            amax = fmaxf(amax, fabsf(kco_bf16_to_f32(x[c]) / s[c]));
+        float sc = row_scale(amax);
+        scales[r] = sc;
+        for (int64_t c = 0; c < cols; ++c)
+            out[r * cols + c] =
+                (int8_t)clamp_encode((kco_bf16_to_f32(x[c]) / s[c]) / sc);
+    }
+}
+
+/* W*s (fp32 multiply) then per-output-channel quantization, i.e. the
+ * per-token quantizer applied to W's rows. */
+void kco_quantize_fp8_smooth_mul_bf16(const uint16_t* in, const float* s,
+                                      int8_t* out, float* scales,
+                                      int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint16_t* w = in + r * cols;
+        float amax = 0.0f;
+        for (int64_t c = 0; c < cols; ++c)
+            amax = fmaxf(amax, fabsf(kco_bf16_to_f32(w[c]) * s[c]));
+        float sc = row_scale(amax);
+        scales[r] = sc;
+        for (int64_t c = 0; c < cols; ++c)
+            out[r * cols + c] =
+                (int8_t)clamp_encode((kco_bf16_to_f32(w[c]) * s[c]) / sc);
+    }
+}

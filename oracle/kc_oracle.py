@@ -1,0 +1,232 @@
+"""ctypes wrapper over the CPU oracle (oracle/kc_oracle.c).
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, ``__graft_entry__.smoke()`` and
+bench.py's ``cpu_baseline`` leg import this module, and only as the checker or
+as the timed CPU baseline.  The product path never imports it.
+
+Arrays are numpy; bf16 tensors travel as ``np.uint16`` bit patterns.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "_build" / "libkc_oracle.so"
+_lib = None
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+
+_SIGS = {
+    "kco_sext4": ([ctypes.c_uint], ctypes.c_int),
+    "kco_e4m3_encode": ([ctypes.c_float], ctypes.c_uint8),
+    "kco_e4m3_decode": ([ctypes.c_uint8], ctypes.c_float),
+    "kco_bf16_to_f32": ([ctypes.c_uint16], ctypes.c_float),
+    "kco_f32_to_bf16": ([ctypes.c_float], ctypes.c_uint16),
+    "kco_e4m3_sweep_mismatches": ([ctypes.c_uint32, ctypes.c_uint64, _P,
+                                   ctypes.POINTER(ctypes.c_uint32)], ctypes.c_uint64),
+    "kco_dequantize_int4": ([_P, _P, _P, _P, _I64, _I64, _I64], None),
+    "kco_gemv_int4_f64": ([_P, _P, _P, _P, _P, _I64, _I64, _I64], None),
+    "kco_gemv_int4_refkernel_f32": ([_P, _P, _P, _P, _P, _I64, _I64, _I64], None),
+    "kco_gemm_int4_bf16_f64": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64], None),
+    "kco_gemv_int4_bf16_f32": ([_P, _P, _P, _P, _P, _I64, _I64, _I64], None),
+    "kco_quantize_fp8_per_token": ([_P, _P, _P, _I64, _I64], None),
+    "kco_quantize_fp8_per_tensor": ([_P, _P, ctypes.c_float, _I64], None),
+    "kco_dequantize_fp8": ([_P, _P, _P, _I64, _I64, ctypes.c_int], None),
+    "kco_smoothquant_scale": ([_P, _P, _P, _I64, _I64], None),
+    "kco_quantize_fp8_per_token_bf16": ([_P, _P, _P, _I64, _I64], None),
+    "kco_col_absmax_f32": ([_P, _P, _I64, _I64], None),
+    "kco_col_absmax_bf16": ([_P, _P, _I64, _I64], None),
+    "kco_smooth_factors": ([_P, _P, _P, _I64], None),
+    "kco_quantize_fp8_smooth_div_f32": ([_P, _P, _P, _P, _I64, _I64], None),
+    "kco_quantize_fp8_smooth_div_bf16": ([_P, _P, _P, _P, _I64, _I64], None),
+    "kco_quantize_fp8_smooth_mul_bf16": ([_P, _P, _P, _P, _I64, _I64], None),
+}
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            raise FileNotFoundError(
+                f"{_LIB_PATH} missing: build it with `make -C oracle`")
+        _lib = ctypes.CDLL(str(_LIB_PATH))
+        for name, (argtypes, restype) in _SIGS.items():
+            fn = getattr(_lib, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
+    return _lib
+
+
+def _p(a: np.ndarray) -> ctypes.c_void_p:
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def _c(a, dtype) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# ---- scalar helpers -------------------------------------------------------
+
+def sext4(n: int) -> int:
+    return lib().kco_sext4(n)
+
+
+def e4m3_encode(x: float) -> int:
+    return int(lib().kco_e4m3_encode(x))
+
+
+def e4m3_decode_table() -> np.ndarray:
+    return np.array([lib().kco_e4m3_decode(c) for c in range(256)], dtype=np.float32)
+
+
+def sweep_mismatches(start: int, codes: np.ndarray):
+    """(mismatch count, first bad fp32 bit pattern) for clamp+encode."""
+    codes = _c(codes, np.uint8)
+    first = ctypes.c_uint32(0)
+    bad = lib().kco_e4m3_sweep_mismatches(start, codes.size, _p(codes),
+                                          ctypes.byref(first))
+    return int(bad), int(first.value)
+
+
+# ---- INT4 -----------------------------------------------------------------
+
+def dequantize_int4(packed, scales, zeros, rows, cols, group_size):
+    packed, scales, zeros = _c(packed, np.uint8), _c(scales, np.float32), _c(zeros, np.uint8)
+    out = np.empty((rows, cols), np.float32)
+    lib().kco_dequantize_int4(_p(packed), _p(scales), _p(zeros), _p(out),
+                              rows, cols, group_size)
+    return out
+
+
+def gemv_int4_f64(packed, scales, zeros, x, rows, cols, group_size):
+    packed, scales, zeros = _c(packed, np.uint8), _c(scales, np.float32), _c(zeros, np.uint8)
+    x = _c(x, np.float32)
+    y = np.empty(rows, np.float64)
+    lib().kco_gemv_int4_f64(_p(packed), _p(scales), _p(zeros), _p(x), _p(y),
+                            rows, cols, group_size)
+    return y
+
+
+def gemv_int4_refkernel_f32(packed, scales, zeros, x, rows, cols, group_size):
+    packed, scales, zeros = _c(packed, np.uint8), _c(scales, np.float32), _c(zeros, np.uint8)
+    x = _c(x, np.float32)
+    y = np.empty(rows, np.float32)
+    lib().kco_gemv_int4_refkernel_f32(_p(packed), _p(scales), _p(zeros), _p(x),
+                                      _p(y), rows, cols, group_size)
+    return y
+
+
+def gemm_int4_bf16_f64(packed, scales, zeros, x_bf16, m, rows, cols, group_size):
+    """Reference GEMV applied to each of the m bf16 activation rows -> [m, rows]."""
+    packed, scales, zeros = _c(packed, np.uint8), _c(scales, np.float32), _c(zeros, np.uint8)
+    x_bf16 = _c(x_bf16, np.uint16)
+    y = np.empty((m, rows), np.float64)
+    lib().kco_gemm_int4_bf16_f64(_p(packed), _p(scales), _p(zeros), _p(x_bf16),
+                                 _p(y), m, rows, cols, group_size)
+    return y
+
+
+def gemv_int4_bf16_f32(packed, scales, zeros, x_bf16, rows, cols, group_size):
+    packed, scales, zeros = _c(packed, np.uint8), _c(scales, np.float32), _c(zeros, np.uint8)
+    x_bf16 = _c(x_bf16, np.uint16)
+    y = np.empty(rows, np.float32)
+    lib().kco_gemv_int4_bf16_f32(_p(packed), _p(scales), _p(zeros), _p(x_bf16),
+                                 _p(y), rows, cols, group_size)
+    return y
+
+
+# ---- FP8 ------------------------------------------------------------------
+
+def quantize_fp8_per_token(x):
+    x = _c(x, np.float32)
+    rows, cols = x.shape
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty(rows, np.float32)
+    lib().kco_quantize_fp8_per_token(_p(x), _p(q), _p(s), rows, cols)
+    return q, s
+
+
+def quantize_fp8_per_tensor(x, scale):
+    x = _c(x, np.float32)
+    q = np.empty(x.shape, np.int8)
+    lib().kco_quantize_fp8_per_tensor(_p(x), _p(q), float(scale), x.size)
+    return q
+
+
+def dequantize_fp8(q, scales, rows, cols, per_token=True):
+    q, scales = _c(q, np.int8), _c(scales, np.float32)
+    out = np.empty((rows, cols), np.float32)
+    lib().kco_dequantize_fp8(_p(q), _p(scales), _p(out), rows, cols, int(per_token))
+    return out
+
+
+def smoothquant_scale(x, smooth):
+    x, smooth = _c(x, np.float32), _c(smooth, np.float32)
+    rows, cols = x.shape
+    out = np.empty_like(x)
+    lib().kco_smoothquant_scale(_p(x), _p(smooth), _p(out), rows, cols)
+    return out
+
+
+def quantize_fp8_per_token_bf16(x_bf16):
+    x_bf16 = _c(x_bf16, np.uint16)
+    rows, cols = x_bf16.shape
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty(rows, np.float32)
+    lib().kco_quantize_fp8_per_token_bf16(_p(x_bf16), _p(q), _p(s), rows, cols)
+    return q, s
+
+
+def col_absmax(x):
+    if x.dtype == np.uint16:
+        x = _c(x, np.uint16)
+        fn = lib().kco_col_absmax_bf16
+    else:
+        x = _c(x, np.float32)
+        fn = lib().kco_col_absmax_f32
+    rows, cols = x.shape
+    out = np.empty(cols, np.float32)
+    fn(_p(x), _p(out), rows, cols)
+    return out
+
+
+def smooth_factors(amax_x, amax_w):
+    amax_x, amax_w = _c(amax_x, np.float32), _c(amax_w, np.float32)
+    s = np.empty_like(amax_x)
+    lib().kco_smooth_factors(_p(amax_x), _p(amax_w), _p(s), amax_x.size)
+    return s
+
+
+def quantize_fp8_smooth_div(x, s):
+    """x [rows, cols] fp32 or bf16 bits; returns (codes, scales) of (x / s)."""
+    s = _c(s, np.float32)
+    if x.dtype == np.uint16:
+        x = _c(x, np.uint16)
+        fn = lib().kco_quantize_fp8_smooth_div_bf16
+    else:
+        x = _c(x, np.float32)
+        fn = lib().kco_quantize_fp8_smooth_div_f32
+    rows, cols = x.shape
+    q = np.empty((rows, cols), np.int8)
+    sc = np.empty(rows, np.float32)
+    fn(_p(x), _p(s), _p(q), _p(sc), rows, cols)
+    return q, sc
+
+
+def quantize_fp8_smooth_mul_bf16(w_bf16, s):
+    w_bf16, s = _c(w_bf16, np.uint16), _c(s, np.float32)
+    rows, cols = w_bf16.shape
+    q = np.empty((rows, cols), np.int8)
+    sc = np.empty(rows, np.float32)
+    lib().kco_quantize_fp8_smooth_mul_bf16(_p(w_bf16), _p(s), _p(q), _p(sc), rows, cols)
+    return q, sc
+
+
+def lib_path() -> str:
+    return os.fspath(_LIB_PATH)

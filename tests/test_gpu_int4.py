@@ -1,0 +1,270 @@
+"""INT4 dequantization, GEMV and MFMA GEMM on the GPU vs the CPU oracle.
+
+Bars (from the build's north star): dequantization is bit-exact (one fp32
+rounding, as the reference); fp32-output GEMV within relative L2 1e-5 of the
+fp64 truth; bf16-output GEMV/GEMM within relative L2 1e-2.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import kc_abi
+from kc_abi import ptr, stream
+from kc_data import bf16_bits_to_f32, make_int4, normal_bf16, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-5
+TOL_BF16 = 1e-2
+
+
+def _dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _dev_bf16(torch, bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).cuda().view(torch.bfloat16)
+
+
+def _host_bf16_bits(t):
+    return t.view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+
+
+def _gemv_f32(torch, packed, scales, zeros, x, rows, cols, gs):
+    L = kc_abi.lib()
+    dp, ds, dz, dx = (_dev(torch, packed), _dev(torch, scales), _dev(torch, zeros),
+                      _dev(torch, x))
+    dy = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")
+    print(f"launch_gemv_int4 rows={rows} cols={cols} gs={gs}", flush=True)
+    L.launch_gemv_int4(ptr(dp), ptr(ds), ptr(dz), ptr(dx), ptr(dy), rows, cols, gs, stream())
+    kc_abi.check("launch_gemv_int4")
+    return dy.cpu().numpy()
+
+
+def _dequant(torch, packed, scales, zeros, rows, cols, gs):
+    L = kc_abi.lib()
+    dp, ds, dz = _dev(torch, packed), _dev(torch, scales), _dev(torch, zeros)
+    out = torch.full((rows, cols), float("nan"), dtype=torch.float32, device="cuda")
+    print(f"launch_dequantize_int4 rows={rows} cols={cols} gs={gs}", flush=True)
+    L.launch_dequantize_int4(ptr(dp), ptr(ds), ptr(dz), ptr(out), rows, cols, gs, stream())
+    kc_abi.check("launch_dequantize_int4")
+    return out.cpu().numpy()
+
+
+def _gemv_bf16(torch, packed, scales, zeros, xb, rows, cols, gs):
+    L = kc_abi.lib()
+    dp, ds, dz, dx = (_dev(torch, packed), _dev(torch, scales), _dev(torch, zeros),
+                      _dev_bf16(torch, xb))
+    dy = torch.full((rows,), float("nan"), dtype=torch.bfloat16, device="cuda")
+    print(f"kc_gemv_int4_bf16 rows={rows} cols={cols} gs={gs}", flush=True)
+    st = L.kc_gemv_int4_bf16(ptr(dp), ptr(ds), ptr(dz), ptr(dx), ptr(dy), rows, cols, gs,
+                             stream())
+    kc_abi.check("kc_gemv_int4_bf16", st)
+    torch.cuda.synchronize()
+    return bf16_bits_to_f32(_host_bf16_bits(dy))
+
+
+# ---------------------------------------------------------------------------
+# Reference known-answer tests through the GPU
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["deq_basic", "deq_multigroup", "deq_rng42"])
+def test_dequant_reference_kats(gpu, golden, name):
+    rows, cols, gs = (int(v) for v in golden[f"{name}_shape"])
+    out = _dequant(gpu, golden[f"{name}_packed"], golden[f"{name}_scales"],
+                   golden[f"{name}_zeros"], rows, cols, gs)
+    np.testing.assert_array_equal(out, golden[f"{name}_expected"])
+
+
+@pytest.mark.parametrize("name,atol", [("gemv_srand42", 1e-4), ("triton_small", 5e-3),
+                                       ("triton_medium", 5e-3), ("triton_gs64", 5e-3)])
+def test_gemv_reference_kats(gpu, golden, oracle, name, atol):
+    rows, cols, gs = (int(v) for v in golden[f"{name}_shape"])
+    packed, scales, zeros = (golden[f"{name}_packed"], golden[f"{name}_scales"],
+                             golden[f"{name}_zeros"])
+    x = golden[f"{name}_x"]
+    y = _gemv_f32(gpu, packed, scales, zeros, x, rows, cols, gs)
+    assert np.max(np.abs(y - golden[f"{name}_expected"])) < atol
+    truth = oracle.gemv_int4_f64(packed, scales, zeros.reshape(-1), x, rows, cols, gs)
+    assert rel_l2(y, truth) < TOL_F32
+
+
+# ---------------------------------------------------------------------------
+# cfg0 and shape coverage (fast and generic paths)
+# ---------------------------------------------------------------------------
+
+def test_gemv_cfg0_4096(gpu, oracle):
+    """BASELINE cfg0: K = N = 4096, gs 128, fp32 x and y."""
+    rows = cols = 4096
+    gs = 128
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=1)
+    x = np.random.default_rng(2).standard_normal(cols).astype(np.float32)
+    y = _gemv_f32(gpu, packed, scales, zeros, x, rows, cols, gs)
+    zf = zeros.reshape(-1)
+    truth = oracle.gemv_int4_f64(packed, scales, zf, x, rows, cols, gs)
+    assert rel_l2(y, truth) < TOL_F32
+    ref32 = oracle.gemv_int4_refkernel_f32(packed, scales, zf, x, rows, cols, gs)
+    assert rel_l2(y, ref32) < 2 * TOL_F32
+
+
+SHAPES = [
+    # (rows, cols, gs): fast path (gs pow2 >= 32)
+    (1, 32, 32), (3, 64, 32), (17, 256, 64), (16, 4096, 128), (33, 2080, 32),
+    (64, 14336, 128), (100, 384, 128), (5, 6144, 256), (257, 1024, 1024),
+    # generic path: gs < 32, non power of two, tiny K
+    (4, 8, 8), (7, 2, 2), (9, 96, 96), (5, 120, 24), (3, 1000, 10), (2, 4, 4),
+]
+
+
+@pytest.mark.parametrize("rows,cols,gs", SHAPES)
+def test_gemv_f32_shapes(gpu, oracle, rows, cols, gs):
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=rows * 7 + cols)
+    x = np.random.default_rng(cols).standard_normal(cols).astype(np.float32)
+    y = _gemv_f32(gpu, packed, scales, zeros, x, rows, cols, gs)
+    truth = oracle.gemv_int4_f64(packed, scales, zeros.reshape(-1), x, rows, cols, gs)
+    assert rel_l2(y, truth) < TOL_F32
+
+
+@pytest.mark.parametrize("rows,cols,gs", SHAPES)
+def test_dequant_shapes_bit_exact(gpu, oracle, rows, cols, gs):
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=rows * 3 + cols)
+    out = _dequant(gpu, packed, scales, zeros, rows, cols, gs)
+    exp = oracle.dequantize_int4(packed, scales, zeros.reshape(-1), rows, cols, gs)
+    np.testing.assert_array_equal(out, exp)
+
+
+def test_gemv_sign_and_zero_point_invariants(gpu):
+    rows, cols, gs = 64, 1024, 128
+    x = np.random.default_rng(3).standard_normal(cols).astype(np.float32)
+    G = cols // gs
+    # 0x33 with zero point 3 -> all weights 0 -> y == 0 exactly
+    y = _gemv_f32(gpu, np.full((rows, cols // 2), 0x33, np.uint8),
+                  np.full((rows, G), 0.01, np.float32), np.full((rows, G // 2), 0x33, np.uint8),
+                  x, rows, cols, gs)
+    assert np.all(y == 0.0)
+    # 0x88 with zero point 8 -> every weight -16 * s (sign extension)
+    y = _gemv_f32(gpu, np.full((rows, cols // 2), 0x88, np.uint8),
+                  np.full((rows, G), 0.5, np.float32), np.full((rows, G // 2), 0x88, np.uint8),
+                  x, rows, cols, gs)
+    np.testing.assert_allclose(y, np.full(rows, -8.0 * x.astype(np.float64).sum()), rtol=1e-5)
+
+
+def test_gemv_linearity(gpu):
+    rows, cols, gs = 256, 4096, 128
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=4)
+    rng = np.random.default_rng(5)
+    x1 = rng.standard_normal(cols).astype(np.float32)
+    x2 = rng.standard_normal(cols).astype(np.float32)
+    y1 = _gemv_f32(gpu, packed, scales, zeros, x1, rows, cols, gs)
+    y2 = _gemv_f32(gpu, packed, scales, zeros, x2, rows, cols, gs)
+    y3 = _gemv_f32(gpu, packed, scales, zeros, (2 * x1 - x2).astype(np.float32), rows, cols, gs)
+    assert rel_l2(y3, 2 * y1.astype(np.float64) - y2) < 1e-5
+    y0 = _gemv_f32(gpu, packed, scales, zeros, np.zeros(cols, np.float32), rows, cols, gs)
+    assert np.all(y0 == 0.0)
+
+
+def test_gemv_unaligned_pointers_take_generic_path(gpu, oracle):
+    torch = gpu
+    rows, cols, gs = 8, 512, 128
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=6)
+    x = np.random.default_rng(7).standard_normal(cols + 1).astype(np.float32)
+    L = kc_abi.lib()
+    dp = torch.empty(packed.size + 3, dtype=torch.uint8, device="cuda")
+    dp[3:] = _dev(torch, packed.reshape(-1))
+    dx = _dev(torch, x)
+    ds, dz = _dev(torch, scales), _dev(torch, zeros)
+    dy = torch.empty(rows, dtype=torch.float32, device="cuda")
+    L.launch_gemv_int4(ctypes.c_void_p(dp.data_ptr() + 3), ptr(ds), ptr(dz),
+                       ctypes.c_void_p(dx.data_ptr() + 4), ptr(dy), rows, cols, gs, stream())
+    kc_abi.check("launch_gemv_int4")
+    truth = oracle.gemv_int4_f64(packed, scales, zeros.reshape(-1), x[1:], rows, cols, gs)
+    assert rel_l2(dy.cpu().numpy(), truth) < TOL_F32
+
+
+def test_reference_launchers_empty_shapes(gpu):
+    L = kc_abi.lib()
+    L.kc_get_last_error()
+    L.launch_gemv_int4(None, None, None, None, None, 0, 256, 128, stream())
+    L.launch_dequantize_int4(None, None, None, None, 0, 256, 128, stream())
+    assert L.kc_get_last_error() == 0
+
+
+# ---------------------------------------------------------------------------
+# bf16 GEMV at the Llama-3-8B decode shapes (BASELINE cfg2)
+# ---------------------------------------------------------------------------
+
+LLAMA_SHAPES = [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)]  # (N, K)
+
+
+@pytest.mark.parametrize("rows,cols", LLAMA_SHAPES)
+def test_gemv_bf16_llama_shapes(gpu, oracle, rows, cols):
+    gs = 128
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=2000 + rows + cols)
+    xb = normal_bf16(cols, seed=2001 + cols)
+    y = _gemv_bf16(gpu, packed, scales, zeros, xb, rows, cols, gs)
+    truth = oracle.gemv_int4_f64(packed, scales, zeros.reshape(-1), bf16_bits_to_f32(xb),
+                                 rows, cols, gs)
+    assert rel_l2(y, truth) < TOL_BF16
+    # tighter: bf16 output rounding alone is ~1e-3
+    assert rel_l2(y, truth) < 3e-3
+
+
+@pytest.mark.parametrize("rows,cols,gs", [(5, 96, 32), (3, 100, 10), (70, 2048, 64)])
+def test_gemv_bf16_other_shapes(gpu, oracle, rows, cols, gs):
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=rows + cols)
+    xb = normal_bf16(cols, seed=cols)
+    y = _gemv_bf16(gpu, packed, scales, zeros, xb, rows, cols, gs)
+    truth = oracle.gemv_int4_f64(packed, scales, zeros.reshape(-1), bf16_bits_to_f32(xb),
+                                 rows, cols, gs)
+    assert rel_l2(y, truth) < 3e-3
+
+
+# ---------------------------------------------------------------------------
+# MFMA small-batch GEMM (BASELINE cfg3) vs the reference GEMV per row
+# ---------------------------------------------------------------------------
+
+def _gemm(torch, packed, scales, zeros, xb, m, rows, cols, gs):
+    L = kc_abi.lib()
+    dp, ds, dz, dx = (_dev(torch, packed), _dev(torch, scales), _dev(torch, zeros),
+                      _dev_bf16(torch, xb))
+    dy = torch.full((m, rows), float("nan"), dtype=torch.bfloat16, device="cuda")
+    print(f"kc_gemm_int4_bf16 m={m} rows={rows} cols={cols} gs={gs}", flush=True)
+    st = L.kc_gemm_int4_bf16(ptr(dp), ptr(ds), ptr(dz), ptr(dx), ptr(dy), m, rows, cols, gs,
+                             stream())
+    kc_abi.check("kc_gemm_int4_bf16", st)
+    torch.cuda.synchronize()
+    return bf16_bits_to_f32(_host_bf16_bits(dy)).reshape(m, rows), (dp, ds, dz, dx)
+
+
+@pytest.mark.parametrize("m", [4, 16, 64])
+def test_gemm_cfg3(gpu, oracle, m):
+    """M in {4, 16, 64}, K = 8192, N = 28672, gs 128.  Sampled rows against the
+    fp64 oracle (reference GEMV per activation row); every row against an fp32
+    GPU reference built from the bit-exact dequantization."""
+    torch = gpu
+    rows, cols, gs = 28672, 8192, 128
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=3000 + m)
+    xb = normal_bf16((m, cols), seed=3001 + m)
+    y, (dp, ds, dz, dx) = _gemm(torch, packed, scales, zeros, xb, m, rows, cols, gs)
+    sample = np.arange(0, rows, 97)
+    truth = oracle.gemm_int4_bf16_f64(packed[sample], scales[sample], zeros[sample].reshape(-1),
+                                      xb, m, sample.size, cols, gs)
+    assert rel_l2(y[:, sample], truth) < 3e-3
+    L = kc_abi.lib()
+    W = torch.empty(rows, cols, dtype=torch.float32, device="cuda")
+    L.launch_dequantize_int4(ptr(dp), ptr(ds), ptr(dz), ptr(W), rows, cols, gs, stream())
+    kc_abi.check("launch_dequantize_int4")
+    ref = (dx.float() @ W.t()).cpu().numpy()
+    assert rel_l2(y, ref) < 3e-3
+
+
+@pytest.mark.parametrize("m,rows,cols,gs", [(1, 100, 1024, 128), (3, 64, 256, 128),
+                                            (17, 130, 2048, 256), (33, 48, 640, 128),
+                                            (64, 16, 128, 128), (5, 40, 512, 64)])
+def test_gemm_shapes(gpu, oracle, m, rows, cols, gs):
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=m * 1000 + rows)
+    xb = normal_bf16((m, cols), seed=m + rows)
+    y, _ = _gemm(gpu, packed, scales, zeros, xb, m, rows, cols, gs)
+    truth = oracle.gemm_int4_bf16_f64(packed, scales, zeros.reshape(-1), xb, m, rows, cols, gs)
+    assert rel_l2(y, truth) < 3e-3

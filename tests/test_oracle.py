@@ -1,0 +1,441 @@
+"""Pins the CPU oracle (oracle/kc_oracle.c) before it is trusted as the checker.
+
+Each oracle function is checked against the reference's own known-answer
+tests (tests/golden/reference_kats.npz, made by
+tests/golden/make_reference_kats.py from the reference tests' inputs and
+expected-value expressions), against an independent library (torch's
+float8_e4m3fn for the OCP encoding), or against what the mathematics fixes
+(closed forms, invariants, brute force), so that a dropped term, a wrong
+sign or index, or a transposed operand fails at least one test.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from kc_data import bf16_bits_to_f32, f32_to_bf16_bits, make_int4, outlier_activations, rel_l2
+
+
+def _kat(golden, name):
+    rows, cols, gs = (int(v) for v in golden[f"{name}_shape"])
+    return (golden[f"{name}_packed"], golden[f"{name}_scales"], golden[f"{name}_zeros"],
+            rows, cols, gs)
+
+
+def _flat_zeros(z):
+    return np.ascontiguousarray(z).reshape(-1)
+
+
+# ---------------------------------------------------------------------------
+# INT4 against the reference's own tests
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["deq_basic", "deq_multigroup", "deq_rng42"])
+def test_dequant_reference_kats(oracle, golden, name):
+    """test_quant_int4.cpp:35-88, :148-199; test_transformer_bindings.py:185-196.
+    The expected values are single fp32 products, so equality is exact."""
+    packed, scales, zeros, rows, cols, gs = _kat(golden, name)
+    out = oracle.dequantize_int4(packed, scales, _flat_zeros(zeros), rows, cols, gs)
+    np.testing.assert_array_equal(out, golden[f"{name}_expected"])
+
+
+def test_gemv_reference_kat_srand42(oracle, golden):
+    """test_quant_int4.cpp:90-146 (tolerance 1e-4 absolute there)."""
+    packed, scales, zeros, rows, cols, gs = _kat(golden, "gemv_srand42")
+    x = golden["gemv_srand42_x"]
+    exp = golden["gemv_srand42_expected"]
+    y64 = oracle.gemv_int4_f64(packed, scales, _flat_zeros(zeros), x, rows, cols, gs)
+    yref = oracle.gemv_int4_refkernel_f32(packed, scales, _flat_zeros(zeros), x, rows, cols, gs)
+    assert np.max(np.abs(y64 - exp)) < 1e-4
+    assert np.max(np.abs(yref - exp)) < 1e-4
+    assert rel_l2(y64, exp) < 1e-6
+
+
+@pytest.mark.parametrize("name", ["triton_small", "triton_medium", "triton_gs64"])
+def test_gemv_reference_kats_triton(oracle, golden, name):
+    """test_triton_kernels.py:76-119,244-256 (rtol 1e-2, atol 5e-3 there)."""
+    packed, scales, zeros, rows, cols, gs = _kat(golden, name)
+    x = golden[f"{name}_x"]
+    exp = golden[f"{name}_expected"]
+    y64 = oracle.gemv_int4_f64(packed, scales, _flat_zeros(zeros), x, rows, cols, gs)
+    assert np.allclose(y64, exp, rtol=1e-2, atol=5e-3)
+    assert rel_l2(y64, exp) < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# INT4 invariants and independent restatements
+# ---------------------------------------------------------------------------
+
+def _numpy_dequant(packed, scales, zeros_flat, rows, cols, gs):
+    """Vectorized restatement written independently of the C oracle."""
+    p = packed.astype(np.int32)
+    q = np.empty((rows, cols), np.int32)
+    q[:, 0::2] = p & 0xF
+    q[:, 1::2] = p >> 4
+    q = np.where(q >= 8, q - 16, q)
+    G = cols // gs
+    g = np.arange(cols) // gs
+    zidx = np.arange(rows)[:, None] * (G // 2) + (g // 2)[None, :]
+    zb = zeros_flat.astype(np.int32)[zidx]
+    z = np.where((g % 2 == 0)[None, :], zb & 0xF, zb >> 4)
+    s = scales.reshape(rows, G)[:, g]
+    return (q - z).astype(np.float32) * s
+
+
+@pytest.mark.parametrize("rows,cols,gs", [(7, 256, 128), (5, 384, 128), (3, 96, 32),
+                                          (4, 64, 64), (2, 10, 2), (3, 12, 6)])
+def test_dequant_matches_numpy_restatement(oracle, rows, cols, gs):
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=rows * 100 + cols)
+    zf = _flat_zeros(zeros)
+    out = oracle.dequantize_int4(packed, scales, zf, rows, cols, gs)
+    np.testing.assert_array_equal(out, _numpy_dequant(packed, scales, zf, rows, cols, gs))
+
+
+def test_sign_extension_not_offset(oracle):
+    """0x88 with zero point 8: sext4(8) = -8, so w = (-8 - 8) * s = -16 s;
+    unsigned (GPTQ-style) nibbles would give 0.  quant_int4.cu:34-48,95-96."""
+    rows, cols, gs = 2, 256, 128
+    packed = np.full((rows, cols // 2), 0x88, np.uint8)
+    scales = np.full((rows, 2), 0.25, np.float32)
+    zeros = np.full((rows, 1), 0x88, np.uint8)
+    out = oracle.dequantize_int4(packed, scales, zeros.reshape(-1), rows, cols, gs)
+    assert np.all(out == -4.0)
+
+
+def test_zero_point_cancels_nibble(oracle):
+    """Nibble 3 with zero point 3 dequantizes to exactly 0 -> y = 0."""
+    rows, cols, gs = 3, 512, 128
+    packed = np.full((rows, cols // 2), 0x33, np.uint8)
+    scales = np.random.default_rng(0).uniform(0.005, 0.02, (rows, 4)).astype(np.float32)
+    zeros = np.full((rows, 2), 0x33, np.uint8)
+    x = np.random.default_rng(1).standard_normal(cols).astype(np.float32)
+    y = oracle.gemv_int4_f64(packed, scales, zeros.reshape(-1), x, rows, cols, gs)
+    assert np.all(y == 0.0)
+
+
+def test_zero_point_group_parity(oracle):
+    """Even groups use the low nibble of the zero byte, odd groups the high."""
+    rows, cols, gs = 1, 256, 64   # G = 4: zero bytes [z0|z1<<4, z2|z3<<4]
+    packed = np.zeros((rows, cols // 2), np.uint8)     # all weights sext4(0) = 0
+    scales = np.ones((rows, 4), np.float32)
+    zeros = np.array([0x21, 0x43], np.uint8)            # z = 1, 2, 3, 4
+    out = oracle.dequantize_int4(packed, scales, zeros, rows, cols, gs)
+    for g, z in enumerate([1, 2, 3, 4]):
+        assert np.all(out[0, g * gs:(g + 1) * gs] == -z)
+
+
+def test_zero_row_stride_is_floor(oracle):
+    """G odd: row r's zero bytes start at r * floor(G/2) (quant_int4.cu:93)."""
+    rows, cols, gs = 3, 96, 32   # G = 3, floor(G/2) = 1
+    packed = np.zeros((rows, cols // 2), np.uint8)
+    scales = np.ones((rows, 3), np.float32)
+    zeros = np.array([0x21, 0x43, 0x65, 0x07], np.uint8)
+    out = oracle.dequantize_int4(packed, scales, zeros, rows, cols, gs)
+    # row r, group g reads byte r + g // 2
+    for r in range(rows):
+        for g in range(3):
+            zb = int(zeros[r + g // 2])
+            z = zb & 0xF if g % 2 == 0 else zb >> 4
+            assert np.all(out[r, g * gs:(g + 1) * gs] == -z)
+
+
+def test_gemv_brute_force_tiny(oracle):
+    rows, cols, gs = 3, 8, 4
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=5)
+    x = np.random.default_rng(6).standard_normal(cols).astype(np.float32)
+    y = oracle.gemv_int4_f64(packed, scales, zeros.reshape(-1), x, rows, cols, gs)
+    G = cols // gs
+    for r in range(rows):
+        acc = 0.0
+        for k in range(cols):
+            byte = int(packed[r, k // 2])
+            nib = (byte >> 4) if k % 2 else (byte & 0xF)
+            q = nib - 16 if nib >= 8 else nib
+            g = k // gs
+            zb = int(zeros.reshape(-1)[r * (G // 2) + g // 2])
+            z = (zb >> 4) if g % 2 else (zb & 0xF)
+            w = float(np.float32(q - z) * np.float32(scales[r, g]))
+            acc += w * float(x[k])
+        assert math.isclose(y[r], acc, rel_tol=1e-12, abs_tol=1e-12)
+
+
+def test_gemv_linearity_and_matmul(oracle):
+    rows, cols, gs = 16, 1024, 128
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=11)
+    zf = zeros.reshape(-1)
+    rng = np.random.default_rng(12)
+    x1 = rng.standard_normal(cols).astype(np.float32)
+    x2 = rng.standard_normal(cols).astype(np.float32)
+    y1 = oracle.gemv_int4_f64(packed, scales, zf, x1, rows, cols, gs)
+    y2 = oracle.gemv_int4_f64(packed, scales, zf, x2, rows, cols, gs)
+    y12 = oracle.gemv_int4_f64(packed, scales, zf, (x1 + x2).astype(np.float32), rows, cols, gs)
+    # x1 + x2 is rounded to fp32 once per element, so compare at that level
+    assert rel_l2(y12, y1 + y2) < 1e-6
+    W = oracle.dequantize_int4(packed, scales, zf, rows, cols, gs).astype(np.float64)
+    np.testing.assert_allclose(y1, W @ x1.astype(np.float64), rtol=1e-12, atol=1e-12)
+    assert np.all(oracle.gemv_int4_f64(packed, scales, zf, np.zeros(cols, np.float32),
+                                       rows, cols, gs) == 0.0)
+
+
+def test_refkernel_order_within_tolerance(oracle):
+    """The reference kernel's fp32 order stays within 1e-5 of the fp64 truth
+    at the cfg0 distribution (here 256 x 4096)."""
+    rows, cols, gs = 256, 4096, 128
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=0)
+    x = np.random.default_rng(1).standard_normal(cols).astype(np.float32)
+    zf = zeros.reshape(-1)
+    y64 = oracle.gemv_int4_f64(packed, scales, zf, x, rows, cols, gs)
+    y32 = oracle.gemv_int4_refkernel_f32(packed, scales, zf, x, rows, cols, gs)
+    assert rel_l2(y32, y64) < 1e-5
+
+
+def test_gemm_is_gemv_per_row(oracle):
+    rows, cols, gs, m = 8, 512, 128, 3
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=21)
+    zf = zeros.reshape(-1)
+    xb = f32_to_bf16_bits(np.random.default_rng(22).standard_normal((m, cols)).astype(np.float32))
+    Y = oracle.gemm_int4_bf16_f64(packed, scales, zf, xb, m, rows, cols, gs)
+    for i in range(m):
+        y = oracle.gemv_int4_f64(packed, scales, zf, bf16_bits_to_f32(xb[i]), rows, cols, gs)
+        np.testing.assert_array_equal(Y[i], y)
+    y32 = oracle.gemv_int4_bf16_f32(packed, scales, zf, xb[0], rows, cols, gs)
+    assert rel_l2(y32, Y[0]) < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# E4M3 encoding: OCP spec, cross-checked against torch.float8_e4m3fn
+# ---------------------------------------------------------------------------
+
+def _torch_e4m3(bits_u32: np.ndarray) -> np.ndarray:
+    f = torch.from_numpy(bits_u32.view(np.float32).copy())
+    return f.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def test_e4m3_special_cases(oracle):
+    enc = oracle.e4m3_encode
+    assert enc(0.0) == 0x00 and enc(-0.0) == 0x80
+    assert enc(448.0) == 0x7E and enc(-448.0) == 0xFE
+    assert enc(2.0 ** -9) == 0x01 and enc(-(2.0 ** -9)) == 0x81
+    assert enc(2.0 ** -10) == 0x00                      # tie -> even (0)
+    assert enc(3 * 2.0 ** -10) == 0x02                  # 1.5 units -> 2 (even)
+    assert enc(2.0 ** -6) == 0x08                       # min normal
+    assert enc(1.0) == 0x38 and enc(1.0625) == 0x38     # 1 + 1/16: tie -> even
+    assert enc(1.1875) == 0x3A                          # 1 + 3/16: tie -> even (1.25)
+    assert enc(464.0) == 0x7E and enc(1e30) == 0x7E     # saturate to finite
+    assert enc(float("inf")) == 0x7E and enc(float("-inf")) == 0xFE
+    assert enc(float("nan")) & 0x7F == 0x7F
+
+
+def test_e4m3_decode_table_matches_torch(oracle):
+    table = oracle.e4m3_decode_table()
+    ref = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn)
+    ref = ref.to(torch.float32).numpy()
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(table), nan)
+    assert set(np.flatnonzero(nan)) == {0x7F, 0xFF}
+    np.testing.assert_array_equal(table[~nan], ref[~nan])
+
+
+def _boundary_dense_patterns():
+    """Every fp32 magnitude <= 448 whose low 14 mantissa bits are one of a few
+    values on either side of the E4M3 rounding points (which sit at bit 19 for
+    normals and at bits 20..23 for subnormal results), both signs."""
+    hi = np.arange(0, (0x43E00000 >> 14) + 1, dtype=np.uint32) << 14
+    lows = np.array([0, 1, 0x1FFF, 0x2000, 0x2001, 0x3FFF], np.uint32)
+    mags = (hi[:, None] | lows[None, :]).reshape(-1)
+    mags = mags[mags <= 0x43E00000]
+    return np.concatenate([mags, mags | np.uint32(0x80000000)])
+
+
+def test_e4m3_encoder_matches_torch_boundary_dense(oracle):
+    bits = _boundary_dense_patterns()
+    codes = _torch_e4m3(bits)
+    # every 97th block of 2^14 consecutive patterns, both signs
+    mism = 0
+    for h in range(0, (0x43E00000 >> 14) + 1, 97):
+        start = h << 14
+        rng_bits = np.arange(start, start + (1 << 14), dtype=np.uint32)
+        for sign in (0, 0x80000000):
+            b = rng_bits | np.uint32(sign)
+            bad, _ = oracle.sweep_mismatches(int(b[0]), _torch_e4m3(b))
+            mism += bad
+    assert mism == 0
+    # and the boundary-dense set, one pattern at a time through the encoder
+    enc = np.frombuffer(bytes(oracle.lib().kco_e4m3_encode(float(f))
+                              for f in bits.view(np.float32)), np.uint8)
+    assert np.array_equal(enc, codes)
+
+
+@pytest.mark.slow
+def test_e4m3_encoder_matches_torch_exhaustive(oracle):
+    """All 2.27e9 fp32 patterns with |x| <= 448 (about a minute)."""
+    top = 0x43E00000
+    chunk = 1 << 26
+    for sign in (0, 0x80000000):
+        for start in range(0, top + 1, chunk):
+            n = min(chunk, top + 1 - start)
+            b = np.arange(start, start + n, dtype=np.uint32) | np.uint32(sign)
+            bad, first = oracle.sweep_mismatches(int(b[0]), _torch_e4m3(b))
+            assert bad == 0, hex(first)
+
+
+# ---------------------------------------------------------------------------
+# FP8 quantization
+# ---------------------------------------------------------------------------
+
+def _torch_per_token(x: np.ndarray):
+    """Independent per-token restatement with torch ops (NaN-free input)."""
+    t = torch.from_numpy(x)
+    amax = t.abs().amax(dim=1)
+    scale = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+    q = torch.clamp(t / scale[:, None], -448.0, 448.0).to(torch.float8_e4m3fn)
+    return q.view(torch.int8).numpy(), scale.numpy()
+
+
+def test_per_token_matches_torch_restatement(oracle):
+    x, _ = outlier_activations(64, 4096, 0.01, 50.0, seed=1)
+    q, s = oracle.quantize_fp8_per_token(x)
+    tq, ts = _torch_per_token(x)
+    np.testing.assert_array_equal(s, ts)
+    np.testing.assert_array_equal(q, tq)
+
+
+def test_per_token_weight_distribution(oracle):
+    w = (np.random.default_rng(3).standard_normal((128, 4096)) * 0.02).astype(np.float32)
+    q, s = oracle.quantize_fp8_per_token(w)
+    tq, ts = _torch_per_token(w)
+    np.testing.assert_array_equal(s, ts)
+    np.testing.assert_array_equal(q, tq)
+
+
+@pytest.mark.parametrize("name", ["fp8_tok_srand42_x", "fp8_tok_rng42_x", "fp8_tok_rng11_x"])
+def test_per_token_reference_roundtrip_bound(oracle, golden, name):
+    """test_fp8_quant.cpp:34-71, test_transformer_bindings.py:212-220,
+    test_vllm_backend.py:214-223: round-trip relative error < 15 %."""
+    x = golden[name]
+    q, s = oracle.quantize_fp8_per_token(x)
+    xh = oracle.dequantize_fp8(q, s, *x.shape, per_token=True)
+    nz = np.abs(x) > 1e-6
+    assert np.max(np.abs(xh[nz] - x[nz]) / np.abs(x[nz])) < 0.15
+
+
+def test_per_tensor_reference_roundtrip_bound(oracle, golden):
+    """test_fp8_quant.cpp:137-174."""
+    x = golden["fp8_tensor_srand7_x"]
+    scale = golden["fp8_tensor_srand7_scale"]
+    q = oracle.quantize_fp8_per_tensor(x, scale[0])
+    xh = oracle.dequantize_fp8(q, scale, *x.shape, per_token=False)
+    nz = np.abs(x) > 1e-6
+    assert np.max(np.abs(xh[nz] - x[nz]) / np.abs(x[nz])) < 0.15
+
+
+def test_zero_rows_and_specials(oracle):
+    """All-zero row -> scale 1 and codes 0 (test_fp8_quant.cpp:73-97);
+    NaN ignored by the absmax and clamped to +448; -0 keeps its sign."""
+    x = np.zeros((4, 32), np.float32)
+    x[1, 3] = np.nan
+    x[2, :] = -0.0
+    x[3, :] = 1.0
+    x[3, 5] = np.nan
+    x[3, 6] = -2.0
+    q, s = oracle.quantize_fp8_per_token(x)
+    assert s[0] == 1.0 and s[1] == 1.0 and s[2] == 1.0
+    assert s[3] == np.float32(2.0) / np.float32(448.0)
+    assert np.all(q[0] == 0) and np.all(q[2].view(np.uint8) == 0x80)
+    assert q[1, 3].view(np.uint8) == 0x7E and q[3, 5].view(np.uint8) == 0x7E
+    assert q[3, 6].view(np.uint8) == 0xFE
+    assert q[3, 0].view(np.uint8) == oracle.e4m3_encode(np.float32(1.0) / s[3])
+
+
+def test_per_tensor_zero_scale_saturates(oracle):
+    """Via ctypes the reference passes scale 0 (kernel_craft_torch_ops.py:347):
+    x/0 is +-inf (or NaN for 0/0), clamped to +-448 (or +448)."""
+    x = np.array([[1.0, -1.0, 0.0, -0.0]], np.float32)
+    q = oracle.quantize_fp8_per_tensor(x, 0.0).view(np.uint8)
+    assert list(q[0]) == [0x7E, 0xFE, 0x7E, 0x7E]
+
+
+def test_dequant_is_decode_times_scale(oracle):
+    q = np.arange(256, dtype=np.uint8).view(np.int8).reshape(2, 128)
+    s = np.array([0.5, 3.0], np.float32)
+    out = oracle.dequantize_fp8(q, s, 2, 128, per_token=True)
+    table = oracle.e4m3_decode_table()
+    exp = np.stack([table[:128] * s[0], table[128:] * s[1]])
+    np.testing.assert_array_equal(np.isnan(out), np.isnan(exp))
+    ok = ~np.isnan(exp)
+    np.testing.assert_array_equal(out[ok], exp[ok])
+
+
+def test_smoothquant_reference_kat(oracle, golden):
+    """test_fp8_quant.cpp:99-135: 100/100 = 1 and 1/1 = 1."""
+    out = oracle.smoothquant_scale(golden["smooth_kat_x"], golden["smooth_kat_s"])
+    np.testing.assert_array_equal(out, golden["smooth_kat_expected"])
+
+
+def test_smoothquant_matches_numpy(oracle):
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((16, 100)).astype(np.float32)
+    s = rng.uniform(0.1, 10, 100).astype(np.float32)
+    np.testing.assert_array_equal(oracle.smoothquant_scale(x, s), x / s[None, :])
+
+
+# ---------------------------------------------------------------------------
+# Extensions: composition identities with the pinned functions
+# ---------------------------------------------------------------------------
+
+def test_fused_smooth_div_equals_two_step(oracle):
+    x, _ = outlier_activations(32, 1024, 0.005, 100.0, seed=4)
+    s = np.random.default_rng(5).uniform(0.5, 20.0, 1024).astype(np.float32)
+    q1, s1 = oracle.quantize_fp8_smooth_div(x, s)
+    q2, s2 = oracle.quantize_fp8_per_token(oracle.smoothquant_scale(x, s))
+    np.testing.assert_array_equal(q1, q2)
+    np.testing.assert_array_equal(s1, s2)
+    xb = f32_to_bf16_bits(x)
+    q3, s3 = oracle.quantize_fp8_smooth_div(xb, s)
+    q4, s4 = oracle.quantize_fp8_per_token(oracle.smoothquant_scale(bf16_bits_to_f32(xb), s))
+    np.testing.assert_array_equal(q3, q4)
+    np.testing.assert_array_equal(s3, s4)
+
+
+def test_fused_smooth_mul_equals_two_step(oracle):
+    wb = f32_to_bf16_bits((np.random.default_rng(6).standard_normal((64, 512)) * 0.02)
+                          .astype(np.float32))
+    s = np.random.default_rng(7).uniform(0.5, 20.0, 512).astype(np.float32)
+    q1, s1 = oracle.quantize_fp8_smooth_mul_bf16(wb, s)
+    q2, s2 = oracle.quantize_fp8_per_token(bf16_bits_to_f32(wb) * s[None, :])
+    np.testing.assert_array_equal(q1, q2)
+    np.testing.assert_array_equal(s1, s2)
+
+
+def test_bf16_per_token_equals_widened_fp32(oracle):
+    xb = f32_to_bf16_bits(np.random.default_rng(8).standard_normal((8, 300)).astype(np.float32))
+    q1, s1 = oracle.quantize_fp8_per_token_bf16(xb)
+    q2, s2 = oracle.quantize_fp8_per_token(bf16_bits_to_f32(xb))
+    np.testing.assert_array_equal(q1, q2)
+    np.testing.assert_array_equal(s1, s2)
+
+
+def test_col_absmax_and_smooth_factors(oracle):
+    x, ch = outlier_activations(64, 256, 0.02, 100.0, seed=10)
+    x[3, 7] = np.nan
+    amax = oracle.col_absmax(x)
+    np.testing.assert_array_equal(amax, np.nanmax(np.abs(x), axis=0))
+    xb = f32_to_bf16_bits(x)
+    np.testing.assert_array_equal(oracle.col_absmax(xb),
+                                  np.nanmax(np.abs(bf16_bits_to_f32(xb)), axis=0))
+    aw = np.abs(np.random.default_rng(11).standard_normal(256).astype(np.float32)) * 0.05
+    aw[0] = 0.0
+    s = oracle.smooth_factors(amax, aw)
+    exp = np.maximum(np.sqrt(amax) / np.sqrt(np.maximum(aw, np.float32(1e-5))), np.float32(1e-5))
+    np.testing.assert_array_equal(s, exp.astype(np.float32))
+    assert np.all(s[ch] > np.median(s))          # outlier channels get the large factors
+
+
+def test_bf16_rounding_helpers(oracle):
+    vals = np.array([1.0, 1.00390625, 1.0117188, -3.3e38, 1e-40, np.inf], np.float32)
+    bits = f32_to_bf16_bits(vals)
+    for v, b in zip(vals, bits):
+        assert oracle.lib().kco_f32_to_bf16(float(v)) == int(b)
+    ref = torch.from_numpy(vals).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(bits, ref)
