@@ -31,6 +31,19 @@ constexpr float kE4M3Max = 448.0f;  // fp8_quant.cu:31
 
 __device__ __forceinline__ float clamp448(float v) { return fmaxf(-kE4M3Max, fminf(kE4M3Max, v)); }
 
+// Every input element is quieted once as it is loaded (v_max_f32 x, x in IEEE
+// mode; any other value, -0 and denormals included, is unchanged).  gfx950's
+// division sequence passes a signaling NaN through unquieted, and the
+// IEEE-mode v_min/v_max of the clamp then return NaN instead of the bound;
+// CUDA's fminf/fmaxf (fp8_quant.cu:127) return the bound, +448, for every NaN.
+// LLVM cannot drop the canonicalize of a loaded value, and treats its result
+// as quiet from there on.
+__device__ __forceinline__ float quiet(float x) { return __builtin_canonicalizef(x); }
+
+__device__ __forceinline__ f32x4 quiet4(f32x4 v) {
+    return f32x4{quiet(v.x), quiet(v.y), quiet(v.z), quiet(v.w)};
+}
+
 // 4 fp32 -> 4 E4M3 codes, byte i of the result holds input i.
 __device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
     int v = __builtin_amdgcn_cvt_pk_fp8_f32(clamp448(a), clamp448(b), 0, false);
@@ -72,7 +85,7 @@ __device__ __forceinline__ f32x4 apply_smooth(f32x4 v, const float* __restrict__
     if constexpr (S == Smooth::kNone) {
         return v;
     } else {
-        const f32x4 f = *reinterpret_cast<const f32x4*>(s + col);
+        const f32x4 f = quiet4(*reinterpret_cast<const f32x4*>(s + col));
         if constexpr (S == Smooth::kDiv)
             return f32x4{v.x / f.x, v.y / f.y, v.z / f.z, v.w / f.w};  // fp8_quant.cu:183
         else
@@ -101,7 +114,8 @@ __global__ __launch_bounds__(kThreads) void quant_rows_f32_kernel(
     for (int j = 0; j < NV; ++j) {
         const int i = threadIdx.x + j * kThreads;
         if (i < n4) {
-            v[j] = apply_smooth<S>(__builtin_nontemporal_load(src + i), smooth, 4 * int64_t{i});
+            v[j] = apply_smooth<S>(quiet4(__builtin_nontemporal_load(src + i)), smooth,
+                                   4 * int64_t{i});
             m = absmax4(m, v[j]);
         }
     }
@@ -134,8 +148,8 @@ __global__ __launch_bounds__(kThreads) void quant_rows_bf16_kernel(
         const int i = threadIdx.x + j * kThreads;
         if (i < n8) {
             const u32x4 d = __builtin_nontemporal_load(src + i);
-            lo[j] = apply_smooth<S>(bf16x4_to_f32(d.x, d.y), smooth, 8 * int64_t{i});
-            hi[j] = apply_smooth<S>(bf16x4_to_f32(d.z, d.w), smooth, 8 * int64_t{i} + 4);
+            lo[j] = apply_smooth<S>(quiet4(bf16x4_to_f32(d.x, d.y)), smooth, 8 * int64_t{i});
+            hi[j] = apply_smooth<S>(quiet4(bf16x4_to_f32(d.z, d.w)), smooth, 8 * int64_t{i} + 4);
             m = absmax4(absmax4(m, lo[j]), hi[j]);
         }
     }
@@ -164,8 +178,9 @@ __device__ __forceinline__ float load_elem(const void* in, const float* smooth, 
     float v;
     if constexpr (BF16) v = kc::bf16_to_f32(static_cast<const uint16_t*>(in)[row * cols + c]);
     else v = static_cast<const float*>(in)[row * cols + c];
-    if constexpr (S == Smooth::kDiv) v = v / smooth[c];
-    if constexpr (S == Smooth::kMul) v = v * smooth[c];
+    v = quiet(v);
+    if constexpr (S == Smooth::kDiv) v = v / quiet(smooth[c]);
+    if constexpr (S == Smooth::kMul) v = v * quiet(smooth[c]);
     return v;
 }
 
@@ -193,7 +208,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_generic_kernel(
 __global__ __launch_bounds__(kThreads) void quant_tensor_f32_kernel(
     const float* __restrict__ in, const float* __restrict__ d_scale, int8_t* __restrict__ out,
     int64_t count, bool vec) {
-    const float scale = *d_scale;
+    const float scale = quiet(*d_scale);
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
     const int64_t tid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
     int64_t done = 0;
@@ -202,14 +217,14 @@ __global__ __launch_bounds__(kThreads) void quant_tensor_f32_kernel(
         const f32x4* src = reinterpret_cast<const f32x4*>(in);
         uint32_t* dst = reinterpret_cast<uint32_t*>(out);
         for (int64_t i = tid; i < n4; i += stride) {
-            const f32x4 q = __builtin_nontemporal_load(src + i);
+            const f32x4 q = quiet4(__builtin_nontemporal_load(src + i));
             __builtin_nontemporal_store(e4m3x4(q.x / scale, q.y / scale, q.z / scale, q.w / scale),
                                         dst + i);
         }
         done = n4 << 2;
     }
     for (int64_t i = done + tid; i < count; i += stride)
-        out[i] = static_cast<int8_t>(e4m3x1(in[i] / scale));
+        out[i] = static_cast<int8_t>(e4m3x1(quiet(in[i]) / scale));
 }
 
 // ---------------------------------------------------------------------------

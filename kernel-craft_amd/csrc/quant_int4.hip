@@ -35,7 +35,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;                    // 4 waves per workgroup
 constexpr int kWavesPerBlock = kThreads / kWave;
-constexpr int kMaxLdsBytes = 64 * 1024;
 
 __device__ __forceinline__ int sext4(uint32_t v) { return static_cast<int>(v << 28) >> 28; }
 
@@ -94,16 +93,18 @@ __global__ __launch_bounds__(kThreads) void gemv_int4_generic_kernel(
 // ---------------------------------------------------------------------------
 // Fast GEMV.
 //
-// LDS holds x for the whole K, split into chunks of 32 k.  A chunk is Q
-// 16-byte quads (Q = 4 for bf16, 8 for fp32); quad q of chunk c lives at
-// xq[q * cpr + c], so the 64 lanes of a wave, which work on 64 consecutive
-// chunks, read 64 consecutive quads (conflict-free ds_read_b128).  For bf16
-// the quad of k-block i (k = 8i..8i+7 of the chunk) stores the pairs
-// (x0,x4) (x1,x5) (x2,x6) (x3,x7), the order in which the nibble unpack
-// below produces weights.  xs[c] is the fp32 sum of the chunk's 32 x.
-//
-// Each wave owns R consecutive rows and walks their chunks c = lane,
-// lane + 64, ... with one 16-byte load per row per step.
+// A row is split into chunks of 32 k (16 bytes of packed weights).  One
+// workgroup computes R consecutive rows; its W waves split K, wave w owning
+// chunks [w*64*CPL, (w+1)*64*CPL) of every row and lane l the chunks
+// w*64*CPL + 64*j + l (j < CPL), so each wave-wide load reads 1 KB of one
+// row.  Every weight load of the workgroup is issued up front.  The lane's x
+// for its chunks is loaded once into registers: for bf16 the quad of k-block
+// i (k = 8i..8i+7 of a chunk) is rearranged into the pairs (x0,x4) (x1,x5)
+// (x2,x6) (x3,x7), the order in which the nibble unpack produces weights;
+// xs is the chunk's fp32 sum of x.  Partial sums are reduced across the wave
+// with a transposed butterfly (R values in log2(64) + R - 1 shuffles) and
+// across the W waves through LDS in a fixed order, so results do not depend
+// on scheduling.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t nib_bf16_pair(uint32_t d) {
     // nibbles at bits 0-3 and 16-19 -> bf16 (128 + (q ^ 8)) in each half
@@ -126,8 +127,7 @@ __device__ __forceinline__ float dot8_bf16(uint32_t d, uint32_t x04, uint32_t x1
     return a;
 }
 
-__device__ __forceinline__ float dot8_f32(uint32_t d, f32x4 xa, f32x4 xb,
-                                          float a) {
+__device__ __forceinline__ float dot8_f32(uint32_t d, f32x4 xa, f32x4 xb, float a) {
     const uint32_t o = d ^ 0x88888888u;  // n' = q ^ 8 in every nibble
     const uint32_t L = o & 0x0F0F0F0Fu;  // even k of each byte
     const uint32_t H = (o >> 4) & 0x0F0F0F0Fu;  // odd k
@@ -142,119 +142,180 @@ __device__ __forceinline__ float dot8_f32(uint32_t d, f32x4 xa, f32x4 xb,
     return a;
 }
 
-__device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
+// The lane's x for one chunk: bf16 as 4 quads of pairs, fp32 as 8 quads.
+template <bool XBF16>
+struct XChunk {
+    u32x4 q[XBF16 ? 4 : 8];
+    float sum;
+};
 
 template <bool XBF16>
-__device__ __forceinline__ void stage_x(const void* __restrict__ x, u32x4* xq, float* xs,
-                                        int cols) {
-    const int cpr = cols >> 5;
-    const int nblk = cols >> 3;  // multiple of 4, so a chunk's 4 blocks share a quad of lanes
-    for (int b = threadIdx.x; b < nblk; b += kThreads) {
-        const int c = b >> 2, i = b & 3;
-        float part;
-        if constexpr (XBF16) {
-            const u32x4 d = static_cast<const u32x4*>(x)[b];
+__device__ __forceinline__ XChunk<XBF16> load_x_chunk(const void* __restrict__ x, int c) {
+    XChunk<XBF16> xc;
+    if constexpr (XBF16) {
+        const u32x4* src = static_cast<const u32x4*>(x) + 4 * c;
+        const bf16x2_t ones = as_bf16x2(0x3F803F80u);
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4 d = src[i];
+            const uint32_t d0 = d.x, d1 = d.y, d2 = d.z, d3 = d.w;
             u32x4 p;
-            p.x = (d.x & 0xFFFFu) | (d.z << 16);
-            p.y = (d.x >> 16) | (d.z & 0xFFFF0000u);
-            p.z = (d.y & 0xFFFFu) | (d.w << 16);
-            p.w = (d.y >> 16) | (d.w & 0xFFFF0000u);
-            xq[i * cpr + c] = p;
-            part = ((bf16_lo(d.x) + bf16_hi(d.x)) + (bf16_lo(d.y) + bf16_hi(d.y))) +
-                   ((bf16_lo(d.z) + bf16_hi(d.z)) + (bf16_lo(d.w) + bf16_hi(d.w)));
-        } else {
-            const f32x4* src = static_cast<const f32x4*>(x) + 2 * b;
-            const f32x4 a = src[0], e = src[1];
-            xq[(2 * i) * cpr + c] = __builtin_bit_cast(u32x4, a);
-            xq[(2 * i + 1) * cpr + c] = __builtin_bit_cast(u32x4, e);
-            part = ((a.x + a.y) + (a.z + a.w)) + ((e.x + e.y) + (e.z + e.w));
+            p.x = (d0 & 0xFFFFu) | (d2 << 16);
+            p.y = (d0 >> 16) | (d2 & 0xFFFF0000u);
+            p.z = (d1 & 0xFFFFu) | (d3 << 16);
+            p.w = (d1 >> 16) | (d3 & 0xFFFF0000u);
+            xc.q[i] = p;
+            sum = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d0), ones, sum, false);
+            sum = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d1), ones, sum, false);
+            sum = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d2), ones, sum, false);
+            sum = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d3), ones, sum, false);
         }
-        part += __shfl_xor(part, 1, kWave);
-        part += __shfl_xor(part, 2, kWave);
-        if (i == 0) xs[c] = part;
+        xc.sum = sum;
+    } else {
+        const f32x4* src = static_cast<const f32x4*>(x) + 8 * c;
+        float part[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const f32x4 v = src[i];
+            xc.q[i] = __builtin_bit_cast(u32x4, v);
+            part[i] = (v.x + v.y) + (v.z + v.w);
+        }
+        xc.sum = ((part[0] + part[1]) + (part[2] + part[3])) +
+                 ((part[4] + part[5]) + (part[6] + part[7]));
+    }
+    return xc;
+}
+
+template <bool XBF16>
+__device__ __forceinline__ float chunk_dot(const u32x4 w, const XChunk<XBF16>& xc) {
+    const uint32_t w0 = w.x, w1 = w.y, w2 = w.z, w3 = w.w;
+    if constexpr (XBF16) {
+        const u32x4 a0 = xc.q[0], a1 = xc.q[1], a2 = xc.q[2], a3 = xc.q[3];
+        float a = dot8_bf16(w0, a0.x, a0.y, a0.z, a0.w, 0.0f);
+        a = dot8_bf16(w1, a1.x, a1.y, a1.z, a1.w, a);
+        a = dot8_bf16(w2, a2.x, a2.y, a2.z, a2.w, a);
+        return dot8_bf16(w3, a3.x, a3.y, a3.z, a3.w, a);
+    } else {
+        float a = dot8_f32(w0, __builtin_bit_cast(f32x4, xc.q[0]), __builtin_bit_cast(f32x4, xc.q[1]), 0.0f);
+        a = dot8_f32(w1, __builtin_bit_cast(f32x4, xc.q[2]), __builtin_bit_cast(f32x4, xc.q[3]), a);
+        a = dot8_f32(w2, __builtin_bit_cast(f32x4, xc.q[4]), __builtin_bit_cast(f32x4, xc.q[5]), a);
+        return dot8_f32(w3, __builtin_bit_cast(f32x4, xc.q[6]), __builtin_bit_cast(f32x4, xc.q[7]), a);
     }
 }
 
-template <int R, bool XBF16, bool YBF16>
-__global__ __launch_bounds__(kThreads) void gemv_int4_fast_kernel(
+// v + v of lane (lane ^ m): ds_swizzle (bit-mask mode) within 32 lanes,
+// ds_bpermute across the halves.
+__device__ __forceinline__ float xor_shuffle(float v, int m) {
+    switch (m) {
+        case 1: return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x041F));
+        case 2: return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x081F));
+        case 4: return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x101F));
+        case 8: return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x201F));
+        case 16: return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+        default: return __shfl_xor(v, 32, kWave);
+    }
+}
+
+// Sums v[r] over the wave for R rows.  Afterwards lane (64/R)*r holds the
+// total of row r (the other lanes of its group hold it too).
+template <int R>
+__device__ __forceinline__ float wave_reduce_rows(float (&v)[R], int lane) {
+    int n = R;
+    int m = 32;
+#pragma unroll
+    for (int step = 0; step < 3; ++step) {
+        if (n > 1) {
+            const bool upper = (lane & m) != 0;
+            const int h = n >> 1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (i < h) {
+                    const float send = upper ? v[i] : v[i + h];
+                    const float keep = upper ? v[i + h] : v[i];
+                    v[i] = keep + xor_shuffle(send, m);
+                }
+            }
+            n = h;
+            m >>= 1;
+        }
+    }
+    float t = v[0];
+#pragma unroll
+    for (int mm = 32; mm >= 1; mm >>= 1)
+        if (mm <= m) t += xor_shuffle(t, mm);
+    return t;
+}
+
+constexpr int kMaxWaves = 16;
+
+template <int R, int CPL, bool XBF16, bool YBF16>
+__global__ __launch_bounds__(kMaxWaves * kWave) void gemv_int4_fast_kernel(
     const uint8_t* __restrict__ packed, const float* __restrict__ scales,
     const uint8_t* __restrict__ zeros, const void* __restrict__ x, void* __restrict__ y,
     int rows, int cols, int gshift) {
-    extern __shared__ u32x4 lds[];
-    constexpr int Q = XBF16 ? 4 : 8;
-    const int cpr = cols >> 5;
-    u32x4* xq = lds;
-    float* xs = reinterpret_cast<float*>(lds + Q * cpr);
-    stage_x<XBF16>(x, xq, xs, cols);
-    __syncthreads();
-
+    __shared__ float red[kMaxWaves][R];
     const int lane = threadIdx.x & (kWave - 1);
-    const int row0 = (blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6)) * R;
-    if (row0 >= rows) return;
-    const int64_t rbytes = cols >> 1;
+    const int wave = threadIdx.x >> 6;
+    const int nwaves = blockDim.x >> 6;
+    const int cpr = cols >> 5;
     const int G = cols >> (5 + gshift);
-    const u32x4* prow[R];
-    const float* srow[R];
-    const uint8_t* zrow[R];
+    const int64_t rbytes = cols >> 1;
+    const int row0 = blockIdx.x * R;
+
+    int cidx[CPL];
+    bool act[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c = (wave * CPL + j) * kWave + lane;
+        act[j] = c < cpr;
+        cidx[j] = act[j] ? c : 0;
+    }
+    // weights, scales and zero bytes of every row first: they are the HBM stream
+    u32x4 w[R][CPL];
+    float s[R][CPL];
+    uint32_t zb[R][CPL];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int64_t rr = min(row0 + r, rows - 1);  // tail rows re-read the last row
-        prow[r] = reinterpret_cast<const u32x4*>(packed + rr * rbytes);
-        srow[r] = scales + rr * G;
-        zrow[r] = zeros + rr * (G >> 1);
+        const u32x4* prow = reinterpret_cast<const u32x4*>(packed + rr * rbytes);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) w[r][j] = __builtin_nontemporal_load(prow + cidx[j]);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t rr = min(row0 + r, rows - 1);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int g = cidx[j] >> gshift;
+            s[r][j] = act[j] ? scales[rr * G + g] : 0.0f;
+            zb[r][j] = zeros[rr * (G >> 1) + (g >> 1)];
+        }
     }
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-
-    for (int c = lane; c < cpr; c += kWave) {
-        const int g = c >> gshift;
-        u32x4 w[R];
-        float s[R];
-        uint32_t zb[R];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const XChunk<XBF16> xc = load_x_chunk<XBF16>(x, cidx[j]);
+        const uint32_t godd = (cidx[j] >> gshift) & 1u;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            w[r] = __builtin_nontemporal_load(prow[r] + c);
-            s[r] = srow[r][g];
-            zb[r] = zrow[r][g >> 1];
-        }
-        const float xsum = xs[c];
-        if constexpr (XBF16) {
-            const u32x4 x0 = xq[c], x1 = xq[cpr + c], x2 = xq[2 * cpr + c], x3 = xq[3 * cpr + c];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const uint32_t z = (g & 1) ? (zb[r] >> 4) : (zb[r] & 0xFu);
-                const u32x4 wr = w[r];
-                float a = dot8_bf16(wr.x, x0.x, x0.y, x0.z, x0.w, 0.0f);
-                a = dot8_bf16(wr.y, x1.x, x1.y, x1.z, x1.w, a);
-                a = dot8_bf16(wr.z, x2.x, x2.y, x2.z, x2.w, a);
-                a = dot8_bf16(wr.w, x3.x, x3.y, x3.z, x3.w, a);
-                acc[r] = fmaf(s[r], fmaf(-static_cast<float>(136u + z), xsum, a), acc[r]);
-            }
-        } else {
-            f32x4 xf[8];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const u32x4 v = xq[q * cpr + c];
-                xf[q] = __builtin_bit_cast(f32x4, v);
-            }
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const uint32_t z = (g & 1) ? (zb[r] >> 4) : (zb[r] & 0xFu);
-                const u32x4 wr = w[r];
-                float a = dot8_f32(wr.x, xf[0], xf[1], 0.0f);
-                a = dot8_f32(wr.y, xf[2], xf[3], a);
-                a = dot8_f32(wr.z, xf[4], xf[5], a);
-                a = dot8_f32(wr.w, xf[6], xf[7], a);
-                acc[r] = fmaf(s[r], fmaf(-static_cast<float>(8u + z), xsum, a), acc[r]);
-            }
+            const uint32_t z = godd ? (zb[r][j] >> 4) : (zb[r][j] & 0xFu);
+            const float off = static_cast<float>((XBF16 ? 136u : 8u) + z);
+            const float part = fmaf(s[r][j], fmaf(-off, xc.sum, chunk_dot<XBF16>(w[r][j], xc)), acc[r]);
+            acc[r] = act[j] ? part : acc[r];
         }
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const float v = kc::wave_sum(acc[r]);
-        if (lane == 0 && row0 + r < rows) store_y<YBF16>(y, row0 + r, v);
+    const float t = wave_reduce_rows<R>(acc, lane);
+    constexpr int kGroup = kWave / R;
+    if ((lane & (kGroup - 1)) == 0) red[wave][lane / kGroup] = t;
+    __syncthreads();
+    if (threadIdx.x < R) {
+        float tot = red[0][threadIdx.x];
+        for (int wv = 1; wv < nwaves; ++wv) tot += red[wv][threadIdx.x];
+        if (row0 + static_cast<int>(threadIdx.x) < rows)
+            store_y<YBF16>(y, row0 + threadIdx.x, tot);
     }
 }
 
@@ -340,21 +401,50 @@ int check_int4_args(const char* fn, const void* packed, const void* scales, cons
     return KC_SUCCESS;
 }
 
-int rows_per_wave_override() {
+int rows_per_block_override() {
     static const int v = [] {
-        const char* e = getenv("KC_GEMV_ROWS_PER_WAVE");
+        const char* e = getenv("KC_GEMV_ROWS_PER_BLOCK");
         return e ? atoi(e) : 0;
     }();
     return v;
 }
 
-template <int R, bool XB, bool YB>
+// Rows per workgroup: enough workgroups to give every CU several waves, and
+// as many rows as that allows so x (loaded once per workgroup) is reused.
+int pick_rows_per_block(int64_t rows, int waves_per_block) {
+    const int o = rows_per_block_override();
+    if (o == 1 || o == 2 || o == 4 || o == 8) return o;
+    const int64_t target_waves = 256 * 24;  // CUs x resident waves per CU
+    for (int R : {8, 4, 2}) {
+        if (((rows + R - 1) / R) * waves_per_block >= target_waves) return R;
+    }
+    return 1;
+}
+
+template <int R, int CPL, bool XB, bool YB>
 void launch_fast(const uint8_t* packed, const float* scales, const uint8_t* zeros, const void* x,
-                 void* y, int rows, int cols, int gshift, size_t lds, hipStream_t stream) {
-    const int per_block = kWavesPerBlock * R;
-    const unsigned grid = static_cast<unsigned>((rows + per_block - 1) / per_block);
-    gemv_int4_fast_kernel<R, XB, YB><<<grid, kThreads, lds, stream>>>(packed, scales, zeros, x, y,
-                                                                      rows, cols, gshift);
+                 void* y, int rows, int cols, int gshift, int waves, hipStream_t stream) {
+    const unsigned grid = static_cast<unsigned>((rows + R - 1) / R);
+    gemv_int4_fast_kernel<R, CPL, XB, YB><<<grid, waves * kWave, 0, stream>>>(
+        packed, scales, zeros, x, y, rows, cols, gshift);
+}
+
+// R * CPL is capped at 8 (the register file at 16 waves per workgroup).
+template <int CPL, bool XB, bool YB>
+void launch_fast_r(int R, const uint8_t* packed, const float* scales, const uint8_t* zeros,
+                   const void* x, void* y, int rows, int cols, int gshift, int waves,
+                   hipStream_t stream) {
+    R = std::min(R, 8 / CPL);
+    if constexpr (CPL == 1) {
+        if (R == 8) return launch_fast<8, 1, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, waves, stream);
+    }
+    if constexpr (CPL <= 2) {
+        if (R == 4) return launch_fast<4, CPL, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, waves, stream);
+    }
+    if constexpr (CPL <= 4) {
+        if (R == 2) return launch_fast<2, CPL, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, waves, stream);
+    }
+    launch_fast<1, CPL, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, waves, stream);
 }
 
 template <bool XB, bool YB>
@@ -364,20 +454,24 @@ int gemv_int4(const char* fn, const uint8_t* packed, const float* scales, const 
     int st = check_int4_args(fn, packed, scales, zeros, x, y, rows, cols, gs);
     if (st != KC_SUCCESS) return st;
     if (rows == 0) return KC_SUCCESS;
-    const size_t lds =
-        static_cast<size_t>(cols >> 5) * ((XB ? 4 : 8) * 16 + 4);
-    const bool fast = cols > 0 && gs >= 32 && kc::is_pow2(gs) && lds <= kMaxLdsBytes &&
+    const int64_t cpr = cols >> 5;
+    // chunks per lane per row: the smallest of 1, 2, 4, 8 that needs <= 16 waves
+    int cpl = 0;
+    for (int c : {1, 2, 4, 8}) {
+        if ((cpr + 64 * c - 1) / (64 * c) <= kMaxWaves) { cpl = c; break; }
+    }
+    const bool fast = cols > 0 && gs >= 32 && kc::is_pow2(gs) && cpl > 0 &&
                       rows <= INT32_MAX && kc::aligned(packed, 16) && kc::aligned(x, 16);
     if (fast) {
         const int gshift = kc::ilog2(gs) - 5;
-        int R = rows_per_wave_override();
-        if (R != 1 && R != 2 && R != 4 && R != 8) R = 4;
+        const int waves = static_cast<int>((cpr + 64 * cpl - 1) / (64 * cpl));
+        const int R = pick_rows_per_block(rows, waves);
         const int r = static_cast<int>(rows), c = static_cast<int>(cols);
-        switch (R) {
-            case 1: launch_fast<1, XB, YB>(packed, scales, zeros, x, y, r, c, gshift, lds, stream); break;
-            case 2: launch_fast<2, XB, YB>(packed, scales, zeros, x, y, r, c, gshift, lds, stream); break;
-            case 8: launch_fast<8, XB, YB>(packed, scales, zeros, x, y, r, c, gshift, lds, stream); break;
-            default: launch_fast<4, XB, YB>(packed, scales, zeros, x, y, r, c, gshift, lds, stream); break;
+        switch (cpl) {
+            case 1: launch_fast_r<1, XB, YB>(R, packed, scales, zeros, x, y, r, c, gshift, waves, stream); break;
+            case 2: launch_fast_r<2, XB, YB>(R, packed, scales, zeros, x, y, r, c, gshift, waves, stream); break;
+            case 4: launch_fast_r<4, XB, YB>(R, packed, scales, zeros, x, y, r, c, gshift, waves, stream); break;
+            default: launch_fast_r<8, XB, YB>(R, packed, scales, zeros, x, y, r, c, gshift, waves, stream); break;
         }
     } else {
         const int64_t grid = (rows + kWavesPerBlock - 1) / kWavesPerBlock;

@@ -37,6 +37,22 @@
 static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 
+/* CUDA's fmaxf/fminf (the reference's, fp8_quant.cu:105,127): a NaN operand,
+ * quiet or signaling, is ignored and the other operand returned.  glibc's
+ * fmaxf/fminf follow IEEE 754-2008 maxNum instead and return a quiet NaN for a
+ * signaling operand, so they are not used.  Signed zeros never meet here (the
+ * operands are |x| >= +0 or compared against +-448). */
+static inline float cu_fmaxf(float a, float b) {
+    if (isnan(a)) return b;
+    if (isnan(b)) return a;
+    return a > b ? a : b;
+}
+static inline float cu_fminf(float a, float b) {
+    if (isnan(a)) return b;
+    if (isnan(b)) return a;
+    return a < b ? a : b;
+}
+
 /* quant_int4.cu:34-48: bits 3:0 (or 7:4) sign-extended from 4 bits. */
 int kco_sext4(unsigned nibble) {
     nibble &= 0xFu;
@@ -93,7 +109,7 @@ uint16_t kco_f32_to_bf16(float f) {
 /* fp8_quant.cu:126-129: clamp to +-448 (fmaxf/fminf drop NaN in favour of the
  * bound, so NaN becomes +448), then convert. */
 static inline uint8_t clamp_encode(float q) {
-    q = fmaxf(-E4M3_MAX, fminf(E4M3_MAX, q));
+    q = cu_fmaxf(-E4M3_MAX, cu_fminf(E4M3_MAX, q));
     return kco_e4m3_encode(q);
 }
 
@@ -237,7 +253,7 @@ void kco_quantize_fp8_per_token(const float* in, int8_t* out, float* scales,
     for (int64_t r = 0; r < rows; ++r) {
         const float* x = in + r * cols;
         float amax = 0.0f;
-        for (int64_t c = 0; c < cols; ++c) amax = fmaxf(amax, fabsf(x[c]));
+        for (int64_t c = 0; c < cols; ++c) amax = cu_fmaxf(amax, fabsf(x[c]));
         float s = row_scale(amax);
         scales[r] = s;
         for (int64_t c = 0; c < cols; ++c)
@@ -280,7 +296,7 @@ void kco_quantize_fp8_per_token_bf16(const uint16_t* in, int8_t* out,
         const uint16_t* x = in + r * cols;
         float amax = 0.0f;
         for (int64_t c = 0; c < cols; ++c)
-            amax = fmaxf(amax, fabsf(kco_bf16_to_f32(x[c])));
+            amax = cu_fmaxf(amax, fabsf(kco_bf16_to_f32(x[c])));
         float s = row_scale(amax);
         scales[r] = s;
         for (int64_t c = 0; c < cols; ++c)
@@ -292,7 +308,7 @@ void kco_col_absmax_f32(const float* in, float* amax, int64_t rows, int64_t cols
     for (int64_t c = 0; c < cols; ++c) amax[c] = 0.0f;
     for (int64_t r = 0; r < rows; ++r)
         for (int64_t c = 0; c < cols; ++c)
-            amax[c] = fmaxf(amax[c], fabsf(in[r * cols + c]));
+            amax[c] = cu_fmaxf(amax[c], fabsf(in[r * cols + c]));
 }
 
 void kco_col_absmax_bf16(const uint16_t* in, float* amax, int64_t rows,
@@ -300,7 +316,7 @@ void kco_col_absmax_bf16(const uint16_t* in, float* amax, int64_t rows,
     for (int64_t c = 0; c < cols; ++c) amax[c] = 0.0f;
     for (int64_t r = 0; r < rows; ++r)
         for (int64_t c = 0; c < cols; ++c)
-            amax[c] = fmaxf(amax[c], fabsf(kco_bf16_to_f32(in[r * cols + c])));
+            amax[c] = cu_fmaxf(amax[c], fabsf(kco_bf16_to_f32(in[r * cols + c])));
 }
 
 /* SmoothQuant factor with alpha = 0.5 (Xiao et al. 2023, eq. 4):
@@ -310,8 +326,8 @@ void kco_col_absmax_bf16(const uint16_t* in, float* amax, int64_t rows,
 void kco_smooth_factors(const float* amax_x, const float* amax_w, float* s,
                         int64_t cols) {
     for (int64_t c = 0; c < cols; ++c) {
-        float v = sqrtf(amax_x[c]) / sqrtf(fmaxf(amax_w[c], 1e-5f));
-        s[c] = fmaxf(v, 1e-5f);
+        float v = sqrtf(amax_x[c]) / sqrtf(cu_fmaxf(amax_w[c], 1e-5f));
+        s[c] = cu_fmaxf(v, 1e-5f);
     }
 }
 
@@ -323,7 +339,7 @@ void kco_quantize_fp8_smooth_div_f32(const float* in, const float* s,
     for (int64_t r = 0; r < rows; ++r) {
         const float* x = in + r * cols;
         float amax = 0.0f;
-        for (int64_t c = 0; c < cols; ++c) amax = fmaxf(amax, fabsf(x[c] / s[c]));
+        for (int64_t c = 0; c < cols; ++c) amax = cu_fmaxf(amax, fabsf(x[c] / s[c]));
         float sc = row_scale(amax);
         scales[r] = sc;
         for (int64_t c = 0; c < cols; ++c)
@@ -338,7 +354,7 @@ void kco_quantize_fp8_smooth_div_bf16(const uint16_t* in, const float* s,
         const uint16_t* x = in + r * cols;
         float amax = 0.0f;
         for (int64_t c = 0; c < cols; ++c)
-            amax = fmaxf(amax, fabsf(kco_bf16_to_f32(x[c]) / s[c]));
+            amax = cu_fmaxf(amax, fabsf(kco_bf16_to_f32(x[c]) / s[c]));
         float sc = row_scale(amax);
         scales[r] = sc;
         for (int64_t c = 0; c < cols; ++c)
@@ -356,7 +372,7 @@ void kco_quantize_fp8_smooth_mul_bf16(const uint16_t* in, const float* s,
         const uint16_t* w = in + r * cols;
         float amax = 0.0f;
         for (int64_t c = 0; c < cols; ++c)
-            amax = fmaxf(amax, fabsf(kco_bf16_to_f32(w[c]) * s[c]));
+            amax = cu_fmaxf(amax, fabsf(kco_bf16_to_f32(w[c]) * s[c]));
         float sc = row_scale(amax);
         scales[r] = sc;
         for (int64_t c = 0; c < cols; ++c)

@@ -87,7 +87,7 @@ def test_per_token_shapes(gpu, oracle, rows, cols):
 
 def test_per_token_special_values(gpu, oracle):
     rng = np.random.default_rng(7)
-    x = rng.standard_normal((13, 256)).astype(np.float32)
+    x = rng.standard_normal((15, 256)).astype(np.float32)
     x[0] = 0.0                                   # all zero -> scale 1
     x[1] = -0.0                                  # -0 -> code 0x80
     x[2, ::7] = np.nan                           # NaN ignored by absmax, -> +448
@@ -103,6 +103,9 @@ def test_per_token_special_values(gpu, oracle):
     x[11] = np.float32(2.0) ** rng.integers(-20, 20, 256).astype(np.float32)
     x[12] = np.float32(1e-44) * np.sign(rng.standard_normal(256)).astype(np.float32)  # scale 0
     x[12, 3] = 0.0
+    snan = np.array([0x7F800001, 0x7FA00000, 0xFF800001, 0xFFBFFFFF], np.uint32).view(np.float32)
+    x[13, :4] = snan                             # signaling NaNs: ignored, -> +448
+    x[14, 10:14] = snan
     q, s = _per_token(gpu, x)
     eq, es = oracle.quantize_fp8_per_token(x)
     np.testing.assert_array_equal(s.view(np.uint32), es.view(np.uint32))
@@ -141,7 +144,8 @@ def test_reference_kats_roundtrip(gpu, golden):
         x = golden[name]
         q, s = _per_token(torch, x)
         out = torch.empty(*x.shape, dtype=torch.float32, device="cuda")
-        kc_abi.lib().launch_dequantize_fp8(ptr(_dev(torch, q)), ptr(_dev(torch, s)), ptr(out),
+        dq, ds = _dev(torch, q), _dev(torch, s)      # keep alive across the launch
+        kc_abi.lib().launch_dequantize_fp8(ptr(dq), ptr(ds), ptr(out),
                                            x.shape[0], x.shape[1], True, stream())
         kc_abi.check("launch_dequantize_fp8")
         xh = out.cpu().numpy()
@@ -214,8 +218,8 @@ def test_dequant_all_codes(gpu, oracle):
     s = np.array([1.0, 0.5, 3.7e-3, 1e30], np.float32)
     out = torch.empty(4, 512, dtype=torch.float32, device="cuda")
     L = kc_abi.lib()
-    L.launch_dequantize_fp8(ptr(_dev(torch, q)), ptr(_dev(torch, s)), ptr(out), 4, 512, True,
-                            stream())
+    dq, ds = _dev(torch, q), _dev(torch, s)
+    L.launch_dequantize_fp8(ptr(dq), ptr(ds), ptr(out), 4, 512, True, stream())
     kc_abi.check("launch_dequantize_fp8")
     got = out.cpu().numpy()
     exp = oracle.dequantize_fp8(q, s, 4, 512, True)
@@ -224,8 +228,8 @@ def test_dequant_all_codes(gpu, oracle):
     # per-tensor mode and ragged columns (generic tail)
     q2 = q.reshape(-1)[:3 * 7].reshape(3, 7)
     out2 = torch.empty(3, 7, dtype=torch.float32, device="cuda")
-    L.launch_dequantize_fp8(ptr(_dev(torch, q2)), ptr(_dev(torch, s)), ptr(out2), 3, 7, False,
-                            stream())
+    dq2 = _dev(torch, q2)
+    L.launch_dequantize_fp8(ptr(dq2), ptr(ds), ptr(out2), 3, 7, False, stream())
     kc_abi.check("launch_dequantize_fp8")
     exp2 = oracle.dequantize_fp8(q2, s, 3, 7, False)
     np.testing.assert_array_equal(out2.cpu().numpy(), exp2)
@@ -253,8 +257,8 @@ def test_smoothquant_scale_kat_and_random(gpu, oracle, golden):
                  (np.random.default_rng(3).standard_normal((5, 37)).astype(np.float32),
                   np.random.default_rng(4).uniform(0.1, 50, 37).astype(np.float32))]:
         out = torch.empty(*x.shape, dtype=torch.float32, device="cuda")
-        L.launch_smoothquant_scale(ptr(_dev(torch, x)), ptr(_dev(torch, s)), ptr(out),
-                                   x.shape[0], x.shape[1], stream())
+        dx, ds = _dev(torch, x), _dev(torch, s)
+        L.launch_smoothquant_scale(ptr(dx), ptr(ds), ptr(out), x.shape[0], x.shape[1], stream())
         kc_abi.check("launch_smoothquant_scale")
         np.testing.assert_array_equal(out.cpu().numpy(), oracle.smoothquant_scale(x, s))
 

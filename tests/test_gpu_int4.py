@@ -138,11 +138,14 @@ def test_gemv_sign_and_zero_point_invariants(gpu):
     rows, cols, gs = 64, 1024, 128
     x = np.random.default_rng(3).standard_normal(cols).astype(np.float32)
     G = cols // gs
-    # 0x33 with zero point 3 -> all weights 0 -> y == 0 exactly
+    # 0x33 with zero point 3 -> all weights 0 -> y == 0.  The fast path folds
+    # the zero point per 32-k chunk as s*(sum n'x - (8+z) sum x), so the two
+    # sums cancel to within fp32 rounding of s * 11 * sum|x| rather than to 0.
     y = _gemv_f32(gpu, np.full((rows, cols // 2), 0x33, np.uint8),
                   np.full((rows, G), 0.01, np.float32), np.full((rows, G // 2), 0x33, np.uint8),
                   x, rows, cols, gs)
-    assert np.all(y == 0.0)
+    scale = 0.01 * 11 * np.abs(x).sum()
+    assert np.all(np.abs(y) <= 1e-6 * scale)
     # 0x88 with zero point 8 -> every weight -16 * s (sign extension)
     y = _gemv_f32(gpu, np.full((rows, cols // 2), 0x88, np.uint8),
                   np.full((rows, G), 0.5, np.float32), np.full((rows, G // 2), 0x88, np.uint8),

@@ -348,6 +348,22 @@ def test_zero_rows_and_specials(oracle):
     assert q[3, 0].view(np.uint8) == oracle.e4m3_encode(np.float32(1.0) / s[3])
 
 
+def test_nan_follows_cuda_fmaxf_semantics(oracle):
+    """CUDA's fmaxf/fminf (fp8_quant.cu:105,127) ignore a NaN operand, quiet or
+    signaling: every one of the 2^24 - 2 NaN bit patterns clamps to +448, and
+    a signaling NaN never interrupts a row's absmax (glibc's maxNum would turn
+    it into a quiet NaN and restart the maximum after it)."""
+    for start in (0x7F800001, 0xFF800001):
+        n = 0x7FFFFF
+        bad, first = oracle.sweep_mismatches(start, np.full(n, 0x7E, np.uint8))
+        assert bad == 0, hex(first)
+    snan = np.array([0x7F800001], np.uint32).view(np.float32)[0]
+    x = np.array([[3.0, 1.0, snan, 2.0], [snan, snan, snan, snan]], np.float32)
+    q, s = oracle.quantize_fp8_per_token(x)
+    assert s[0] == np.float32(3.0) / np.float32(448.0) and s[1] == 1.0
+    assert q[0, 2].view(np.uint8) == 0x7E and np.all(q[1].view(np.uint8) == 0x7E)
+
+
 def test_per_tensor_zero_scale_saturates(oracle):
     """Via ctypes the reference passes scale 0 (kernel_craft_torch_ops.py:347):
     x/0 is +-inf (or NaN for 0/0), clamped to +-448 (or +448)."""
