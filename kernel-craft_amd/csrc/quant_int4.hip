@@ -204,64 +204,181 @@ __device__ __forceinline__ float chunk_dot(const u32x4 w, const XChunk<XBF16>& x
     }
 }
 
-// v + v of lane (lane ^ m): ds_swizzle (bit-mask mode) within 32 lanes,
-// ds_bpermute across the halves.
-__device__ __forceinline__ float xor_shuffle(float v, int m) {
-    switch (m) {
-        case 1: return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x041F));
-        case 2: return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x081F));
-        case 4: return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x101F));
-        case 8: return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x201F));
-        case 16: return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-        default: return __shfl_xor(v, 32, kWave);
+// Cross-lane steps, all VALU (no LDS round trip):
+//   permlane32_swap(a, b) -> ([a 0-31, b 0-31], [a 32-63, b 32-63])
+//   permlane16_swap(a, b) -> per 32-lane half, ([a 0-15, b 0-15], [a 16-31, b 16-31])
+//   row_ror:n             -> lane i of each 16-lane row reads lane (i - n) mod 16
+__device__ __forceinline__ float ror16(float v, int n) {
+    const int iv = __builtin_bit_cast(int, v);
+    switch (n) {
+        case 8: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x128, 0xF, 0xF, false));
+        case 4: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x124, 0xF, 0xF, false));
+        case 2: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x122, 0xF, 0xF, false));
+        default: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x121, 0xF, 0xF, false));
     }
 }
 
+// The swap builtins return a two-element vector; its elements are copied to
+// scalars before __builtin_bit_cast, which reads element 0 for any element of
+// a vector it is applied to directly (the same clang defect as above).
+__device__ __forceinline__ float sum_swap32(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, a),
+                                                    __builtin_bit_cast(unsigned, b), false, false);
+    const unsigned r0 = r[0], r1 = r[1];
+    return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+}
+
+__device__ __forceinline__ float sum_swap16(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, a),
+                                                    __builtin_bit_cast(unsigned, b), false, false);
+    const unsigned r0 = r[0], r1 = r[1];
+    return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+}
+
+__device__ __forceinline__ float sum_row16(float t) {
+    t += ror16(t, 8);
+    t += ror16(t, 4);
+    t += ror16(t, 2);
+    return t + ror16(t, 1);
+}
+
 // Sums v[r] over the wave for R rows.  Afterwards lane (64/R)*r holds the
-// total of row r (the other lanes of its group hold it too).
+// total of row r (so do the other lanes of its group of 64/R).
 template <int R>
-__device__ __forceinline__ float wave_reduce_rows(float (&v)[R], int lane) {
-    int n = R;
-    int m = 32;
-#pragma unroll
-    for (int step = 0; step < 3; ++step) {
-        if (n > 1) {
-            const bool upper = (lane & m) != 0;
-            const int h = n >> 1;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (i < h) {
-                    const float send = upper ? v[i] : v[i + h];
-                    const float keep = upper ? v[i + h] : v[i];
-                    v[i] = keep + xor_shuffle(send, m);
-                }
-            }
-            n = h;
-            m >>= 1;
-        }
+__device__ __forceinline__ float wave_reduce_rows(float (&v)[R], int /*lane*/) {
+    static_assert(R == 1 || R == 2 || R == 4, "rows per block");
+    if constexpr (R == 4) {
+        const float a = sum_swap32(v[0], v[2]);  // lanes 0-31: row 0, 32-63: row 2
+        const float b = sum_swap32(v[1], v[3]);  // lanes 0-31: row 1, 32-63: row 3
+        return sum_row16(sum_swap16(a, b));     // rows 0, 1, 2, 3 in 16-lane rows
+    } else if constexpr (R == 2) {
+        const float t = sum_row16(sum_swap32(v[0], v[1]));  // halves: row 0, row 1
+        return sum_swap16(t, t);
+    } else {
+        const float t = sum_row16(v[0]);
+        const float u = sum_swap32(t, t);
+        return sum_swap16(u, u);
     }
-    float t = v[0];
-#pragma unroll
-    for (int mm = 32; mm >= 1; mm >>= 1)
-        if (mm <= m) t += xor_shuffle(t, mm);
-    return t;
 }
 
 constexpr int kMaxWaves = 16;
 
+// Per row block, a lane needs for each of its CPL chunks and R rows the
+// group's scale s and zero point z, folded as
+//     acc += c1 * dot + c2 * sum(x),   c1 = s,  c2 = -s * (off + z)
+// (off = 136 for the bf16 encoding 128 + (q ^ 8), 8 for fp32).  A wave's
+// chunk slot j spans NG = max(1, 64 * 32 / gs) groups of a row, so the
+// CPL * R * NG (<= 64) distinct (s, z) of a row block arrive with one
+// coalesced scale load and one zero-byte load, lane i holding item
+// i = (j * R + r) * NG + gi; every lane then picks up its own c1, c2 with
+// ds_bpermute.
+template <int R, int CPL>
+struct RowBlock {
+    u32x4 w[R][CPL];
+    float s;       // item scale
+    uint32_t zb;   // item zero byte
+};
+
+struct SzLayout {
+    int ng;        // groups per chunk slot
+    int gshift;    // log2(gs / 32)
+    int G;         // groups per row
+    int items;     // CPL * R * ng
+};
+
+template <int R, int CPL>
+__device__ __forceinline__ void load_row_block(RowBlock<R, CPL>& b, const uint8_t* __restrict__ packed,
+                                               const float* __restrict__ scales,
+                                               const uint8_t* __restrict__ zeros, int row0, int rows,
+                                               int64_t rbytes, const int (&cidx)[CPL],
+                                               const SzLayout& L, int wave, int lane) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t rr = min(row0 + r, rows - 1);  // tail rows re-read the last row
+        const u32x4* prow = reinterpret_cast<const u32x4*>(packed + rr * rbytes);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) b.w[r][j] = __builtin_nontemporal_load(prow + cidx[j]);
+    }
+    // item owned by this lane (lanes past `items` repeat item 0)
+    const int item = lane < L.items ? lane : 0;
+    const int gi = item % L.ng;
+    const int jr = item / L.ng;
+    const int r = jr % R, j = jr / R;
+    const int gbase = ((wave * CPL + j) * kWave) >> L.gshift;
+    const int g = min(gbase + gi, L.G - 1);
+    const int64_t rr = min(row0 + r, rows - 1);
+    b.s = scales[rr * L.G + g];
+    b.zb = zeros[rr * (L.G >> 1) + (g >> 1)];
+}
+
+// Dot products of one row block, reduced over the wave and the workgroup,
+// stored to y.  `red` is this iteration's half of the LDS exchange buffer.
 template <int R, int CPL, bool XBF16, bool YBF16>
-__global__ __launch_bounds__(kMaxWaves * kWave) void gemv_int4_fast_kernel(
+__device__ __forceinline__ void finish_row_block(const RowBlock<R, CPL>& b,
+                                                 const XChunk<XBF16> (&xc)[CPL],
+                                                 const bool (&act)[CPL], const SzLayout& L,
+                                                 float (*red)[R], int row0, int rows, void* y,
+                                                 int lane, int wave, int nwaves) {
+    // this lane's item -> c1, c2
+    const int item = lane < L.items ? lane : 0;
+    const int g = min(((((item / L.ng) / R) * kWave + wave * CPL * kWave) >> L.gshift) + item % L.ng,
+                      L.G - 1);
+    const uint32_t z = (g & 1) ? (b.zb >> 4) : (b.zb & 0xFu);
+    const float c1 = b.s;
+    const float c2 = -b.s * static_cast<float>((XBF16 ? 136u : 8u) + z);
+    const int gsub = L.ng > 1 ? (lane >> L.gshift) : 0;  // group of my chunk within its slot
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int src = ((j * R + r) * L.ng + gsub) << 2;
+            float m1 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, c1)));
+            float m2 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, c2)));
+            m1 = act[j] ? m1 : 0.0f;
+            m2 = act[j] ? m2 : 0.0f;
+            acc[r] = fmaf(m1, chunk_dot<XBF16>(b.w[r][j], xc[j]), fmaf(m2, xc[j].sum, acc[r]));
+        }
+    }
+    const float t = wave_reduce_rows<R>(acc, lane);
+    constexpr int kGroup = kWave / R;
+    if (nwaves == 1) {
+        const int r = lane / kGroup;
+        if ((lane & (kGroup - 1)) == 0 && row0 + r < rows) store_y<YBF16>(y, row0 + r, t);
+        return;
+    }
+    if ((lane & (kGroup - 1)) == 0) red[wave][lane / kGroup] = t;
+    __syncthreads();
+    if (threadIdx.x < R) {
+        float tot = red[0][threadIdx.x];
+        for (int wv = 1; wv < nwaves; ++wv) tot += red[wv][threadIdx.x];
+        if (row0 + static_cast<int>(threadIdx.x) < rows)
+            store_y<YBF16>(y, row0 + threadIdx.x, tot);
+    }
+}
+
+// Persistent: workgroup b computes row blocks b, b + gridDim.x, ...; the next
+// block's weights are in flight while the current block is reduced.
+template <int R, int CPL, bool XBF16, bool YBF16>
+__global__ __launch_bounds__(CPL == 1 ? kMaxWaves * kWave : kWave) void gemv_int4_fast_kernel(
     const uint8_t* __restrict__ packed, const float* __restrict__ scales,
     const uint8_t* __restrict__ zeros, const void* __restrict__ x, void* __restrict__ y,
     int rows, int cols, int gshift) {
-    __shared__ float red[kMaxWaves][R];
+    __shared__ float red[2][kMaxWaves][R];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x >> 6;
     const int nwaves = blockDim.x >> 6;
     const int cpr = cols >> 5;
-    const int G = cols >> (5 + gshift);
     const int64_t rbytes = cols >> 1;
-    const int row0 = blockIdx.x * R;
+    const int nblocks = (rows + R - 1) / R;
+    const int stride = gridDim.x;
+    SzLayout L;
+    L.gshift = gshift;
+    L.ng = gshift >= 6 ? 1 : (64 >> gshift);
+    L.G = cols >> (5 + gshift);
+    L.items = CPL * R * L.ng;
 
     int cidx[CPL];
     bool act[CPL];
@@ -271,51 +388,36 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_int4_fast_kernel(
         act[j] = c < cpr;
         cidx[j] = act[j] ? c : 0;
     }
-    // weights, scales and zero bytes of every row first: they are the HBM stream
-    u32x4 w[R][CPL];
-    float s[R][CPL];
-    uint32_t zb[R][CPL];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int64_t rr = min(row0 + r, rows - 1);  // tail rows re-read the last row
-        const u32x4* prow = reinterpret_cast<const u32x4*>(packed + rr * rbytes);
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) w[r][j] = __builtin_nontemporal_load(prow + cidx[j]);
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int64_t rr = min(row0 + r, rows - 1);
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const int g = cidx[j] >> gshift;
-            s[r][j] = act[j] ? scales[rr * G + g] : 0.0f;
-            zb[r][j] = zeros[rr * (G >> 1) + (g >> 1)];
-        }
-    }
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    int rb = blockIdx.x;
+    RowBlock<R, CPL> bufA, bufB;
+    load_row_block<R, CPL>(bufA, packed, scales, zeros, rb * R, rows, rbytes, cidx, L, wave, lane);
+    XChunk<XBF16> xc[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const XChunk<XBF16> xc = load_x_chunk<XBF16>(x, cidx[j]);
-        const uint32_t godd = (cidx[j] >> gshift) & 1u;
+        xc[j] = load_x_chunk<XBF16>(x, cidx[j]);
+        if (!act[j]) {  // lanes past the end of a row contribute nothing
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const uint32_t z = godd ? (zb[r][j] >> 4) : (zb[r][j] & 0xFu);
-            const float off = static_cast<float>((XBF16 ? 136u : 8u) + z);
-            const float part = fmaf(s[r][j], fmaf(-off, xc.sum, chunk_dot<XBF16>(w[r][j], xc)), acc[r]);
-            acc[r] = act[j] ? part : acc[r];
+            for (int q = 0; q < (XBF16 ? 4 : 8); ++q) xc[j].q[q] = u32x4{0u, 0u, 0u, 0u};
+            xc[j].sum = 0.0f;
         }
     }
-    const float t = wave_reduce_rows<R>(acc, lane);
-    constexpr int kGroup = kWave / R;
-    if ((lane & (kGroup - 1)) == 0) red[wave][lane / kGroup] = t;
-    __syncthreads();
-    if (threadIdx.x < R) {
-        float tot = red[0][threadIdx.x];
-        for (int wv = 1; wv < nwaves; ++wv) tot += red[wv][threadIdx.x];
-        if (row0 + static_cast<int>(threadIdx.x) < rows)
-            store_y<YBF16>(y, row0 + threadIdx.x, tot);
+
+    // The prefetch is unconditional (the block past the end re-reads the last
+    // one): a conditional load would make the compiler wait for every
+    // outstanding load, prefetch included, before the current block's math.
+    for (;;) {
+        load_row_block<R, CPL>(bufB, packed, scales, zeros, min(rb + stride, nblocks - 1) * R,
+                               rows, rbytes, cidx, L, wave, lane);
+        finish_row_block<R, CPL, XBF16, YBF16>(bufA, xc, act, L, red[0], rb * R, rows, y, lane,
+                                               wave, nwaves);
+        rb += stride;
+        if (rb >= nblocks) break;
+        load_row_block<R, CPL>(bufA, packed, scales, zeros, min(rb + stride, nblocks - 1) * R,
+                               rows, rbytes, cidx, L, wave, lane);
+        finish_row_block<R, CPL, XBF16, YBF16>(bufB, xc, act, L, red[1], rb * R, rows, y, lane,
+                                               wave, nwaves);
+        rb += stride;
+        if (rb >= nblocks) break;
     }
 }
 
@@ -409,41 +511,70 @@ int rows_per_block_override() {
     return v;
 }
 
-// Rows per workgroup: enough workgroups to give every CU several waves, and
-// as many rows as that allows so x (loaded once per workgroup) is reused.
+// Rows per workgroup iteration.
 int pick_rows_per_block(int64_t rows, int waves_per_block) {
     const int o = rows_per_block_override();
-    if (o == 1 || o == 2 || o == 4 || o == 8) return o;
-    const int64_t target_waves = 256 * 24;  // CUs x resident waves per CU
-    for (int R : {8, 4, 2}) {
-        if (((rows + R - 1) / R) * waves_per_block >= target_waves) return R;
-    }
-    return 1;
+    if (o == 1 || o == 2 || o == 4) return o;
+    (void)rows;
+    (void)waves_per_block;
+    return 4;
 }
 
+int waves_per_cu_override() {
+    static const int v = [] {
+        const char* e = getenv("KC_GEMV_WAVES_PER_CU");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
+int device_cu_count() {
+    static const int n = [] {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            cus = 256;
+        return cus;
+    }();
+    return n;
+}
+
+// Persistent grid: as many workgroups as the CUs hold at once (from the
+// occupancy of this kernel instance), with the same number of row blocks (to
+// within one) for every workgroup.
 template <int R, int CPL, bool XB, bool YB>
 void launch_fast(const uint8_t* packed, const float* scales, const uint8_t* zeros, const void* x,
                  void* y, int rows, int cols, int gshift, int waves, hipStream_t stream) {
-    const unsigned grid = static_cast<unsigned>((rows + R - 1) / R);
-    gemv_int4_fast_kernel<R, CPL, XB, YB><<<grid, waves * kWave, 0, stream>>>(
+    const int threads = waves * kWave;
+    static thread_local int cached_threads = -1, cached_occ = 1;
+    if (cached_threads != threads) {
+        int occ = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &occ, gemv_int4_fast_kernel<R, CPL, XB, YB>, threads, 0) != hipSuccess || occ < 1)
+            occ = 1;
+        cached_threads = threads;
+        cached_occ = occ;
+    }
+    int per_cu = cached_occ;
+    if (waves_per_cu_override() > 0) per_cu = std::max(1, std::min(per_cu, waves_per_cu_override() / waves));
+    const int nblocks = (rows + R - 1) / R;
+    const int max_grid = device_cu_count() * per_cu;
+    const int iters = (nblocks + max_grid - 1) / max_grid;
+    const unsigned grid = static_cast<unsigned>((nblocks + iters - 1) / iters);
+    gemv_int4_fast_kernel<R, CPL, XB, YB><<<grid, threads, 0, stream>>>(
         packed, scales, zeros, x, y, rows, cols, gshift);
 }
 
-// R * CPL is capped at 8 (the register file at 16 waves per workgroup).
 template <int CPL, bool XB, bool YB>
 void launch_fast_r(int R, const uint8_t* packed, const float* scales, const uint8_t* zeros,
                    const void* x, void* y, int rows, int cols, int gshift, int waves,
                    hipStream_t stream) {
-    R = std::min(R, 8 / CPL);
-    if constexpr (CPL == 1) {
-        if (R == 8) return launch_fast<8, 1, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, waves, stream);
+    if (R >= 4) {
+        if constexpr (CPL == 1)
+            return launch_fast<4, 1, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, waves, stream);
     }
-    if constexpr (CPL <= 2) {
-        if (R == 4) return launch_fast<4, CPL, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, waves, stream);
-    }
-    if constexpr (CPL <= 4) {
-        if (R == 2) return launch_fast<2, CPL, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, waves, stream);
-    }
+    if (R >= 2) return launch_fast<2, CPL, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, waves, stream);
     launch_fast<1, CPL, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, waves, stream);
 }
 
@@ -455,24 +586,25 @@ int gemv_int4(const char* fn, const uint8_t* packed, const float* scales, const 
     if (st != KC_SUCCESS) return st;
     if (rows == 0) return KC_SUCCESS;
     const int64_t cpr = cols >> 5;
-    // chunks per lane per row: the smallest of 1, 2, 4, 8 that needs <= 16 waves
-    int cpl = 0;
-    for (int c : {1, 2, 4, 8}) {
-        if ((cpr + 64 * c - 1) / (64 * c) <= kMaxWaves) { cpl = c; break; }
-    }
-    const bool fast = cols > 0 && gs >= 32 && kc::is_pow2(gs) && cpl > 0 &&
+    // one 16-byte chunk per lane per row: K <= 32 * 64 * 16 = 32768
+    const bool fast = cols > 0 && gs >= 32 && kc::is_pow2(gs) && cpr <= 64 * kMaxWaves &&
                       rows <= INT32_MAX && kc::aligned(packed, 16) && kc::aligned(x, 16);
     if (fast) {
         const int gshift = kc::ilog2(gs) - 5;
+        const int ng = gshift >= 6 ? 1 : (64 >> gshift);
+        // K <= 4096: one wave covers a row with two chunks per lane (no
+        // cross-wave reduction; the kernel is built for one-wave workgroups);
+        // otherwise one chunk per lane and ceil(K/2048) waves.
+        const int cpl = (cpr <= 128 && 2 * ng <= 64) ? 2 : 1;
         const int waves = static_cast<int>((cpr + 64 * cpl - 1) / (64 * cpl));
-        const int R = pick_rows_per_block(rows, waves);
+        int R = pick_rows_per_block(rows, waves);
+        while (R > 1 && cpl * R * ng > 64) R >>= 1;
+        if (cpl == 2 && R > 2) R = 2;
         const int r = static_cast<int>(rows), c = static_cast<int>(cols);
-        switch (cpl) {
-            case 1: launch_fast_r<1, XB, YB>(R, packed, scales, zeros, x, y, r, c, gshift, waves, stream); break;
-            case 2: launch_fast_r<2, XB, YB>(R, packed, scales, zeros, x, y, r, c, gshift, waves, stream); break;
-            case 4: launch_fast_r<4, XB, YB>(R, packed, scales, zeros, x, y, r, c, gshift, waves, stream); break;
-            default: launch_fast_r<8, XB, YB>(R, packed, scales, zeros, x, y, r, c, gshift, waves, stream); break;
-        }
+        if (cpl == 2)
+            launch_fast_r<2, XB, YB>(R, packed, scales, zeros, x, y, r, c, gshift, waves, stream);
+        else
+            launch_fast_r<1, XB, YB>(R, packed, scales, zeros, x, y, r, c, gshift, waves, stream);
     } else {
         const int64_t grid = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
         if (grid > INT32_MAX)

@@ -110,7 +110,7 @@ def test_gemv_cfg0_4096(gpu, oracle):
 
 SHAPES = [
     # (rows, cols, gs): fast path (gs pow2 >= 32)
-    (1, 32, 32), (3, 64, 32), (17, 256, 64), (16, 4096, 128), (33, 2080, 32),
+    (1, 32, 32), (3, 64, 32), (17, 256, 64), (16, 4096, 128), (33, 2080, 32), (3, 36864, 128),
     (64, 14336, 128), (100, 384, 128), (5, 6144, 256), (257, 1024, 1024),
     # generic path: gs < 32, non power of two, tiny K
     (4, 8, 8), (7, 2, 2), (9, 96, 96), (5, 120, 24), (3, 1000, 10), (2, 4, 4),
