@@ -52,6 +52,18 @@ def fp8_bytes(rows: int, cols: int) -> int:
     return rows * cols * 4 + rows * cols + rows * 4
 
 
+def read_traffic(path: Path):
+    """HBM bytes per launch of the dominant kernel, from the committed
+    rocprofv3 --pmc summary (the line `hbm_bytes_per_launch: N`), or None."""
+    try:
+        for line in path.read_text().splitlines():
+            if line.strip().startswith("hbm_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def log(*a) -> None:
     print(*a, file=sys.stderr, flush=True)
 
@@ -71,6 +83,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="bound on the CPU-baseline sample (0 skips it)")
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of HIP graphs")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="for rocprofv3 --pmc: launch the gate/up GEMV and a plain 64 MiB "
+                         "device copy (the counter calibration) 20 times each, then exit")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -117,6 +132,18 @@ def main() -> int:
                 n, k, GS, torch.cuda.current_stream().cuda_stream)
         if st:
             raise RuntimeError(f"kc_gemv_int4_bf16 failed: {lib.kc_last_error_string().decode()}")
+
+    if args.traffic_probe:
+        src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for j in range(20):
+            launch(j % copies, DOMINANT)
+        torch.cuda.synchronize()
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print("traffic probe done: 20 x gate/up GEMV, 20 x copy of 67108864 B", flush=True)
+        return 0
 
     # ---- parity guard: every shape against an fp32 reference --------------
     for i, (name, n, k) in enumerate(LLAMA):
@@ -192,13 +219,7 @@ def main() -> int:
     dom_name, dom_n, dom_k = LLAMA[DOMINANT]
     dom_bytes = gemv_bytes(dom_n, dom_k)
     achieved = dom_bytes / (kernel_us[dom_name] * 1e-6) / 1e9
-    traffic = None
-    tfile = ROOT / "profiles" / "gemv_int4_bf16_gate_up_traffic.json"
-    if tfile.exists():
-        try:
-            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
-        except Exception:
-            traffic = None
+    traffic = read_traffic(ROOT / "profiles" / "gemv_int4_bf16_gate_up_traffic.md")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                 "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
                 "kernel": f"gemv_int4_fast_kernel bf16 gate/up N={dom_n} K={dom_k}",

@@ -520,6 +520,14 @@ int pick_rows_per_block(int64_t rows, int waves_per_block) {
     return 4;
 }
 
+int chunks_per_lane_override() {
+    static const int v = [] {
+        const char* e = getenv("KC_GEMV_CHUNKS_PER_LANE");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
 int waves_per_cu_override() {
     static const int v = [] {
         const char* e = getenv("KC_GEMV_WAVES_PER_CU");
@@ -595,7 +603,8 @@ int gemv_int4(const char* fn, const uint8_t* packed, const float* scales, const 
         // K <= 4096: one wave covers a row with two chunks per lane (no
         // cross-wave reduction; the kernel is built for one-wave workgroups);
         // otherwise one chunk per lane and ceil(K/2048) waves.
-        const int cpl = (cpr <= 128 && 2 * ng <= 64) ? 2 : 1;
+        int cpl = (cpr <= 128 && 2 * ng <= 64) ? 2 : 1;
+        if (chunks_per_lane_override() == 1) cpl = 1;
         const int waves = static_cast<int>((cpr + 64 * cpl - 1) / (64 * cpl));
         int R = pick_rows_per_block(rows, waves);
         while (R > 1 && cpl * R * ng > 64) R >>= 1;
