@@ -448,6 +448,24 @@ def test_col_absmax_and_smooth_factors(oracle):
     assert np.all(s[ch] > np.median(s))          # outlier channels get the large factors
 
 
+def test_smooth_factors_balance_channel_maxima(oracle):
+    """alpha = 0.5 migration: after X/s and W*s every channel's maximum is
+    sqrt(max|X_j| * max|W_j|) on both sides, and swapping the operands
+    inverts the factor (a transposed or mis-rooted formula fails both)."""
+    rng = np.random.default_rng(12)
+    ax = (10.0 ** rng.uniform(-2, 3, 512)).astype(np.float32)
+    aw = (10.0 ** rng.uniform(-3, 0, 512)).astype(np.float32)
+    s = oracle.smooth_factors(ax, aw).astype(np.float64)
+    geo = np.sqrt(ax.astype(np.float64) * aw.astype(np.float64))
+    np.testing.assert_allclose(ax / s, geo, rtol=1e-6)
+    np.testing.assert_allclose(aw * s, geo, rtol=1e-6)
+    inv = oracle.smooth_factors(aw, ax).astype(np.float64)
+    np.testing.assert_allclose(s * inv, 1.0, rtol=1e-6)
+    # floors: a zero weight channel uses 1e-5, and the factor never drops below 1e-5
+    f = oracle.smooth_factors(np.array([4.0, 0.0], np.float32), np.array([0.0, 1.0], np.float32))
+    assert f[0] == np.float32(2.0) / np.sqrt(np.float32(1e-5)) and f[1] == np.float32(1e-5)
+
+
 def test_bf16_rounding_helpers(oracle):
     vals = np.array([1.0, 1.00390625, 1.0117188, -3.3e38, 1e-40, np.inf], np.float32)
     bits = f32_to_bf16_bits(vals)
