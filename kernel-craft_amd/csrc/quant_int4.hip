@@ -93,23 +93,43 @@ __global__ __launch_bounds__(kThreads) void gemv_int4_generic_kernel(
 // ---------------------------------------------------------------------------
 // Fast GEMV.
 //
-// A row is split into chunks of 32 k (16 bytes of packed weights).  One
-// workgroup computes R consecutive rows; its W waves split K, wave w owning
-// chunks [w*64*CPL, (w+1)*64*CPL) of every row and lane l the chunks
-// w*64*CPL + 64*j + l (j < CPL), so each wave-wide load reads 1 KB of one
-// row.  Every weight load of the workgroup is issued up front.  The lane's x
-// for its chunks is loaded once into registers: for bf16 the quad of k-block
-// i (k = 8i..8i+7 of a chunk) is rearranged into the pairs (x0,x4) (x1,x5)
-// (x2,x6) (x3,x7), the order in which the nibble unpack produces weights;
-// xs is the chunk's fp32 sum of x.  Partial sums are reduced across the wave
-// with a transposed butterfly (R values in log2(64) + R - 1 shuffles) and
-// across the W waves through LDS in a fixed order, so results do not depend
-// on scheduling.
+// A row is split into chunks of 32 k (16 bytes of packed weights); lane l of
+// a wave owns chunks j*64 + l (j < CPL) of every row it computes, so each
+// wave-wide load reads 1 KB of one row.  A workgroup of WPB waves computes
+// R*WPB consecutive rows, R per wave, and shares one copy of x in LDS:
+//
+//   1. every thread issues its x loads first, then the scale/zero loads of
+//      its wave's rows, then all R*CPL weight loads (vector loads return in
+//      order, so x arrives first and the weights are all in flight at once);
+//   2. the workgroup writes x to LDS in the order the nibble decode needs
+//      (bf16: k-block quads rearranged to the pairs (x0,x4)(x1,x5)(x2,x6)
+//      (x3,x7) with v_perm_b32; fp32: as is) together with each chunk's
+//      fp32 sum of x;
+//   3. after one barrier each wave reads its chunks of x from LDS as it
+//      reaches them, decodes and multiplies, and reduces its R rows across
+//      the wave with permlane swaps and DPP row rotations.
+//
+// Per workgroup the x staging is done once instead of once per wave, and no
+// wave holds more than one chunk of x in registers.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t nib_bf16_pair(uint32_t d) {
-    // nibbles at bits 0-3 and 16-19 -> bf16 (128 + (q ^ 8)) in each half
-    return ((d ^ 0x00080008u) & 0x000F000Fu) | 0x43004300u;
+// The decode constants live in VGPRs: on gfx950 a VALU operation that reads
+// an SGPR operand issues at half the rate of one with VGPR operands, and the
+// compiler would otherwise put one of the two masks in an SGPR.  The asm
+// makes the values opaque so they stay in VGPRs.
+struct NibConsts {
+    uint32_t mask;   // 0x000F000F
+    uint32_t magic;  // 0x43084308 = 0x43004300 | (8 << 16) | 8
+};
+
+__device__ __forceinline__ NibConsts nib_consts() {
+    NibConsts k;
+    asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(k.mask));
+    asm volatile("v_mov_b32 %0, 0x43084308" : "=v"(k.magic));
+    return k;
 }
+
+// ((d ^ 0x00080008) & 0x000F000F) | 0x43004300 == (d & 0x000F000F) ^ 0x43084308
+__device__ __forceinline__ uint32_t nib_pair(uint32_t d, NibConsts k) { return (d & k.mask) ^ k.magic; }
 
 // Takes its operand by value: clang miscompiles __builtin_bit_cast applied to
 // an element of an ext_vector reached through a reference (every element
@@ -118,12 +138,12 @@ __device__ __forceinline__ bf16x2_t as_bf16x2(uint32_t v) {
     return __builtin_bit_cast(bf16x2_t, v);
 }
 
-__device__ __forceinline__ float dot8_bf16(uint32_t d, uint32_t x04, uint32_t x15, uint32_t x26,
-                                           uint32_t x37, float a) {
-    a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(nib_bf16_pair(d)), as_bf16x2(x04), a, false);
-    a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(nib_bf16_pair(d >> 4)), as_bf16x2(x15), a, false);
-    a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(nib_bf16_pair(d >> 8)), as_bf16x2(x26), a, false);
-    a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(nib_bf16_pair(d >> 12)), as_bf16x2(x37), a, false);
+__device__ __forceinline__ float dot8_bf16(uint32_t d, u32x4 xq, float a, NibConsts k) {
+    const uint32_t x04 = xq.x, x15 = xq.y, x26 = xq.z, x37 = xq.w;
+    a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(nib_pair(d, k)), as_bf16x2(x04), a, false);
+    a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(nib_pair(d >> 4, k)), as_bf16x2(x15), a, false);
+    a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(nib_pair(d >> 8, k)), as_bf16x2(x26), a, false);
+    a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(nib_pair(d >> 12, k)), as_bf16x2(x37), a, false);
     return a;
 }
 
@@ -142,65 +162,23 @@ __device__ __forceinline__ float dot8_f32(uint32_t d, f32x4 xa, f32x4 xb, float 
     return a;
 }
 
-// The lane's x for one chunk: bf16 as 4 quads of pairs, fp32 as 8 quads.
+// Dot product of one 16-byte weight chunk with the chunk's x, read from LDS
+// (bf16: 4 permuted quads; fp32: 8 quads of 4 values).
 template <bool XBF16>
-struct XChunk {
-    u32x4 q[XBF16 ? 4 : 8];
-    float sum;
-};
-
-template <bool XBF16>
-__device__ __forceinline__ XChunk<XBF16> load_x_chunk(const void* __restrict__ x, int c) {
-    XChunk<XBF16> xc;
-    if constexpr (XBF16) {
-        const u32x4* src = static_cast<const u32x4*>(x) + 4 * c;
-        const bf16x2_t ones = as_bf16x2(0x3F803F80u);
-        float sum = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const u32x4 d = src[i];
-            const uint32_t d0 = d.x, d1 = d.y, d2 = d.z, d3 = d.w;
-            u32x4 p;
-            p.x = (d0 & 0xFFFFu) | (d2 << 16);
-            p.y = (d0 >> 16) | (d2 & 0xFFFF0000u);
-            p.z = (d1 & 0xFFFFu) | (d3 << 16);
-            p.w = (d1 >> 16) | (d3 & 0xFFFF0000u);
-            xc.q[i] = p;
-            sum = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d0), ones, sum, false);
-            sum = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d1), ones, sum, false);
-            sum = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d2), ones, sum, false);
-            sum = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d3), ones, sum, false);
-        }
-        xc.sum = sum;
-    } else {
-        const f32x4* src = static_cast<const f32x4*>(x) + 8 * c;
-        float part[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const f32x4 v = src[i];
-            xc.q[i] = __builtin_bit_cast(u32x4, v);
-            part[i] = (v.x + v.y) + (v.z + v.w);
-        }
-        xc.sum = ((part[0] + part[1]) + (part[2] + part[3])) +
-                 ((part[4] + part[5]) + (part[6] + part[7]));
-    }
-    return xc;
-}
-
-template <bool XBF16>
-__device__ __forceinline__ float chunk_dot(const u32x4 w, const XChunk<XBF16>& xc) {
+__device__ __forceinline__ float chunk_dot(const u32x4 w, const u32x4* xl, NibConsts k) {
     const uint32_t w0 = w.x, w1 = w.y, w2 = w.z, w3 = w.w;
     if constexpr (XBF16) {
-        const u32x4 a0 = xc.q[0], a1 = xc.q[1], a2 = xc.q[2], a3 = xc.q[3];
-        float a = dot8_bf16(w0, a0.x, a0.y, a0.z, a0.w, 0.0f);
-        a = dot8_bf16(w1, a1.x, a1.y, a1.z, a1.w, a);
-        a = dot8_bf16(w2, a2.x, a2.y, a2.z, a2.w, a);
-        return dot8_bf16(w3, a3.x, a3.y, a3.z, a3.w, a);
+        float a = dot8_bf16(w0, xl[0], 0.0f, k);
+        a = dot8_bf16(w1, xl[1], a, k);
+        a = dot8_bf16(w2, xl[2], a, k);
+        return dot8_bf16(w3, xl[3], a, k);
     } else {
-        float a = dot8_f32(w0, __builtin_bit_cast(f32x4, xc.q[0]), __builtin_bit_cast(f32x4, xc.q[1]), 0.0f);
-        a = dot8_f32(w1, __builtin_bit_cast(f32x4, xc.q[2]), __builtin_bit_cast(f32x4, xc.q[3]), a);
-        a = dot8_f32(w2, __builtin_bit_cast(f32x4, xc.q[4]), __builtin_bit_cast(f32x4, xc.q[5]), a);
-        return dot8_f32(w3, __builtin_bit_cast(f32x4, xc.q[6]), __builtin_bit_cast(f32x4, xc.q[7]), a);
+        (void)k;
+        const f32x4* xf = reinterpret_cast<const f32x4*>(xl);
+        float a = dot8_f32(w0, xf[0], xf[1], 0.0f);
+        a = dot8_f32(w1, xf[2], xf[3], a);
+        a = dot8_f32(w2, xf[4], xf[5], a);
+        return dot8_f32(w3, xf[6], xf[7], a);
     }
 }
 
@@ -245,8 +223,8 @@ __device__ __forceinline__ float sum_row16(float t) {
 // Sums v[r] over the wave for R rows.  Afterwards lane (64/R)*r holds the
 // total of row r (so do the other lanes of its group of 64/R).
 template <int R>
-__device__ __forceinline__ float wave_reduce_rows(float (&v)[R], int /*lane*/) {
-    static_assert(R == 1 || R == 2 || R == 4, "rows per block");
+__device__ __forceinline__ float wave_reduce_rows(const float (&v)[R]) {
+    static_assert(R == 1 || R == 2 || R == 4, "rows per wave");
     if constexpr (R == 4) {
         const float a = sum_swap32(v[0], v[2]);  // lanes 0-31: row 0, 32-63: row 2
         const float b = sum_swap32(v[1], v[3]);  // lanes 0-31: row 1, 32-63: row 3
@@ -261,164 +239,165 @@ __device__ __forceinline__ float wave_reduce_rows(float (&v)[R], int /*lane*/) {
     }
 }
 
-constexpr int kMaxWaves = 16;
+// Scale/zero items.  Slot (r, j) -- row r, chunk slot j -- covers the groups
+// of chunks j*64 .. j*64+63 of its row: NG = max(1, 64 / (gs/32)) of them,
+// at most SLOT items.  Slots are packed 64/SLOT to a register: slot s lives
+// in register s / (64/SLOT), lanes (s % (64/SLOT)) * SLOT + gi.  One scale
+// load and one zero-byte load per register bring in every (s, z) a wave
+// needs; a lane then fetches the pair for its own chunk with ds_bpermute
+// from a register index known at compile time.
+//   SLOT = 16 serves gs >= 128, SLOT = 64 serves gs = 32 and 64.
+template <int SLOT>
+struct SlotMap {
+    static constexpr int kPerReg = 64 / SLOT;
+    static constexpr int reg(int s) { return s / kPerReg; }
+    static constexpr int base_lane(int s) { return (s % kPerReg) * SLOT; }
+};
 
-// Per row block, a lane needs for each of its CPL chunks and R rows the
-// group's scale s and zero point z, folded as
+// The fold of one chunk's dot product into the row sum:
 //     acc += c1 * dot + c2 * sum(x),   c1 = s,  c2 = -s * (off + z)
-// (off = 136 for the bf16 encoding 128 + (q ^ 8), 8 for fp32).  A wave's
-// chunk slot j spans NG = max(1, 64 * 32 / gs) groups of a row, so the
-// CPL * R * NG (<= 64) distinct (s, z) of a row block arrive with one
-// coalesced scale load and one zero-byte load, lane i holding item
-// i = (j * R + r) * NG + gi; every lane then picks up its own c1, c2 with
-// ds_bpermute.
-template <int R, int CPL>
-struct RowBlock {
+// off = 136 for the bf16 encoding 128 + (q ^ 8), 8 for fp32.
+template <int R, int CPL, int SLOT, int WPB, bool XBF16, bool YBF16>
+__global__ __launch_bounds__(WPB * kWave) void gemv_int4_fast_kernel(
+    const uint8_t* __restrict__ packed, const float* __restrict__ scales,
+    const uint8_t* __restrict__ zeros, const void* __restrict__ x, void* __restrict__ y,
+    int rows, int cols, int gshift) {
+    using SM = SlotMap<SLOT>;
+    constexpr int kSlots = R * CPL;
+    constexpr int kRegs = (kSlots + SM::kPerReg - 1) / SM::kPerReg;
+    constexpr int kQuadsPerChunk = XBF16 ? 4 : 8;
+    constexpr int kThreadsWG = WPB * kWave;
+    constexpr int kMaxQuads = CPL * 64 * kQuadsPerChunk;
+    constexpr int kQPT = (kMaxQuads + kThreadsWG - 1) / kThreadsWG;  // x quads per thread
+    extern __shared__ u32x4 xl[];                                    // x quads, then chunk sums
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x >> 6;
+    const int cpr = cols >> 5;                      // chunks per row
+    const int nquads = cpr * kQuadsPerChunk;
+    float* xsum = reinterpret_cast<float*>(xl + nquads);
+    const int row0 = (blockIdx.x * WPB + wave) * R;
+    const int64_t rbytes = cols >> 1;
+    const int G = cols >> (5 + gshift);             // groups per row
+    const int ng = gshift >= 6 ? 1 : (64 >> gshift);  // groups per chunk slot
+
+    // 1a. x, raw
+    u32x4 xr[kQPT];
+    {
+        const u32x4* src = static_cast<const u32x4*>(x);
+#pragma unroll
+        for (int u = 0; u < kQPT; ++u)
+            xr[u] = src[min(static_cast<int>(threadIdx.x) + u * kThreadsWG, nquads - 1)];
+    }
+    // 1b. scale and zero byte of every item this lane holds
+    float s_it[kRegs];
+    uint32_t z_it[kRegs];
+#pragma unroll
+    for (int q = 0; q < kRegs; ++q) {
+        const int s = min(q * SM::kPerReg + lane / SLOT, kSlots - 1);
+        const int gi = min(lane % SLOT, ng - 1);
+        const int r = s / CPL, j = s % CPL;
+        const int g = min(((j * 64) >> gshift) + gi, G - 1);
+        const int64_t rr = min(row0 + r, rows - 1);
+        s_it[q] = scales[rr * G + g];
+        z_it[q] = zeros[rr * (G >> 1) + (g >> 1)];
+    }
+    // 1c. weights (chunks past the end of a row read chunk 0 and are masked)
     u32x4 w[R][CPL];
-    float s;       // item scale
-    uint32_t zb;   // item zero byte
-};
-
-struct SzLayout {
-    int ng;        // groups per chunk slot
-    int gshift;    // log2(gs / 32)
-    int G;         // groups per row
-    int items;     // CPL * R * ng
-};
-
-template <int R, int CPL>
-__device__ __forceinline__ void load_row_block(RowBlock<R, CPL>& b, const uint8_t* __restrict__ packed,
-                                               const float* __restrict__ scales,
-                                               const uint8_t* __restrict__ zeros, int row0, int rows,
-                                               int64_t rbytes, const int (&cidx)[CPL],
-                                               const SzLayout& L, int wave, int lane) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int64_t rr = min(row0 + r, rows - 1);  // tail rows re-read the last row
+        const int64_t rr = min(row0 + r, rows - 1);
         const u32x4* prow = reinterpret_cast<const u32x4*>(packed + rr * rbytes);
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) b.w[r][j] = __builtin_nontemporal_load(prow + cidx[j]);
+        for (int j = 0; j < CPL; ++j) {
+            const int c = j * 64 + lane;
+            w[r][j] = __builtin_nontemporal_load(prow + (c < cpr ? c : 0));
+        }
     }
-    // item owned by this lane (lanes past `items` repeat item 0)
-    const int item = lane < L.items ? lane : 0;
-    const int gi = item % L.ng;
-    const int jr = item / L.ng;
-    const int r = jr % R, j = jr / R;
-    const int gbase = ((wave * CPL + j) * kWave) >> L.gshift;
-    const int g = min(gbase + gi, L.G - 1);
-    const int64_t rr = min(row0 + r, rows - 1);
-    b.s = scales[rr * L.G + g];
-    b.zb = zeros[rr * (L.G >> 1) + (g >> 1)];
-}
+    // keep every load above this point: the compiler otherwise sinks weight
+    // loads towards their uses, leaving one row in flight at a time
+    __builtin_amdgcn_sched_barrier(0);
 
-// Dot products of one row block, reduced over the wave and the workgroup,
-// stored to y.  `red` is this iteration's half of the LDS exchange buffer.
-template <int R, int CPL, bool XBF16, bool YBF16>
-__device__ __forceinline__ void finish_row_block(const RowBlock<R, CPL>& b,
-                                                 const XChunk<XBF16> (&xc)[CPL],
-                                                 const bool (&act)[CPL], const SzLayout& L,
-                                                 float (*red)[R], int row0, int rows, void* y,
-                                                 int lane, int wave, int nwaves) {
-    // this lane's item -> c1, c2
-    const int item = lane < L.items ? lane : 0;
-    const int g = min(((((item / L.ng) / R) * kWave + wave * CPL * kWave) >> L.gshift) + item % L.ng,
-                      L.G - 1);
-    const uint32_t z = (g & 1) ? (b.zb >> 4) : (b.zb & 0xFu);
-    const float c1 = b.s;
-    const float c2 = -b.s * static_cast<float>((XBF16 ? 136u : 8u) + z);
-    const int gsub = L.ng > 1 ? (lane >> L.gshift) : 0;  // group of my chunk within its slot
+    // 2. stage x in LDS
+    {
+        const uint32_t ones = 0x3F803F80u;
+        uint32_t sel_lo, sel_hi;  // v_perm_b32 selectors, in VGPRs (see nib_consts)
+        asm volatile("v_mov_b32 %0, 0x05040100" : "=v"(sel_lo));
+        asm volatile("v_mov_b32 %0, 0x07060302" : "=v"(sel_hi));
+#pragma unroll
+        for (int u = 0; u < kQPT; ++u) {
+            const int i = threadIdx.x + u * kThreadsWG;
+            const u32x4 d = xr[u];
+            const uint32_t d0 = d.x, d1 = d.y, d2 = d.z, d3 = d.w;
+            u32x4 p;
+            float sm;
+            if constexpr (XBF16) {
+                p.x = __builtin_amdgcn_perm(d2, d0, sel_lo);   // (x0, x4)
+                p.y = __builtin_amdgcn_perm(d2, d0, sel_hi);   // (x1, x5)
+                p.z = __builtin_amdgcn_perm(d3, d1, sel_lo);   // (x2, x6)
+                p.w = __builtin_amdgcn_perm(d3, d1, sel_hi);   // (x3, x7)
+                sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d0), as_bf16x2(ones), 0.0f, false);
+                sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d1), as_bf16x2(ones), sm, false);
+                sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d2), as_bf16x2(ones), sm, false);
+                sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d3), as_bf16x2(ones), sm, false);
+                sm += __shfl_xor(sm, 1, kWave);  // 4 consecutive quads form a chunk
+                sm += __shfl_xor(sm, 2, kWave);
+            } else {
+                p = d;
+                sm = (__uint_as_float(d0) + __uint_as_float(d1)) +
+                     (__uint_as_float(d2) + __uint_as_float(d3));
+                sm += __shfl_xor(sm, 1, kWave);  // 8 consecutive quads form a chunk
+                sm += __shfl_xor(sm, 2, kWave);
+                sm += __shfl_xor(sm, 4, kWave);
+            }
+            if (i < nquads) {
+                xl[i] = p;
+                if (i % kQuadsPerChunk == 0) xsum[i / kQuadsPerChunk] = sm;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 3. decode, multiply, fold, reduce
+    float c1[kRegs], c2[kRegs];
+#pragma unroll
+    for (int q = 0; q < kRegs; ++q) {
+        const int s = min(q * SM::kPerReg + lane / SLOT, kSlots - 1);
+        const int gi = min(lane % SLOT, ng - 1);
+        const int j = s % CPL;
+        const int g = min(((j * 64) >> gshift) + gi, G - 1);
+        const uint32_t z = (g & 1) ? (z_it[q] >> 4) : (z_it[q] & 0xFu);
+        c1[q] = s_it[q];
+        c2[q] = -s_it[q] * static_cast<float>((XBF16 ? 136u : 8u) + z);
+    }
+    const NibConsts nk = nib_consts();
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
+        const int c = j * 64 + lane;
+        const bool act = c < cpr;
+        const int cc = act ? c : 0;
+        const u32x4* xc = xl + cc * kQuadsPerChunk;
+        const float xs = xsum[cc];
+        // this lane's group within the slot
+        const int gi = ((j * 64 + lane) >> gshift) - ((j * 64) >> gshift);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int src = ((j * R + r) * L.ng + gsub) << 2;
-            float m1 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, c1)));
-            float m2 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, c2)));
-            m1 = act[j] ? m1 : 0.0f;
-            m2 = act[j] ? m2 : 0.0f;
-            acc[r] = fmaf(m1, chunk_dot<XBF16>(b.w[r][j], xc[j]), fmaf(m2, xc[j].sum, acc[r]));
+            const int s = r * CPL + j;
+            const int src = (SM::base_lane(s) + gi) << 2;
+            float m1 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, c1[SM::reg(s)])));
+            float m2 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, c2[SM::reg(s)])));
+            m1 = act ? m1 : 0.0f;
+            m2 = act ? m2 : 0.0f;
+            acc[r] = fmaf(m1, chunk_dot<XBF16>(w[r][j], xc, nk), fmaf(m2, xs, acc[r]));
         }
     }
-    const float t = wave_reduce_rows<R>(acc, lane);
+    const float t = wave_reduce_rows<R>(acc);
     constexpr int kGroup = kWave / R;
-    if (nwaves == 1) {
-        const int r = lane / kGroup;
-        if ((lane & (kGroup - 1)) == 0 && row0 + r < rows) store_y<YBF16>(y, row0 + r, t);
-        return;
-    }
-    if ((lane & (kGroup - 1)) == 0) red[wave][lane / kGroup] = t;
-    __syncthreads();
-    if (threadIdx.x < R) {
-        float tot = red[0][threadIdx.x];
-        for (int wv = 1; wv < nwaves; ++wv) tot += red[wv][threadIdx.x];
-        if (row0 + static_cast<int>(threadIdx.x) < rows)
-            store_y<YBF16>(y, row0 + threadIdx.x, tot);
-    }
-}
-
-// Persistent: workgroup b computes row blocks b, b + gridDim.x, ...; the next
-// block's weights are in flight while the current block is reduced.
-template <int R, int CPL, bool XBF16, bool YBF16>
-__global__ __launch_bounds__(CPL == 1 ? kMaxWaves * kWave : kWave) void gemv_int4_fast_kernel(
-    const uint8_t* __restrict__ packed, const float* __restrict__ scales,
-    const uint8_t* __restrict__ zeros, const void* __restrict__ x, void* __restrict__ y,
-    int rows, int cols, int gshift) {
-    __shared__ float red[2][kMaxWaves][R];
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x >> 6;
-    const int nwaves = blockDim.x >> 6;
-    const int cpr = cols >> 5;
-    const int64_t rbytes = cols >> 1;
-    const int nblocks = (rows + R - 1) / R;
-    const int stride = gridDim.x;
-    SzLayout L;
-    L.gshift = gshift;
-    L.ng = gshift >= 6 ? 1 : (64 >> gshift);
-    L.G = cols >> (5 + gshift);
-    L.items = CPL * R * L.ng;
-
-    int cidx[CPL];
-    bool act[CPL];
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        const int c = (wave * CPL + j) * kWave + lane;
-        act[j] = c < cpr;
-        cidx[j] = act[j] ? c : 0;
-    }
-    int rb = blockIdx.x;
-    RowBlock<R, CPL> bufA, bufB;
-    load_row_block<R, CPL>(bufA, packed, scales, zeros, rb * R, rows, rbytes, cidx, L, wave, lane);
-    XChunk<XBF16> xc[CPL];
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        xc[j] = load_x_chunk<XBF16>(x, cidx[j]);
-        if (!act[j]) {  // lanes past the end of a row contribute nothing
-#pragma unroll
-            for (int q = 0; q < (XBF16 ? 4 : 8); ++q) xc[j].q[q] = u32x4{0u, 0u, 0u, 0u};
-            xc[j].sum = 0.0f;
-        }
-    }
-
-    // The prefetch is unconditional (the block past the end re-reads the last
-    // one): a conditional load would make the compiler wait for every
-    // outstanding load, prefetch included, before the current block's math.
-    for (;;) {
-        load_row_block<R, CPL>(bufB, packed, scales, zeros, min(rb + stride, nblocks - 1) * R,
-                               rows, rbytes, cidx, L, wave, lane);
-        finish_row_block<R, CPL, XBF16, YBF16>(bufA, xc, act, L, red[0], rb * R, rows, y, lane,
-                                               wave, nwaves);
-        rb += stride;
-        if (rb >= nblocks) break;
-        load_row_block<R, CPL>(bufA, packed, scales, zeros, min(rb + stride, nblocks - 1) * R,
-                               rows, rbytes, cidx, L, wave, lane);
-        finish_row_block<R, CPL, XBF16, YBF16>(bufB, xc, act, L, red[1], rb * R, rows, y, lane,
-                                               wave, nwaves);
-        rb += stride;
-        if (rb >= nblocks) break;
-    }
+    const int r = lane / kGroup;
+    if ((lane & (kGroup - 1)) == 0 && row0 + r < rows) store_y<YBF16>(y, row0 + r, t);
 }
 
 // ---------------------------------------------------------------------------
@@ -503,87 +482,39 @@ int check_int4_args(const char* fn, const void* packed, const void* scales, cons
     return KC_SUCCESS;
 }
 
-int rows_per_block_override() {
+int device_max_lds() {
     static const int v = [] {
-        const char* e = getenv("KC_GEMV_ROWS_PER_BLOCK");
-        return e ? atoi(e) : 0;
-    }();
-    return v;
-}
-
-// Rows per workgroup iteration.
-int pick_rows_per_block(int64_t rows, int waves_per_block) {
-    const int o = rows_per_block_override();
-    if (o == 1 || o == 2 || o == 4) return o;
-    (void)rows;
-    (void)waves_per_block;
-    return 4;
-}
-
-int chunks_per_lane_override() {
-    static const int v = [] {
-        const char* e = getenv("KC_GEMV_CHUNKS_PER_LANE");
-        return e ? atoi(e) : 0;
-    }();
-    return v;
-}
-
-int waves_per_cu_override() {
-    static const int v = [] {
-        const char* e = getenv("KC_GEMV_WAVES_PER_CU");
-        return e ? atoi(e) : 0;
-    }();
-    return v;
-}
-
-int device_cu_count() {
-    static const int n = [] {
-        int dev = 0, cus = 0;
+        int dev = 0, lds = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            cus <= 0)
-            cus = 256;
-        return cus;
+            hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+            lds <= 0)
+            lds = 65536;
+        return std::min(lds, 65536);
     }();
-    return n;
+    return v;
 }
 
-// Persistent grid: as many workgroups as the CUs hold at once (from the
-// occupancy of this kernel instance), with the same number of row blocks (to
-// within one) for every workgroup.
-template <int R, int CPL, bool XB, bool YB>
+template <int R, int CPL, int SLOT, int WPB, bool XB, bool YB>
 void launch_fast(const uint8_t* packed, const float* scales, const uint8_t* zeros, const void* x,
-                 void* y, int rows, int cols, int gshift, int waves, hipStream_t stream) {
-    const int threads = waves * kWave;
-    static thread_local int cached_threads = -1, cached_occ = 1;
-    if (cached_threads != threads) {
-        int occ = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &occ, gemv_int4_fast_kernel<R, CPL, XB, YB>, threads, 0) != hipSuccess || occ < 1)
-            occ = 1;
-        cached_threads = threads;
-        cached_occ = occ;
-    }
-    int per_cu = cached_occ;
-    if (waves_per_cu_override() > 0) per_cu = std::max(1, std::min(per_cu, waves_per_cu_override() / waves));
-    const int nblocks = (rows + R - 1) / R;
-    const int max_grid = device_cu_count() * per_cu;
-    const int iters = (nblocks + max_grid - 1) / max_grid;
-    const unsigned grid = static_cast<unsigned>((nblocks + iters - 1) / iters);
-    gemv_int4_fast_kernel<R, CPL, XB, YB><<<grid, threads, 0, stream>>>(
+                 void* y, int rows, int cols, int gshift, size_t lds, hipStream_t stream) {
+    const int wave_blocks = (rows + R - 1) / R;
+    const unsigned grid = static_cast<unsigned>((wave_blocks + WPB - 1) / WPB);
+    gemv_int4_fast_kernel<R, CPL, SLOT, WPB, XB, YB><<<grid, WPB * kWave, lds, stream>>>(
         packed, scales, zeros, x, y, rows, cols, gshift);
 }
 
+// Rows per wave and waves per workgroup: 2 rows and 4 waves up to K = 16384
+// (at most 8 weight chunks per row and lane); 1 row and 8 waves beyond.
 template <int CPL, bool XB, bool YB>
-void launch_fast_r(int R, const uint8_t* packed, const float* scales, const uint8_t* zeros,
-                   const void* x, void* y, int rows, int cols, int gshift, int waves,
-                   hipStream_t stream) {
-    if (R >= 4) {
-        if constexpr (CPL == 1)
-            return launch_fast<4, 1, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, waves, stream);
-    }
-    if (R >= 2) return launch_fast<2, CPL, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, waves, stream);
-    launch_fast<1, CPL, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, waves, stream);
+void launch_fast_cpl(int slot, const uint8_t* packed, const float* scales, const uint8_t* zeros,
+                     const void* x, void* y, int rows, int cols, int gshift, size_t lds,
+                     hipStream_t stream) {
+    constexpr int R = CPL <= 8 ? 2 : 1;
+    constexpr int WPB = CPL <= 8 ? 4 : 8;
+    if (slot == 16)
+        launch_fast<R, CPL, 16, WPB, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, lds, stream);
+    else
+        launch_fast<R, CPL, 64, WPB, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, lds, stream);
 }
 
 template <bool XB, bool YB>
@@ -594,26 +525,28 @@ int gemv_int4(const char* fn, const uint8_t* packed, const float* scales, const 
     if (st != KC_SUCCESS) return st;
     if (rows == 0) return KC_SUCCESS;
     const int64_t cpr = cols >> 5;
-    // one 16-byte chunk per lane per row: K <= 32 * 64 * 16 = 32768
-    const bool fast = cols > 0 && gs >= 32 && kc::is_pow2(gs) && cpr <= 64 * kMaxWaves &&
-                      rows <= INT32_MAX && kc::aligned(packed, 16) && kc::aligned(x, 16);
+    const int64_t cpl = (cpr + 63) / 64;
+    // x and its chunk sums in LDS
+    const size_t lds = static_cast<size_t>(cpr) * (XB ? 64 : 128) + static_cast<size_t>(cpr) * 4;
+    const bool fast = cols > 0 && gs >= 32 && kc::is_pow2(gs) && cpl <= 16 &&
+                      rows <= INT32_MAX && kc::aligned(packed, 16) && kc::aligned(x, 16) &&
+                      lds <= static_cast<size_t>(device_max_lds());
     if (fast) {
         const int gshift = kc::ilog2(gs) - 5;
-        const int ng = gshift >= 6 ? 1 : (64 >> gshift);
-        // K <= 4096: one wave covers a row with two chunks per lane (no
-        // cross-wave reduction; the kernel is built for one-wave workgroups);
-        // otherwise one chunk per lane and ceil(K/2048) waves.
-        int cpl = (cpr <= 128 && 2 * ng <= 64) ? 2 : 1;
-        if (chunks_per_lane_override() == 1) cpl = 1;
-        const int waves = static_cast<int>((cpr + 64 * cpl - 1) / (64 * cpl));
-        int R = pick_rows_per_block(rows, waves);
-        while (R > 1 && cpl * R * ng > 64) R >>= 1;
-        if (cpl == 2 && R > 2) R = 2;
+        const int slot = gshift >= 2 ? 16 : 64;
         const int r = static_cast<int>(rows), c = static_cast<int>(cols);
-        if (cpl == 2)
-            launch_fast_r<2, XB, YB>(R, packed, scales, zeros, x, y, r, c, gshift, waves, stream);
-        else
-            launch_fast_r<1, XB, YB>(R, packed, scales, zeros, x, y, r, c, gshift, waves, stream);
+#define KC_FAST_CASE(N)                                                                         \
+    case N:                                                                                     \
+        launch_fast_cpl<N, XB, YB>(slot, packed, scales, zeros, x, y, r, c, gshift, lds, stream); \
+        break;
+        switch (cpl) {
+            KC_FAST_CASE(1) KC_FAST_CASE(2) KC_FAST_CASE(3) KC_FAST_CASE(4)
+            KC_FAST_CASE(5) KC_FAST_CASE(6) KC_FAST_CASE(7) KC_FAST_CASE(8)
+            KC_FAST_CASE(9) KC_FAST_CASE(10) KC_FAST_CASE(11) KC_FAST_CASE(12)
+            KC_FAST_CASE(13) KC_FAST_CASE(14) KC_FAST_CASE(15) KC_FAST_CASE(16)
+            default: break;
+        }
+#undef KC_FAST_CASE
     } else {
         const int64_t grid = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
         if (grid > INT32_MAX)
