@@ -14,6 +14,7 @@
 // Per-token kernels read a row once: each thread keeps its slice of the row in
 // registers across the absmax reduction, then converts and stores it.
 #include <algorithm>
+#include <type_traits>
 
 #include "kc_common.hpp"
 
@@ -57,6 +58,50 @@ __device__ __forceinline__ uint8_t e4m3x1(float a) {
 
 __device__ __forceinline__ float row_scale(float amax) {
     return amax > 0.0f ? amax / kE4M3Max : 1.0f;  // fp8_quant.cu:121
+}
+
+// Division by the row scale.  The reference divides every element by its
+// row's scale with an IEEE division (fp8_quant.cu:126).  With r = RN(1/s),
+// computed once per row by a correctly rounded division, Markstein's
+// correction step
+//     q0 = RN(x * r),   e = x - s * q0 (exact: one FMA),   q = RN(q0 + e * r)
+// returns RN(x / s) whenever the residual e is exactly representable, which
+// holds for |x| >= 2^-103 (no underflow in e).  It is used for rows with
+// 2^-60 <= absmax <= FLT_MAX: there r is a normal number, and every element
+// with |x| < 2^-103 has |x/s| < 2^-34, far below the smallest E4M3 step
+// (2^-9), so its code is +0 or -0 on both routes; copysign carries the sign
+// of x through, including -0 (the FMA steps would turn -0 into +0).  Other
+// rows (all-tiny or non-finite absmax) divide exactly.  Three VALU operations
+// instead of the ~10 of a correctly rounded division per element.
+struct RowDiv {
+    float s;      // row scale
+    float r;      // RN(1 / s)
+    bool fast;    // Markstein is exact for this row
+};
+
+__device__ __forceinline__ RowDiv row_div(float amax) {
+    RowDiv d;
+    d.s = row_scale(amax);
+    d.r = 1.0f / d.s;
+    d.fast = amax >= 0x1p-60f && amax <= 3.40282347e38f;
+    return d;
+}
+
+template <bool FAST>
+__device__ __forceinline__ float div_scale(float x, const RowDiv& d) {
+    if constexpr (FAST) {
+        const float q0 = __fmul_rn(x, d.r);
+        const float e = fmaf(-d.s, q0, x);
+        return copysignf(fmaf(e, d.r, q0), x);
+    } else {
+        return x / d.s;
+    }
+}
+
+template <bool FAST>
+__device__ __forceinline__ uint32_t e4m3x4_div(f32x4 v, const RowDiv& d) {
+    return e4m3x4(div_scale<FAST>(v.x, d), div_scale<FAST>(v.y, d), div_scale<FAST>(v.z, d),
+                  div_scale<FAST>(v.w, d));
 }
 
 __device__ __forceinline__ float absmax4(float m, f32x4 v) {
@@ -119,17 +164,17 @@ __global__ __launch_bounds__(kThreads) void quant_rows_f32_kernel(
             m = absmax4(m, v[j]);
         }
     }
-    const float scale = row_scale(block_max(m, red));
-    if (threadIdx.x == 0) scales[row] = scale;
+    const RowDiv d = row_div(block_max(m, red));
+    if (threadIdx.x == 0) scales[row] = d.s;
+    auto emit = [&](auto fast) {
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const int i = threadIdx.x + j * kThreads;
-        if (i < n4) {
-            const f32x4 q = v[j];
-            __builtin_nontemporal_store(e4m3x4(q.x / scale, q.y / scale, q.z / scale, q.w / scale),
-                                        dst + i);
+        for (int j = 0; j < NV; ++j) {
+            const int i = threadIdx.x + j * kThreads;
+            if (i < n4) __builtin_nontemporal_store(e4m3x4_div<decltype(fast)::value>(v[j], d), dst + i);
         }
-    }
+    };
+    if (d.fast) emit(std::true_type{});
+    else emit(std::false_type{});
 }
 
 template <int NV, Smooth S>
@@ -153,19 +198,94 @@ __global__ __launch_bounds__(kThreads) void quant_rows_bf16_kernel(
             m = absmax4(absmax4(m, lo[j]), hi[j]);
         }
     }
-    const float scale = row_scale(block_max(m, red));
-    if (threadIdx.x == 0) scales[row] = scale;
+    const RowDiv d = row_div(block_max(m, red));
+    if (threadIdx.x == 0) scales[row] = d.s;
+    auto emit = [&](auto fast) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int i = threadIdx.x + j * kThreads;
+            if (i < n8) {
+                u32x2 o;
+                o.x = e4m3x4_div<decltype(fast)::value>(lo[j], d);
+                o.y = e4m3x4_div<decltype(fast)::value>(hi[j], d);
+                __builtin_nontemporal_store(o, dst + i);
+            }
+        }
+    };
+    if (d.fast) emit(std::true_type{});
+    else emit(std::false_type{});
+}
+
+// ---------------------------------------------------------------------------
+// Per-row quantizer, one wave per row (rows of up to 4096 fp32 / 8192 bf16).
+// Lane l holds 16-byte slots l, l+64, ... (NV of them) of the row in
+// registers: the row is read once, its absmax is a wave reduction (no LDS,
+// no barrier), and the codes are written from the same registers.  Each wave
+// keeps its whole row (up to 16 KB) in flight.  With smoothing the smoothed
+// fp32 values are kept instead of the raw input.
+// ---------------------------------------------------------------------------
+template <int NV, bool BF16, Smooth S>
+__global__ __launch_bounds__(kWave) void quant_rows_wave_kernel(
+    const void* __restrict__ in, const float* __restrict__ smooth, int8_t* __restrict__ out,
+    float* __restrict__ scales, int64_t cols) {
+    constexpr int kVals = BF16 ? 8 : 4;                 // values per 16-byte slot
+    constexpr int kF4 = BF16 ? 2 : 1;                   // float4 per slot
+    constexpr bool kKeep = S != Smooth::kNone;          // keep smoothed values
+    const int lane = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const int nslots = static_cast<int>(cols / kVals);
+    const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const char*>(in) +
+                                                      row * cols * (BF16 ? 2 : 4));
+    u32x4 raw[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int i = threadIdx.x + j * kThreads;
-        if (i < n8) {
-            const f32x4 a = lo[j], b = hi[j];
-            u32x2 o;
-            o.x = e4m3x4(a.x / scale, a.y / scale, a.z / scale, a.w / scale);
-            o.y = e4m3x4(b.x / scale, b.y / scale, b.z / scale, b.w / scale);
-            __builtin_nontemporal_store(o, dst + i);
+        const int i = j * kWave + lane;
+        raw[j] = __builtin_nontemporal_load(src + (i < nslots ? i : 0));
+    }
+    auto values = [&](int j, int h) -> f32x4 {  // float4 h of slot j, before smoothing
+        const u32x4 d = raw[j];
+        if constexpr (BF16) return h == 0 ? bf16x4_to_f32(d.x, d.y) : bf16x4_to_f32(d.z, d.w);
+        else return __builtin_bit_cast(f32x4, d);
+    };
+    f32x4 kept[kKeep ? NV * kF4 : 1];
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i = j * kWave + lane;
+        if (i < nslots) {
+#pragma unroll
+            for (int h = 0; h < kF4; ++h) {
+                const f32x4 v = apply_smooth<S>(quiet4(values(j, h)), smooth,
+                                                int64_t{i} * kVals + 4 * h);
+                if constexpr (kKeep) kept[j * kF4 + h] = v;
+                m = absmax4(m, v);
+            }
         }
     }
+    const RowDiv d = row_div(kc::wave_max(m));
+    if (lane == 0) scales[row] = d.s;
+    auto emit = [&](auto fast) {
+        constexpr bool F = decltype(fast)::value;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int i = j * kWave + lane;
+            if (i >= nslots) continue;
+            uint32_t o[kF4];
+#pragma unroll
+            for (int h = 0; h < kF4; ++h) {
+                f32x4 v;
+                if constexpr (kKeep) v = kept[j * kF4 + h];
+                else v = F ? values(j, h) : quiet4(values(j, h));  // Markstein quiets sNaN itself
+                o[h] = e4m3x4_div<F>(v, d);
+            }
+            if constexpr (BF16)
+                __builtin_nontemporal_store(u32x2{o[0], o[1]}, reinterpret_cast<u32x2*>(out + row * cols) + i);
+            else
+                __builtin_nontemporal_store(o[0], reinterpret_cast<uint32_t*>(out + row * cols) + i);
+        }
+    };
+    if (d.fast) emit(std::true_type{});
+    else emit(std::false_type{});
 }
 
 // ---------------------------------------------------------------------------
@@ -193,11 +313,12 @@ __global__ __launch_bounds__(kThreads) void quant_rows_generic_kernel(
     float m = 0.0f;
     for (int64_t c = threadIdx.x; c < cols; c += kThreads)
         m = fmaxf(m, fabsf(load_elem<BF16, S>(in, smooth, row, cols, c)));
-    const float scale = row_scale(block_max(m, red));
-    if (threadIdx.x == 0) scales[row] = scale;
-    for (int64_t c = threadIdx.x; c < cols; c += kThreads)
-        out[row * cols + c] =
-            static_cast<int8_t>(e4m3x1(load_elem<BF16, S>(in, smooth, row, cols, c) / scale));
+    const RowDiv d = row_div(block_max(m, red));
+    if (threadIdx.x == 0) scales[row] = d.s;
+    for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
+        const float v = load_elem<BF16, S>(in, smooth, row, cols, c);
+        out[row * cols + c] = static_cast<int8_t>(e4m3x1(d.fast ? div_scale<true>(v, d) : div_scale<false>(v, d)));
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -371,6 +492,15 @@ int quant_rows_f32(const char* fn, const float* in, const float* smooth, int8_t*
     const unsigned grid = static_cast<unsigned>(rows);
     const bool vec = cols > 0 && cols % 4 == 0 && kc::aligned(in, 16) && kc::aligned(out, 4) &&
                      (S == Smooth::kNone || kc::aligned(smooth, 16));
+    const int64_t slots = (cols / 4 + kWave - 1) / kWave;  // 16-byte slots per lane, one wave per row
+    if (vec && slots <= 16) {
+        if (slots <= 1) quant_rows_wave_kernel<1, false, S><<<grid, kWave, 0, stream>>>(in, smooth, out, scales, cols);
+        else if (slots <= 2) quant_rows_wave_kernel<2, false, S><<<grid, kWave, 0, stream>>>(in, smooth, out, scales, cols);
+        else if (slots <= 4) quant_rows_wave_kernel<4, false, S><<<grid, kWave, 0, stream>>>(in, smooth, out, scales, cols);
+        else if (slots <= 8) quant_rows_wave_kernel<8, false, S><<<grid, kWave, 0, stream>>>(in, smooth, out, scales, cols);
+        else quant_rows_wave_kernel<16, false, S><<<grid, kWave, 0, stream>>>(in, smooth, out, scales, cols);
+        return kc::check_launch(fn);
+    }
     const int64_t nv = (cols + 1023) / 1024;
     if (vec && nv <= 1)
         quant_rows_f32_kernel<1, S><<<grid, kThreads, 0, stream>>>(in, smooth, out, scales, cols);
@@ -397,6 +527,15 @@ int quant_rows_bf16(const char* fn, const uint16_t* in, const float* smooth, int
     const unsigned grid = static_cast<unsigned>(rows);
     const bool vec = cols > 0 && cols % 8 == 0 && kc::aligned(in, 16) && kc::aligned(out, 8) &&
                      (S == Smooth::kNone || kc::aligned(smooth, 16));
+    const int64_t slots = (cols / 8 + kWave - 1) / kWave;  // 16-byte slots per lane, one wave per row
+    if (vec && slots <= 16) {
+        if (slots <= 1) quant_rows_wave_kernel<1, true, S><<<grid, kWave, 0, stream>>>(in, smooth, out, scales, cols);
+        else if (slots <= 2) quant_rows_wave_kernel<2, true, S><<<grid, kWave, 0, stream>>>(in, smooth, out, scales, cols);
+        else if (slots <= 4) quant_rows_wave_kernel<4, true, S><<<grid, kWave, 0, stream>>>(in, smooth, out, scales, cols);
+        else if (slots <= 8) quant_rows_wave_kernel<8, true, S><<<grid, kWave, 0, stream>>>(in, smooth, out, scales, cols);
+        else quant_rows_wave_kernel<16, true, S><<<grid, kWave, 0, stream>>>(in, smooth, out, scales, cols);
+        return kc::check_launch(fn);
+    }
     const int64_t nv = (cols + 2047) / 2048;
     if (vec && nv <= 1)
         quant_rows_bf16_kernel<1, S><<<grid, kThreads, 0, stream>>>(in, smooth, out, scales, cols);
