@@ -14,8 +14,12 @@ cannot hold them; each step replays a HIP graph of the four launches.
 `roofline` is for the dominant kernel (the gate/up GEMV): its algorithmic
 bytes per launch over its average duration, timed with HIP events on the
 launch stream; `cpu_baseline` times the CPU oracle's scalar GEMV on the same
-inputs on one host thread.  `fp8_quant` reports the per-token quantizer on
-BASELINE cfg1 (X fp32 [4096, 4096]).
+inputs on one host thread.  The other BASELINE configurations are reported
+beside it, each as algorithmic bytes over the average launch duration:
+`gemv_cfg0` (fp32 reference-ABI GEMV, 4096 x 4096), `gemm_cfg3` (MFMA
+small-batch GEMM, M = 4/16/64, K 8192, N 28672), `fp8_quant` (cfg1 per-token X
+and per-channel W, fp32 [4096, 4096]) and `fp8_cfg4` (SmoothQuant statistics
+and the two fused quantizers on bf16 X [16384, 8192] and W [28672, 8192]).
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20]
 """
@@ -73,6 +77,28 @@ def enqueue_backlog(torch, filler, ms: float = 20.0) -> None:
     the GPU and run back to back (events then time kernels, not the host)."""
     for _ in range(max(1, int(ms / 0.25))):
         filler.fill_(1)
+
+
+def time_launches(torch, filler, launch, reps: int) -> float:
+    """Average microseconds per launch of `launch(j)` over `reps` back-to-back
+    launches on the current stream, timed with HIP events behind a backlog."""
+    launch(0)
+    torch.cuda.synchronize()
+    enqueue_backlog(torch, filler)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for j in range(reps):
+        launch(j)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def hbm(nbytes: int, us: float) -> dict:
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"avg_us": round(us, 3), "bytes": nbytes, "GBps": round(gbs, 1),
+            "frac": round(gbs / PEAK_HBM_GBS, 4)}
 
 
 def main() -> int:
@@ -225,29 +251,126 @@ def main() -> int:
                 "kernel": f"gemv_int4_fast_kernel bf16 gate/up N={dom_n} K={dom_k}",
                 "bytes_per_launch": dom_bytes, "avg_us": round(kernel_us[dom_name], 3)}
 
-    # ---- FP8 E4M3 per-token quantizer (BASELINE cfg1) ----------------------
+    def stream_ptr() -> int:
+        return torch.cuda.current_stream().cuda_stream
+
+    def ck(status: int, name: str) -> None:
+        if status:
+            raise RuntimeError(f"{name}: {lib.kc_last_error_string().decode()}")
+
+    # ---- BASELINE cfg0: the reference-ABI GEMV (fp32 x and y), 4096 x 4096 --
+    n0 = k0 = 4096
+    c0_copies = max(2, math.ceil(ROTATE_BYTES / (n0 * k0 // 2)))
+    c0 = []
+    for _ in range(c0_copies):
+        c0.append((torch.randint(0, 256, (n0, k0 // 2), dtype=torch.uint8, device=dev, generator=gen),
+                   torch.empty(n0, k0 // GS, device=dev).uniform_(0.005, 0.02, generator=gen),
+                   torch.randint(0, 256, (n0, k0 // GS // 2), dtype=torch.uint8, device=dev,
+                                 generator=gen)))
+    x0 = torch.randn(k0, device=dev, generator=gen)
+    y0 = torch.empty(n0, device=dev)
+
+    def launch_cfg0(j: int) -> None:
+        p, sc, z = c0[j % c0_copies]
+        ck(lib.kc_gemv_int4_f32_async(p.data_ptr(), sc.data_ptr(), z.data_ptr(), x0.data_ptr(),
+                                      y0.data_ptr(), n0, k0, GS, stream_ptr()),
+           "kc_gemv_int4_f32_async")
+    cfg0 = hbm(gemv_bytes(n0, k0, xb=4, yb=4), time_launches(torch, filler, launch_cfg0, reps))
+    cfg0["config"] = "cfg0: INT4 GEMV M=1 N=K=4096 gs 128, fp32 x/y (reference ABI kernel)"
+    log(f"# cfg0 fp32 GEMV 4096x4096: {cfg0['avg_us']} us, {cfg0['GBps']} GB/s")
+    del c0
+
+    # ---- BASELINE cfg3: INT4 small-batch GEMM on MFMA, K 8192, N 28672 -----
+    n3, k3 = 28672, 8192
+    w3_bytes = n3 * k3 // 2 + n3 * (k3 // GS) * 4 + n3 * (k3 // GS) // 2
+    c3_copies = max(2, math.ceil(ROTATE_BYTES / w3_bytes))
+    c3 = []
+    for _ in range(c3_copies):
+        c3.append((torch.randint(0, 256, (n3, k3 // 2), dtype=torch.uint8, device=dev, generator=gen),
+                   torch.empty(n3, k3 // GS, device=dev).uniform_(0.005, 0.02, generator=gen),
+                   torch.randint(0, 256, (n3, k3 // GS // 2), dtype=torch.uint8, device=dev,
+                                 generator=gen)))
+    cfg3 = {}
+    for m in (4, 16, 64):
+        x3 = torch.randn(m, k3, device=dev, generator=gen).to(torch.bfloat16)
+        y3 = torch.empty(m, n3, dtype=torch.bfloat16, device=dev)
+
+        def launch_cfg3(j: int, m=m, x3=x3, y3=y3) -> None:
+            p, sc, z = c3[j % c3_copies]
+            ck(lib.kc_gemm_int4_bf16(p.data_ptr(), sc.data_ptr(), z.data_ptr(), x3.data_ptr(),
+                                     y3.data_ptr(), m, n3, k3, GS, stream_ptr()), "kc_gemm_int4_bf16")
+        nbytes = w3_bytes + m * k3 * 2 + m * n3 * 2
+        r = hbm(nbytes, time_launches(torch, filler, launch_cfg3, 50))
+        r["TFLOPs"] = round(2.0 * m * n3 * k3 / (r["avg_us"] * 1e-6) / 1e12, 2)
+        cfg3[f"M{m}"] = r
+        log(f"# cfg3 MFMA GEMM M={m:2d}: {r['avg_us']} us, {r['GBps']} GB/s, {r['TFLOPs']} TFLOP/s")
+    del c3
+
+    # ---- BASELINE cfg1: FP8 per-token X and per-channel W, fp32 [4096, 4096] -
     frows = fcols = 4096
     fcopies = max(2, math.ceil(ROTATE_BYTES / (frows * fcols * 4)))
     fx = [torch.randn(frows, fcols, device=dev, generator=gen) for _ in range(fcopies)]
+    outl = torch.randperm(fcols, device=dev, generator=gen)[:fcols // 100]
+    for t in fx:
+        t[:, outl] *= 50.0                      # 1 % outlier channels x50
     fq = torch.empty(frows, fcols, dtype=torch.int8, device=dev)
     fs = torch.empty(frows, dtype=torch.float32, device=dev)
     qfn = lib.kc_quantize_fp8_per_token_f32
-    for j in range(3):
-        qfn(fx[j % fcopies].data_ptr(), fq.data_ptr(), fs.data_ptr(), frows, fcols,
-            torch.cuda.current_stream().cuda_stream)
-    enqueue_backlog(torch, filler)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for j in range(reps):
-        qfn(fx[j % fcopies].data_ptr(), fq.data_ptr(), fs.data_ptr(), frows, fcols,
-            torch.cuda.current_stream().cuda_stream)
-    e1.record()
-    torch.cuda.synchronize()
-    fp8_us = e0.elapsed_time(e1) * 1e3 / reps
-    fp8_gbs = fp8_bytes(frows, fcols) / (fp8_us * 1e-6) / 1e9
-    log(f"# fp8 per-token [{frows}x{fcols}] fp32: {fp8_us:.2f} us, {fp8_gbs:.1f} GB/s")
-    del fx, filler
+
+    def launch_fp8(j: int, src=fx) -> None:
+        ck(qfn(src[j % len(src)].data_ptr(), fq.data_ptr(), fs.data_ptr(), frows, fcols,
+               stream_ptr()), "kc_quantize_fp8_per_token_f32")
+    fp8_x = hbm(fp8_bytes(frows, fcols), time_launches(torch, filler, launch_fp8, reps))
+    del fx
+    fw = [torch.randn(frows, fcols, device=dev, generator=gen) * 0.02 for _ in range(fcopies)]
+    fp8_w = hbm(fp8_bytes(frows, fcols),
+                time_launches(torch, filler, lambda j: launch_fp8(j, fw), reps))
+    del fw
+    fp8_us, fp8_gbs = fp8_x["avg_us"], fp8_x["GBps"]
+    log(f"# cfg1 fp8 per-token X [{frows}x{fcols}] fp32: {fp8_us} us, {fp8_gbs} GB/s; "
+        f"per-channel W: {fp8_w['avg_us']} us, {fp8_w['GBps']} GB/s")
+
+    # ---- BASELINE cfg4: SmoothQuant + FP8, X bf16 [16384, 8192], W bf16 [28672, 8192]
+    T4, D4, N4 = 16384, 8192, 28672
+    X4 = torch.randn(T4, D4, device=dev, generator=gen)
+    outl4 = torch.randperm(D4, device=dev, generator=gen)[:D4 // 200]
+    X4[:, outl4] *= 100.0                     # 0.5 % outlier channels x100
+    X4 = X4.to(torch.bfloat16)
+    W4 = (torch.randn(N4, D4, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+    ax, aw, sm = (torch.empty(D4, device=dev) for _ in range(3))
+    qx = torch.empty(T4, D4, dtype=torch.int8, device=dev)
+    qw = torch.empty(N4, D4, dtype=torch.int8, device=dev)
+    sx = torch.empty(T4, device=dev)
+    sw = torch.empty(N4, device=dev)
+
+    def cfg4_stats(j: int) -> None:
+        ck(lib.kc_col_absmax_bf16(X4.data_ptr(), ax.data_ptr(), T4, D4, stream_ptr()), "absmax X")
+        ck(lib.kc_col_absmax_bf16(W4.data_ptr(), aw.data_ptr(), N4, D4, stream_ptr()), "absmax W")
+        ck(lib.kc_smooth_factors(ax.data_ptr(), aw.data_ptr(), sm.data_ptr(), D4, stream_ptr()),
+           "smooth factors")
+
+    def cfg4_qx(j: int) -> None:
+        ck(lib.kc_quantize_fp8_smooth_div_bf16(X4.data_ptr(), sm.data_ptr(), qx.data_ptr(),
+                                               sx.data_ptr(), T4, D4, stream_ptr()), "quantize X")
+
+    def cfg4_qw(j: int) -> None:
+        ck(lib.kc_quantize_fp8_smooth_mul_bf16(W4.data_ptr(), sm.data_ptr(), qw.data_ptr(),
+                                               sw.data_ptr(), N4, D4, stream_ptr()), "quantize W")
+    stats_b = T4 * D4 * 2 + N4 * D4 * 2 + 2 * D4 * 4
+    qx_b = T4 * D4 * 2 + T4 * D4 + T4 * 4 + D4 * 4
+    qw_b = N4 * D4 * 2 + N4 * D4 + N4 * 4 + D4 * 4
+    t_stats = time_launches(torch, filler, cfg4_stats, 10)
+    t_qx = time_launches(torch, filler, cfg4_qx, 10)
+    t_qw = time_launches(torch, filler, cfg4_qw, 10)
+    fp8_cfg4 = {"stats": hbm(stats_b, t_stats), "quantize_x": hbm(qx_b, t_qx),
+                "quantize_w": hbm(qw_b, t_qw),
+                "total": hbm(stats_b + qx_b + qw_b, t_stats + t_qx + t_qw),
+                "config": "cfg4: col absmax X and W + smooth factors (alpha 0.5); X/s per-token "
+                          "and W*s per-channel to E4M3, bf16 in"}
+    log(f"# cfg4 smoothquant+fp8: stats {t_stats:.1f} us, X {t_qx:.1f} us "
+        f"({fp8_cfg4['quantize_x']['GBps']} GB/s), W {t_qw:.1f} us "
+        f"({fp8_cfg4['quantize_w']['GBps']} GB/s), total {fp8_cfg4['total']['GBps']} GB/s")
+    del X4, W4, qx, qw, filler
 
     # ---- CPU baseline: the oracle's scalar GEMV, one host thread ----------
     cpu = None
@@ -287,10 +410,16 @@ def main() -> int:
         "pct_of_peak": round(100.0 * value / PEAK_HBM_GBS, 2),
         "roofline": roofline,
         "kernel_us": {k: round(v, 3) for k, v in kernel_us.items()},
+        "kernel_GBps": {nm: round(gemv_bytes(n, k) / (kernel_us[nm] * 1e-6) / 1e9, 1)
+                        for nm, n, k in LLAMA},
         "fp8_quant": {"value": round(fp8_gbs, 1), "unit": "GB/s",
-                      "config": "per-token X fp32 [4096,4096]", "bytes_per_launch":
-                      fp8_bytes(frows, fcols), "avg_us": round(fp8_us, 3),
-                      "frac": round(fp8_gbs / PEAK_HBM_GBS, 4)},
+                      "config": "cfg1 per-token X fp32 [4096,4096], 1% outlier channels x50",
+                      "bytes_per_launch": fp8_bytes(frows, fcols), "avg_us": round(fp8_us, 3),
+                      "frac": round(fp8_gbs / PEAK_HBM_GBS, 4),
+                      "per_channel_w": fp8_w},
+        "fp8_cfg4": fp8_cfg4,
+        "gemv_cfg0": cfg0,
+        "gemm_cfg3": cfg3,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

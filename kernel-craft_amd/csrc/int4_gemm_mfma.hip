@@ -11,18 +11,32 @@
 //   B: 8 bf16 of X row i, same k-slots
 //   D: Y^T rows 4*kb + v (v = 0..3), column i
 // Any bijection between k-slots and real k that A and B share gives the same
-// contraction.  Each 128-k block is one lane-load of 16 bytes per W row (lane
-// (i, kb) reads bytes 16*kb .. 16*kb+15 of the block, 32 nibbles); MFMA step t
-// (t = 0..3) takes dword t, whose 8 nibbles become the bf16 pairs
-// (k0,k4) (k1,k5) (k2,k6) (k3,k7) -- exact values 128 + (q ^ 8), one bitwise
-// op each -- so the B operand holds X in the same pair order.
+// contraction.  A 128-k block ("T-block") of a 16-row tile is one 16-byte
+// load per lane (lane (i, kb) reads bytes 16*kb .. 16*kb+15 of the block of
+// row i, 32 nibbles); MFMA step t (t = 0..3) takes dword t, whose 8 nibbles
+// become the bf16 pairs (k0,k4) (k1,k5) (k2,k6) (k3,k7) -- exact values
+// 128 + (q ^ 8), one bitwise op each -- so the B operand holds X in the same
+// pair order.
 //
-// The block lies inside one quantization group (gs a multiple of 128), so
-// the block's MFMA sum C is folded into the fp32 accumulator as
-//     acc += s * (C - (136 + z) * sum_k X[m, k])
+// A T-block lies inside one quantization group (gs a multiple of 128), so
+// its MFMA sum C is folded into the fp32 accumulator as
+//     acc += s * C + c2 * sum_k X[m, k],   c2 = -s * (136 + z)
 // which removes the +128 encoding offset, the +8 of q ^ 8 and the zero point
 // exactly as the GEMV does.  Groups smaller than 128 fall back to the GEMV
 // per activation row.
+//
+// Work split.  A workgroup of NW waves owns 16*RT*NW consecutive weight rows
+// and the whole K; wave w owns row tiles w*RT .. w*RT+RT-1.  K is walked in
+// chunks of TPC T-blocks, software pipelined:
+//   * X of the next chunk is loaded, rearranged into the B-operand layout
+//     (with its T-block sums) and written to the other half of a
+//     double-buffered LDS area, together with that chunk's fold coefficients
+//     (s, c2) for the workgroup's rows -- one barrier per chunk;
+//   * X and the fold coefficients are loaded two chunks ahead and the
+//     weights one chunk ahead, so no load is waited for before a whole chunk
+//     period has passed.
+// Each B operand read from LDS serves RT row tiles, each decoded A operand
+// MT activation tiles.
 #include <algorithm>
 
 #include "kc_common.hpp"
@@ -33,153 +47,397 @@ using kc::kWave;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / kWave;
-constexpr int kKBlock = 128;  // k per block: 64 bytes of each W row
+constexpr int kTBlock = 128;  // k per T-block: 64 bytes of each W row
 
-__device__ __forceinline__ uint32_t nib_bf16_pair(uint32_t d) {
-    return ((d ^ 0x00080008u) & 0x000F000Fu) | 0x43004300u;
+// Nibble-decode constants in VGPRs (an SGPR operand halves VALU issue rate on
+// gfx950); the asm makes them opaque to the compiler.
+struct NibConsts {
+    uint32_t mask, magic;
+};
+
+__device__ __forceinline__ NibConsts nib_consts() {
+    NibConsts k;
+    asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(k.mask));
+    asm volatile("v_mov_b32 %0, 0x43084308" : "=v"(k.magic));
+    return k;
 }
 
-__device__ __forceinline__ bf16x8_t a_operand(uint32_t d) {
-    const u32x4 p{nib_bf16_pair(d), nib_bf16_pair(d >> 4), nib_bf16_pair(d >> 8),
-                  nib_bf16_pair(d >> 12)};
+// ((d ^ 0x00080008) & 0x000F000F) | 0x43004300 == (d & 0x000F000F) ^ 0x43084308
+__device__ __forceinline__ uint32_t nib_pair(uint32_t d, NibConsts k) { return (d & k.mask) ^ k.magic; }
+
+__device__ __forceinline__ bf16x8_t a_operand(uint32_t d, NibConsts k) {
+    const u32x4 p{nib_pair(d, k), nib_pair(d >> 4, k), nib_pair(d >> 8, k), nib_pair(d >> 12, k)};
     return __builtin_bit_cast(bf16x8_t, p);
 }
 
-__device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
+__device__ __forceinline__ bf16x2_t as_bf16x2(uint32_t v) { return __builtin_bit_cast(bf16x2_t, v); }
 
-// LDS image of one 128-k block of X: B operands bop[mt][t][lane] (16 bytes)
-// and the per-row block sums xsum[m].
-template <int MT>
-struct XBlock {
-    u32x4 bop[MT][4][kWave];
-    float xsum[MT * 16];
+// Workgroup shape.  64 weight rows (4 row tiles of 16) per workgroup; the
+// K dimension is split KW ways across its waves.  Wave w owns K part
+// q = w / (4/RT) and row tiles (w % (4/RT))*RT .. +RT-1.
+template <int MT, int RT, int KW, int TPC>
+struct GemmShape {
+    static constexpr int kRowGroups = 4 / RT;               // waves per K part
+    static constexpr int kNW = kRowGroups * KW;             // waves per workgroup
+    static constexpr int kThreadsWG = kNW * kWave;
+    static constexpr int kRowsWG = 64;
+    // LDS per chunk buffer
+    static constexpr int kXSlots = KW * MT * TPC * 4 * kWave;  // 16-byte B-operand slots
+    static constexpr int kXsum = KW * MT * TPC * 16;           // T-block sums of X per row
+    static constexpr int kCoef = KW * TPC * kRowsWG;           // s (and c2) per T-block and row
+    static constexpr int kBufBytes = kXSlots * 16 + kXsum * 4 + 2 * kCoef * 4;
+    // staging work per thread: X groups of 4 slots (one (q, t, mt, lane)
+    // each: the 4 MFMA steps of a T-block, 64 contiguous bytes of one X row)
+    // and fold coefficients
+    static constexpr int kXGroups = KW * MT * TPC * kWave;
+    static constexpr int kXItems = (kXGroups + kThreadsWG - 1) / kThreadsWG;
+    static constexpr int kCItems = (kCoef + kThreadsWG - 1) / kThreadsWG;
+    static_assert(TPC % 2 == 0, "T-blocks are computed in pairs");
 };
 
-// All 256 threads stage X[0 .. 16*MT) x [k0, k0 + 128) into `xb`.  Item
-// (m, u) is the 8-element slice k0 + 8u .. 8u + 7 of row m; it becomes the B
-// operand of step t = u % 4 for lane (m % 16) + 16 * (u / 4).  Rows >= M are
-// zero.  The 16 items of a row sit in 16 consecutive lanes for the row sum.
-template <int MT>
-__device__ __forceinline__ void stage_x_block(const uint16_t* __restrict__ X, int M, int K,
-                                              int k0, XBlock<MT>& xb) {
+// One chunk buffer in LDS.
+template <class S>
+struct ChunkLds {
+    u32x4* x;       // [KW][MT][TPC][4][64] B-operand slots
+    float* xsum;    // [KW][MT][TPC][16]
+    float* cs;      // [KW][TPC][64 rows]   s
+    float* cz;      // [KW][TPC][64 rows]   c2
+    __device__ ChunkLds(char* base) {
+        x = reinterpret_cast<u32x4*>(base);
+        xsum = reinterpret_cast<float*>(base + S::kXSlots * 16);
+        cs = xsum + S::kXsum;
+        cz = cs + S::kCoef;
+    }
+};
+
+// Raw loads of one chunk's X groups and fold coefficients (registers).
+template <class S>
+struct ChunkRaw {
+    u32x4 x[S::kXItems][4];
+    float s[S::kCItems];
+    uint32_t zb[S::kCItems];
+};
+
+// Position of the chunk's T-block t of K part q in the row.
+struct KSplit {
+    int nT;    // T-blocks per row
+    int nTq;   // T-blocks per K part
+    __device__ int T(int q, int T0, int t) const { return min(q * nTq + min(T0 + t, nTq - 1), nT - 1); }
+};
+
+// X group g -> (K part q, T-block t, m-tile mt, B lane l = j + 16*kb).  A
+// wave's 64 consecutive groups are the 64 lanes of one (q, t, mt): each of
+// its 4 LDS stores covers 64 consecutive 16-byte slots (no bank conflicts),
+// and the 4 lanes of one activation row (kb = 0..3) are lanes j, j+16, j+32,
+// j+48.
+template <int MT, int TPC>
+__device__ __forceinline__ void x_group(int g, int& q, int& t, int& mt, int& j, int& kb) {
+    const int l = g & (kWave - 1);
+    j = l & 15;
+    kb = l >> 4;
+    int r = g >> 6;
+    mt = r % MT;
+    r /= MT;
+    t = r % TPC;
+    q = r / TPC;
+}
+
+template <int MT, int RT, int KW, int TPC>
+__device__ __forceinline__ void load_chunk_raw(ChunkRaw<GemmShape<MT, RT, KW, TPC>>& raw,
+                                               const uint16_t* __restrict__ X,
+                                               const float* __restrict__ scales,
+                                               const uint8_t* __restrict__ zeros, int M, int N,
+                                               int K, int T0, KSplit ks, int nbase, int G,
+                                               int gshift) {
+    using S = GemmShape<MT, RT, KW, TPC>;
 #pragma unroll
-    for (int it = 0; it < MT; ++it) {
-        const int idx = it * kThreads + threadIdx.x;
-        const int m = idx >> 4, u = idx & 15;
-        u32x4 d{0u, 0u, 0u, 0u};
-        if (m < M) d = *reinterpret_cast<const u32x4*>(X + static_cast<int64_t>(m) * K + k0 + 8 * u);
-        u32x4 p;
-        p.x = (d.x & 0xFFFFu) | (d.z << 16);
-        p.y = (d.x >> 16) | (d.z & 0xFFFF0000u);
-        p.z = (d.y & 0xFFFFu) | (d.w << 16);
-        p.w = (d.y >> 16) | (d.w & 0xFFFF0000u);
-        xb.bop[m >> 4][u & 3][(m & 15) + 16 * (u >> 2)] = p;
-        float part = ((bf16_lo(d.x) + bf16_hi(d.x)) + (bf16_lo(d.y) + bf16_hi(d.y))) +
-                     ((bf16_lo(d.z) + bf16_hi(d.z)) + (bf16_lo(d.w) + bf16_hi(d.w)));
-        part += __shfl_xor(part, 1, kWave);
-        part += __shfl_xor(part, 2, kWave);
-        part += __shfl_xor(part, 4, kWave);
-        part += __shfl_xor(part, 8, kWave);
-        if (u == 0) xb.xsum[m] = part;
+    for (int u = 0; u < S::kXItems; ++u) {
+        const int g = threadIdx.x + u * S::kThreadsWG;
+        if (g >= S::kXGroups) break;  // uniform per wave: kXGroups is a multiple of 64
+        int q, t, mt, j, kb;
+        x_group<MT, TPC>(g, q, t, mt, j, kb);
+        const int m = 16 * mt + j;
+        const u32x4* src = reinterpret_cast<const u32x4*>(
+            X + static_cast<int64_t>(min(m, M - 1)) * K + ks.T(q, T0, t) * kTBlock + 32 * kb);
+#pragma unroll
+        for (int w4 = 0; w4 < 4; ++w4) raw.x[u][w4] = m < M ? src[w4] : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < S::kCItems; ++u) {
+        const int it = min(static_cast<int>(threadIdx.x) + u * S::kThreadsWG, S::kCoef - 1);
+        const int rw = it % S::kRowsWG, t = (it / S::kRowsWG) % TPC, q = it / (S::kRowsWG * TPC);
+        const int g = ks.T(q, T0, t) >> gshift;
+        const int64_t row = min(nbase + rw, N - 1);
+        raw.s[u] = scales[row * G + g];
+        raw.zb[u] = zeros[row * (G >> 1) + (g >> 1)];
     }
 }
 
-template <int MT>
-__global__ __launch_bounds__(kThreads) void gemm_int4_mfma_kernel(
-    const uint8_t* __restrict__ packed, const float* __restrict__ scales,
-    const uint8_t* __restrict__ zeros, const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
-    int M, int N, int K, int gshift) {
-    __shared__ XBlock<MT> xbuf[2];
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x >> 6;
-    const int li = lane & 15, kb = lane >> 4;
-    const int n0 = (blockIdx.x * kWaves + wave) * 16;
-    const int G = K >> (7 + gshift);  // gs = 128 << gshift
-    const int64_t rbytes = K >> 1;
-    // this lane's A row and the 4 D rows (4*kb + v) whose scale/zero it needs
-    const int64_t arow = std::min(n0 + li, N - 1);
-    const u32x4* wptr = reinterpret_cast<const u32x4*>(packed + arow * rbytes) + kb;
-    int64_t drow[4];
+template <int MT, int RT, int KW, int TPC>
+__device__ __forceinline__ void stage_chunk(const ChunkRaw<GemmShape<MT, RT, KW, TPC>>& raw,
+                                            ChunkLds<GemmShape<MT, RT, KW, TPC>> L, int T0,
+                                            KSplit ks, int gshift) {
+    using S = GemmShape<MT, RT, KW, TPC>;
+    uint32_t sel_lo, sel_hi;  // v_perm_b32 selectors, in VGPRs
+    asm volatile("v_mov_b32 %0, 0x05040100" : "=v"(sel_lo));
+    asm volatile("v_mov_b32 %0, 0x07060302" : "=v"(sel_hi));
+    const uint32_t ones = 0x3F803F80u;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) drow[v] = std::min(n0 + 4 * kb + v, N - 1);
-
-    f32x4 acc[MT];
+    for (int u = 0; u < S::kXItems; ++u) {
+        const int g = threadIdx.x + u * S::kThreadsWG;
+        if (g >= S::kXGroups) break;
+        int q, t, mt, j, kb;
+        x_group<MT, TPC>(g, q, t, mt, j, kb);
+        const int tile = (q * MT + mt) * TPC + t;
+        float sm = 0.0f;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    const int nblk = K / kKBlock;
-    stage_x_block<MT>(X, M, K, 0, xbuf[0]);
-    u32x4 wv = __builtin_nontemporal_load(wptr);
-    __syncthreads();
-    for (int b = 0; b < nblk; ++b) {
-        XBlock<MT>& cur = xbuf[b & 1];
-        u32x4 wnext = wv;
-        if (b + 1 < nblk) {
-            stage_x_block<MT>(X, M, K, (b + 1) * kKBlock, xbuf[(b + 1) & 1]);
-            wnext = __builtin_nontemporal_load(wptr + 4 * (b + 1));
+        for (int w4 = 0; w4 < 4; ++w4) {
+            const u32x4 d = raw.x[u][w4];
+            const uint32_t d0 = d.x, d1 = d.y, d2 = d.z, d3 = d.w;
+            u32x4 p;
+            p.x = __builtin_amdgcn_perm(d2, d0, sel_lo);  // (x0, x4)
+            p.y = __builtin_amdgcn_perm(d2, d0, sel_hi);  // (x1, x5)
+            p.z = __builtin_amdgcn_perm(d3, d1, sel_lo);  // (x2, x6)
+            p.w = __builtin_amdgcn_perm(d3, d1, sel_hi);  // (x3, x7)
+            L.x[(tile * 4 + w4) * kWave + j + 16 * kb] = p;
+            sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d0), as_bf16x2(ones), sm, false);
+            sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d1), as_bf16x2(ones), sm, false);
+            sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d2), as_bf16x2(ones), sm, false);
+            sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d3), as_bf16x2(ones), sm, false);
         }
-        const int g = (b * kKBlock) >> (7 + gshift);
-        float s[4], zc[4];
+        sm += __shfl_xor(sm, 16, kWave);  // the 4 k-quarters of the row's T-block
+        sm += __shfl_xor(sm, 32, kWave);
+        if (kb == 0) L.xsum[tile * 16 + j] = sm;
+    }
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            s[v] = scales[drow[v] * G + g];
-            const uint32_t zb = zeros[drow[v] * (G >> 1) + (g >> 1)];
-            zc[v] = -static_cast<float>(136u + ((g & 1) ? (zb >> 4) : (zb & 0xFu)));
+    for (int u = 0; u < S::kCItems; ++u) {
+        const int it = threadIdx.x + u * S::kThreadsWG;
+        if (it < S::kCoef) {
+            const int t = (it / S::kRowsWG) % TPC, q = it / (S::kRowsWG * TPC);
+            const int g = ks.T(q, T0, t) >> gshift;
+            const uint32_t z = (g & 1) ? (raw.zb[u] >> 4) : (raw.zb[u] & 0xFu);
+            L.cs[it] = raw.s[u];
+            L.cz[it] = -raw.s[u] * static_cast<float>(136u + z);
         }
-        f32x4 c[MT];
+    }
+}
+
+template <int MT, int RT>
+struct Acc {
+    f32x4 v[RT][MT];
+};
+
+// B operands of one T-block (4 MFMA steps x MT tiles) from LDS.
+template <int MT, int TPC>
+__device__ __forceinline__ void read_b(bf16x8_t (&b)[4][MT], const u32x4* x, int q, int t, int lane) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const uint32_t d = t == 0 ? wv.x : t == 1 ? wv.y : t == 2 ? wv.z : wv.w;
-            const bf16x8_t a = a_operand(d);
+    for (int w4 = 0; w4 < 4; ++w4)
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                const u32x4 bv = cur.bop[mt][t][lane];
-                const bf16x8_t bo = __builtin_bit_cast(bf16x8_t, bv);
-                c[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    a, bo, t == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : c[mt], 0, 0, 0);
+        for (int mt = 0; mt < MT; ++mt)
+            b[w4][mt] = __builtin_bit_cast(bf16x8_t, x[(((q * MT + mt) * TPC + t) * 4 + w4) * kWave + lane]);
+}
+
+// One chunk of MFMA work for this wave: weights w[rt][t] from registers, X
+// and coefficients from LDS.  T-blocks go in pairs so that two independent
+// accumulation chains interleave on the matrix core.
+template <int MT, int RT, int KW, int TPC>
+__device__ __forceinline__ void compute_chunk(Acc<MT, RT>& acc, const u32x4 (&w)[RT][TPC],
+                                              ChunkLds<GemmShape<MT, RT, KW, TPC>> L, int T0,
+                                              int nTq, int q, int rg, int lane, NibConsts nk) {
+    using S = GemmShape<MT, RT, KW, TPC>;
+    const int j = lane & 15, kb = lane >> 4;
+#pragma unroll
+    for (int tp = 0; tp < TPC; tp += 2) {
+        if (T0 + tp >= nTq) break;  // uniform: past the end of this K part
+        const bool second = T0 + tp + 1 < nTq;
+        bf16x8_t b[2][4][MT];
+        read_b<MT, TPC>(b[0], L.x, q, tp, lane);
+        read_b<MT, TPC>(b[1], L.x, q, tp + 1, lane);
+        f32x4 d[2][RT][MT];
+#pragma unroll
+        for (int w4 = 0; w4 < 4; ++w4) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    const u32x4 wv = w[rt][tp + h];
+                    const uint32_t wd = w4 == 0 ? wv.x : w4 == 1 ? wv.y : w4 == 2 ? wv.z : wv.w;
+                    const bf16x8_t a = a_operand(wd, nk);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+                        d[h][rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            a, b[h][w4][mt], w4 == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : d[h][rt][mt], 0, 0, 0);
+                }
             }
         }
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const float xs = cur.xsum[mt * 16 + li];
-            const f32x4 cm = c[mt];
-            f32x4 a4 = acc[mt];
-            a4.x = fmaf(s[0], fmaf(zc[0], xs, cm.x), a4.x);
-            a4.y = fmaf(s[1], fmaf(zc[1], xs, cm.y), a4.y);
-            a4.z = fmaf(s[2], fmaf(zc[2], xs, cm.z), a4.z);
-            a4.w = fmaf(s[3], fmaf(zc[3], xs, cm.w), a4.w);
-            acc[mt] = a4;
-        }
-        wv = wnext;
-        __syncthreads();
-    }
-    // lane holds Y[m = 16*mt + li][n0 + 4*kb + v]
+        for (int h = 0; h < 2; ++h) {
+            if (h == 1 && !second) break;
+            const int t = tp + h;
+            float xs[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const int m = mt * 16 + li;
-        if (m >= M) continue;
-        const f32x4 a4 = acc[mt];
-        const float vals[4] = {a4.x, a4.y, a4.z, a4.w};
+            for (int mt = 0; mt < MT; ++mt) xs[mt] = L.xsum[((q * MT + mt) * TPC + t) * 16 + j];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int n = n0 + 4 * kb + v;
-            if (n < N) Y[static_cast<int64_t>(m) * N + n] = kc::f32_to_bf16(vals[v]);
+            for (int rt = 0; rt < RT; ++rt) {
+                const int rw = (rg * RT + rt) * 16 + 4 * kb;
+                const int ci = (q * TPC + t) * S::kRowsWG + rw;
+                const f32x4 s4 = *reinterpret_cast<const f32x4*>(L.cs + ci);
+                const f32x4 z4 = *reinterpret_cast<const f32x4*>(L.cz + ci);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    f32x4 a = acc.v[rt][mt];
+                    const f32x4 c = d[h][rt][mt];
+                    a.x = fmaf(s4.x, c.x, fmaf(z4.x, xs[mt], a.x));
+                    a.y = fmaf(s4.y, c.y, fmaf(z4.y, xs[mt], a.y));
+                    a.z = fmaf(s4.z, c.z, fmaf(z4.z, xs[mt], a.z));
+                    a.w = fmaf(s4.w, c.w, fmaf(z4.w, xs[mt], a.w));
+                    acc.v[rt][mt] = a;
+                }
+            }
         }
     }
 }
 
-template <int MT>
-void launch_mfma(const uint8_t* packed, const float* scales, const uint8_t* zeros,
-                 const uint16_t* X, uint16_t* Y, int M, int N, int K, int gshift,
-                 hipStream_t stream) {
-    const unsigned grid = static_cast<unsigned>((N + 16 * kWaves - 1) / (16 * kWaves));
-    gemm_int4_mfma_kernel<MT><<<grid, kThreads, 0, stream>>>(packed, scales, zeros, X, Y, M, N, K,
-                                                             gshift);
+template <int RT, int TPC>
+__device__ __forceinline__ void load_weights(u32x4 (&w)[RT][TPC], const uint8_t* __restrict__ packed,
+                                             int N, int64_t rbytes, int nbase, int rg, int q,
+                                             int lane, int T0, KSplit ks) {
+    const int i = lane & 15, kb = lane >> 4;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const int64_t row = min(nbase + (rg * RT + rt) * 16 + i, N - 1);
+        const u32x4* prow = reinterpret_cast<const u32x4*>(packed + row * rbytes);
+#pragma unroll
+        for (int t = 0; t < TPC; ++t)
+            w[rt][t] = __builtin_nontemporal_load(prow + ks.T(q, T0, t) * 4 + kb);
+    }
+}
+
+template <int MT, int RT, int KW, int TPC>
+__global__ __launch_bounds__((4 / RT) * KW * kWave) void gemm_int4_mfma_kernel(
+    const uint8_t* __restrict__ packed, const float* __restrict__ scales,
+    const uint8_t* __restrict__ zeros, const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
+    int M, int N, int K, int gshift) {
+    using S = GemmShape<MT, RT, KW, TPC>;
+    extern __shared__ __align__(16) char lds[];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x >> 6;
+    const int q = wave / S::kRowGroups;             // K part
+    const int rg = wave % S::kRowGroups;            // row-tile group
+    const int nbase = blockIdx.x * S::kRowsWG;
+    KSplit ks;
+    ks.nT = K / kTBlock;
+    ks.nTq = ks.nT / KW;                            // the launcher checks KW divides nT
+    const int G = ks.nT >> gshift;                  // groups per row (gs = 128 << gshift)
+    const int64_t rbytes = K >> 1;
+    const int nchunks = (ks.nTq + TPC - 1) / TPC;
+    ChunkLds<S> buf[2] = {ChunkLds<S>(lds), ChunkLds<S>(lds + S::kBufBytes)};
+
+    Acc<MT, RT> acc;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc.v[rt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Pipeline: in iteration c the wave computes chunk c, while X (with the
+    // fold coefficients) of chunk c+2 and the weights of chunk c+1 are in
+    // flight; chunk c+1's X, loaded during iteration c-1, is staged into
+    // LDS at the end of the iteration.  Every load has a whole chunk period
+    // to arrive before anything waits for it.  Two iterations per loop trip
+    // let the register buffers alternate without copies.
+    ChunkRaw<S> raw0, raw1;
+    u32x4 w0[RT][TPC], w1[RT][TPC];
+    load_chunk_raw<MT, RT, KW, TPC>(raw0, X, scales, zeros, M, N, K, 0, ks, nbase, G, gshift);
+    if (nchunks > 1)
+        load_chunk_raw<MT, RT, KW, TPC>(raw1, X, scales, zeros, M, N, K, TPC, ks, nbase, G, gshift);
+    load_weights<RT, TPC>(w0, packed, N, rbytes, nbase, rg, q, lane, 0, ks);
+    stage_chunk<MT, RT, KW, TPC>(raw0, buf[0], 0, ks, gshift);
+    __syncthreads();
+    const NibConsts nk = nib_consts();
+
+    for (int c = 0; c < nchunks; c += 2) {
+        // chunk c: w0 / buf[0]; chunk c+1 staged from raw1; chunk c+2 -> raw0
+        const int T0 = c * TPC, T1 = T0 + TPC, T2 = T1 + TPC, T3 = T2 + TPC;
+        if (c + 2 < nchunks)
+            load_chunk_raw<MT, RT, KW, TPC>(raw0, X, scales, zeros, M, N, K, T2, ks, nbase, G, gshift);
+        if (c + 1 < nchunks) load_weights<RT, TPC>(w1, packed, N, rbytes, nbase, rg, q, lane, T1, ks);
+        compute_chunk<MT, RT, KW, TPC>(acc, w0, buf[0], T0, ks.nTq, q, rg, lane, nk);
+        if (c + 1 >= nchunks) break;
+        stage_chunk<MT, RT, KW, TPC>(raw1, buf[1], T1, ks, gshift);
+        __syncthreads();
+        // chunk c+1: w1 / buf[1]; chunk c+2 staged from raw0; chunk c+3 -> raw1
+        if (c + 3 < nchunks)
+            load_chunk_raw<MT, RT, KW, TPC>(raw1, X, scales, zeros, M, N, K, T3, ks, nbase, G, gshift);
+        if (c + 2 < nchunks) load_weights<RT, TPC>(w0, packed, N, rbytes, nbase, rg, q, lane, T2, ks);
+        compute_chunk<MT, RT, KW, TPC>(acc, w1, buf[1], T1, ks.nTq, q, rg, lane, nk);
+        if (c + 2 >= nchunks) break;
+        stage_chunk<MT, RT, KW, TPC>(raw0, buf[0], T2, ks, gshift);
+        __syncthreads();
+    }
+
+    // Sum the KW K parts in a fixed order (part 0 + part 1 + ...) through LDS.
+    if constexpr (KW > 1) {
+        __syncthreads();  // every wave is done reading the chunk buffers
+        f32x4* red = reinterpret_cast<f32x4*>(lds);   // [KW-1][row groups][RT*MT][64]
+        if (q > 0) {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    red[(((q - 1) * S::kRowGroups + rg) * RT * MT + rt * MT + mt) * kWave + lane] = acc.v[rt][mt];
+        }
+        __syncthreads();
+        if (q > 0) return;
+        for (int p = 1; p < KW; ++p) {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    acc.v[rt][mt] += red[(((p - 1) * S::kRowGroups + rg) * RT * MT + rt * MT + mt) * kWave + lane];
+        }
+    }
+
+    // lane (j, kb) holds Y[m = 16*mt + j][n = tile + 4*kb + v]
+    const int j = lane & 15, kb = lane >> 4;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int m = mt * 16 + j;
+            if (m >= M) continue;
+            const f32x4 a = acc.v[rt][mt];
+            const float vals[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int n = nbase + (rg * RT + rt) * 16 + 4 * kb + v;
+                if (n < N) Y[static_cast<int64_t>(m) * N + n] = kc::f32_to_bf16(vals[v]);
+            }
+        }
+    }
+}
+
+template <int MT, int RT, int KW, int TPC>
+int launch_mfma(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
+                const uint16_t* X, uint16_t* Y, int M, int N, int K, int gshift,
+                hipStream_t stream) {
+    using S = GemmShape<MT, RT, KW, TPC>;
+    constexpr size_t kLds = std::max<size_t>(2 * static_cast<size_t>(S::kBufBytes),
+                                             (KW - 1) * S::kRowGroups * RT * MT * kWave * 16);
+    static bool attr_set = false;  // launches above 64 KB of LDS need the attribute
+    if (kLds > 65536 && !attr_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_int4_mfma_kernel<MT, RT, KW, TPC>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(kLds)) != hipSuccess)
+            return kc::set_error(KC_ERR_HIP, "%s: cannot reserve %zu bytes of LDS", fn, kLds);
+        attr_set = true;
+    }
+    const unsigned grid = static_cast<unsigned>((N + S::kRowsWG - 1) / S::kRowsWG);
+    gemm_int4_mfma_kernel<MT, RT, KW, TPC><<<grid, S::kThreadsWG, kLds, stream>>>(
+        packed, scales, zeros, X, Y, M, N, K, gshift);
+    return kc::check_launch(fn);
 }
 
 }  // namespace
@@ -197,7 +455,7 @@ extern "C" int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
     if (m == 0 || rows == 0) return KC_SUCCESS;
     if (!d_y || (cols > 0 && (!d_packed || !d_scales || !d_zeros || !d_x)))
         return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: null device pointer", fn);
-    const bool fast = cols > 0 && cols % kKBlock == 0 && group_size % kKBlock == 0 &&
+    const bool fast = cols > 0 && cols % kTBlock == 0 && group_size % kTBlock == 0 &&
                       kc::is_pow2(group_size) && kc::aligned(d_packed, 16) &&
                       kc::aligned(d_x, 16);
     if (!fast) {
@@ -212,11 +470,14 @@ extern "C" int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
         return KC_SUCCESS;
     }
     const int gshift = kc::ilog2(group_size) - 7;
+    // m-tiles of 16 activation rows; with more of them each B operand read
+    // from LDS is reused across two weight row tiles.
+    // (KW = 1: measured on MI355X at K 8192, N 28672, splitting K across the
+    // waves of a workgroup was slower for every M.)
     switch ((m + 15) / 16) {
-        case 1: launch_mfma<1>(d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
-        case 2: launch_mfma<2>(d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
-        case 3: launch_mfma<3>(d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
-        default: launch_mfma<4>(d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+        case 1: return launch_mfma<1, 1, 1, 8>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream);
+        case 2: return launch_mfma<2, 1, 1, 4>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream);
+        case 3: return launch_mfma<3, 2, 1, 2>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream);
+        default: return launch_mfma<4, 2, 1, 2>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream);
     }
-    return kc::check_launch(fn);
 }
