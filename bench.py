@@ -72,19 +72,34 @@ def log(*a) -> None:
     print(*a, file=sys.stderr, flush=True)
 
 
-def enqueue_backlog(torch, filler, ms: float = 20.0) -> None:
-    """Queue ~`ms` of GPU work so the launches that follow are issued ahead of
-    the GPU and run back to back (events then time kernels, not the host)."""
-    for _ in range(max(1, int(ms / 0.25))):
-        filler.fill_(1)
+_SLEEP_CYCLES_PER_MS = None
 
 
-def time_launches(torch, filler, launch, reps: int) -> float:
+def enqueue_backlog(torch, ms: float = 20.0) -> None:
+    """Queue ~`ms` of idle GPU time (a spinning single-wave kernel) so the
+    launches that follow are issued ahead of the GPU and run back to back:
+    events then time kernels, not the host.  The backlog must not touch
+    memory: a bandwidth-heavy backlog (e.g. filling a large buffer) leaves
+    the HBM-bound kernels measured after it about 10 % slower."""
+    global _SLEEP_CYCLES_PER_MS
+    if _SLEEP_CYCLES_PER_MS is None:  # calibrate torch.cuda._sleep once
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        torch.cuda._sleep(1_000_000)
+        e1.record()
+        torch.cuda.synchronize()
+        _SLEEP_CYCLES_PER_MS = 1_000_000 / max(e0.elapsed_time(e1), 1e-3)
+    torch.cuda._sleep(int(_SLEEP_CYCLES_PER_MS * ms))
+
+
+def time_launches(torch, launch, reps: int) -> float:
     """Average microseconds per launch of `launch(j)` over `reps` back-to-back
     launches on the current stream, timed with HIP events behind a backlog."""
     launch(0)
     torch.cuda.synchronize()
-    enqueue_backlog(torch, filler)
+    enqueue_backlog(torch)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -227,11 +242,10 @@ def main() -> int:
         f"({'graph' if graphs is not None else 'eager'})")
 
     # ---- per-kernel durations with HIP events (launch stream, backlogged) ---
-    filler = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     reps = 100
     kernel_us = {}
     for i, (name, n, k) in enumerate(LLAMA):
-        enqueue_backlog(torch, filler)
+        enqueue_backlog(torch)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -275,7 +289,7 @@ def main() -> int:
         ck(lib.kc_gemv_int4_f32_async(p.data_ptr(), sc.data_ptr(), z.data_ptr(), x0.data_ptr(),
                                       y0.data_ptr(), n0, k0, GS, stream_ptr()),
            "kc_gemv_int4_f32_async")
-    cfg0 = hbm(gemv_bytes(n0, k0, xb=4, yb=4), time_launches(torch, filler, launch_cfg0, reps))
+    cfg0 = hbm(gemv_bytes(n0, k0, xb=4, yb=4), time_launches(torch, launch_cfg0, reps))
     cfg0["config"] = "cfg0: INT4 GEMV M=1 N=K=4096 gs 128, fp32 x/y (reference ABI kernel)"
     log(f"# cfg0 fp32 GEMV 4096x4096: {cfg0['avg_us']} us, {cfg0['GBps']} GB/s")
     del c0
@@ -300,7 +314,7 @@ def main() -> int:
             ck(lib.kc_gemm_int4_bf16(p.data_ptr(), sc.data_ptr(), z.data_ptr(), x3.data_ptr(),
                                      y3.data_ptr(), m, n3, k3, GS, stream_ptr()), "kc_gemm_int4_bf16")
         nbytes = w3_bytes + m * k3 * 2 + m * n3 * 2
-        r = hbm(nbytes, time_launches(torch, filler, launch_cfg3, 50))
+        r = hbm(nbytes, time_launches(torch, launch_cfg3, 50))
         r["TFLOPs"] = round(2.0 * m * n3 * k3 / (r["avg_us"] * 1e-6) / 1e12, 2)
         cfg3[f"M{m}"] = r
         log(f"# cfg3 MFMA GEMM M={m:2d}: {r['avg_us']} us, {r['GBps']} GB/s, {r['TFLOPs']} TFLOP/s")
@@ -320,11 +334,11 @@ def main() -> int:
     def launch_fp8(j: int, src=fx) -> None:
         ck(qfn(src[j % len(src)].data_ptr(), fq.data_ptr(), fs.data_ptr(), frows, fcols,
                stream_ptr()), "kc_quantize_fp8_per_token_f32")
-    fp8_x = hbm(fp8_bytes(frows, fcols), time_launches(torch, filler, launch_fp8, reps))
+    fp8_x = hbm(fp8_bytes(frows, fcols), time_launches(torch, launch_fp8, reps))
     del fx
     fw = [torch.randn(frows, fcols, device=dev, generator=gen) * 0.02 for _ in range(fcopies)]
     fp8_w = hbm(fp8_bytes(frows, fcols),
-                time_launches(torch, filler, lambda j: launch_fp8(j, fw), reps))
+                time_launches(torch, lambda j: launch_fp8(j, fw), reps))
     del fw
     fp8_us, fp8_gbs = fp8_x["avg_us"], fp8_x["GBps"]
     log(f"# cfg1 fp8 per-token X [{frows}x{fcols}] fp32: {fp8_us} us, {fp8_gbs} GB/s; "
@@ -359,9 +373,9 @@ def main() -> int:
     stats_b = T4 * D4 * 2 + N4 * D4 * 2 + 2 * D4 * 4
     qx_b = T4 * D4 * 2 + T4 * D4 + T4 * 4 + D4 * 4
     qw_b = N4 * D4 * 2 + N4 * D4 + N4 * 4 + D4 * 4
-    t_stats = time_launches(torch, filler, cfg4_stats, 10)
-    t_qx = time_launches(torch, filler, cfg4_qx, 10)
-    t_qw = time_launches(torch, filler, cfg4_qw, 10)
+    t_stats = time_launches(torch, cfg4_stats, 10)
+    t_qx = time_launches(torch, cfg4_qx, 10)
+    t_qw = time_launches(torch, cfg4_qw, 10)
     fp8_cfg4 = {"stats": hbm(stats_b, t_stats), "quantize_x": hbm(qx_b, t_qx),
                 "quantize_w": hbm(qw_b, t_qw),
                 "total": hbm(stats_b + qx_b + qw_b, t_stats + t_qx + t_qw),
@@ -370,7 +384,7 @@ def main() -> int:
     log(f"# cfg4 smoothquant+fp8: stats {t_stats:.1f} us, X {t_qx:.1f} us "
         f"({fp8_cfg4['quantize_x']['GBps']} GB/s), W {t_qw:.1f} us "
         f"({fp8_cfg4['quantize_w']['GBps']} GB/s), total {fp8_cfg4['total']['GBps']} GB/s")
-    del X4, W4, qx, qw, filler
+    del X4, W4, qx, qw
 
     # ---- CPU baseline: the oracle's scalar GEMV, one host thread ----------
     cpu = None
