@@ -65,11 +65,12 @@ __device__ __forceinline__ float row_scale(float amax) {
 // computed once per row by a correctly rounded division, Markstein's
 // correction step
 //     q0 = RN(x * r),   e = x - s * q0 (exact: one FMA),   q = RN(q0 + e * r)
-// returns RN(x / s) whenever the residual e is exactly representable, which
-// holds for |x| >= 2^-103 (no underflow in e).  It is used for rows with
-// 2^-60 <= absmax <= FLT_MAX: there r is a normal number, and every element
-// with |x| < 2^-103 has |x/s| < 2^-34, far below the smallest E4M3 step
-// (2^-9), so its code is +0 or -0 on both routes; copysign carries the sign
+// returns RN(x / s) whenever the residual e is exactly representable and the
+// quotient is a normal number, which holds for |x| >= 2^-103 and
+// |x/s| >= 2^-126.  It is used for rows with 2^-60 <= absmax <= FLT_MAX:
+// there r is a normal number, and every other element (|x| < 2^-103 gives
+// |x/s| < 2^-34) has a quotient far below the smallest E4M3 step (2^-9), so
+// its code is +0 or -0 on both routes; copysign carries the sign
 // of x through, including -0 (the FMA steps would turn -0 into +0).  Other
 // rows (all-tiny or non-finite absmax) divide exactly.  Three VALU operations
 // instead of the ~10 of a correctly rounded division per element.

@@ -7,9 +7,9 @@
  * r = RN(1/s),
  *     q0 = RN(x*r);  e = RN(x - s*q0) (one FMA);  q = copysign(RN(q0 + e*r), x)
  * for rows with 2^-60 <= absmax <= FLT_MAX.  Claim checked here, for such s:
- *   (a) |x| >= 2^-103:  q == RN(x/s) bit for bit;
- *   (b) |x| <  2^-103:  |q| < 2^-30 and |RN(x/s)| < 2^-30 with the sign of x
- *       (both encode to E4M3 +-0, whose smallest nonzero step is 2^-9).
+ *   (a) |x| >= 2^-103 and RN(x/s) normal:  q == RN(x/s) bit for bit;
+ *   (b) otherwise:  |q| < 2^-30 and |RN(x/s)| < 2^-30, both with the sign of
+ *       x (both encode to E4M3 +-0, whose smallest nonzero step is 2^-9).
  *
  * usage: markstein_check <mode> <n> <seed>
  *   mode 0: n random rows' scales (absmax from a wide exponent range and
@@ -44,7 +44,7 @@ static long check(float x, float absmax) {
     if (isnan(x) || fabsf(x) > absmax) return 0;  /* a row never holds |x| > absmax */
     const float s = absmax / 448.0f, r = 1.0f / s;
     const float want = x / s, got = kernel_div(x, s, r);
-    if (fabsf(x) >= 0x1p-103f) {
+    if (fabsf(x) >= 0x1p-103f && fabsf(want) >= 0x1p-126f) {
         if (f_to_bits(want) != f_to_bits(got)) {
             fprintf(stderr, "absmax=%a x=%a: x/s=%a kernel=%a\n", absmax, x, want, got);
             return 1;

@@ -85,6 +85,81 @@ def test_per_token_shapes(gpu, oracle, rows, cols):
     _assert_codes_equal(q, eq)
 
 
+def _per_token_bf16(torch, xb, smooth=None, mode="none"):
+    """kc_quantize_fp8_per_token_bf16 / _smooth_div_bf16 / _smooth_mul_bf16 on
+    bf16 bits xb [rows, cols]; returns (codes, scales) on the host."""
+    rows, cols = xb.shape
+    L = kc_abi.lib()
+    dx = _dev_bf16(torch, xb)
+    dq = torch.full((rows, cols), 0x55, dtype=torch.int8, device="cuda")
+    ds = torch.full((max(rows, 1),), float("nan"), dtype=torch.float32, device="cuda")
+    print(f"fp8 bf16 {mode} rows={rows} cols={cols}", flush=True)
+    if mode == "none":
+        st = L.kc_quantize_fp8_per_token_bf16(ptr(dx), ptr(dq), ptr(ds), rows, cols, stream())
+    else:
+        dsm = _dev(torch, smooth)
+        fn = L.kc_quantize_fp8_smooth_div_bf16 if mode == "div" else L.kc_quantize_fp8_smooth_mul_bf16
+        st = fn(ptr(dx), ptr(dsm), ptr(dq), ptr(ds), rows, cols, stream())
+    kc_abi.check(f"fp8 bf16 {mode}", st)
+    torch.cuda.synchronize()
+    return dq.cpu().numpy(), ds.cpu().numpy()[:rows]
+
+
+# bf16 rows: one wave per row with 1, 2, 4, 8 and 16 slots per lane (up to
+# D = 8192, partial last slots included), one workgroup per row (8200, 16384),
+# and the generic two-pass kernel (odd D, D > 16384).
+BF16_SHAPES = [(3, 8), (2, 72), (3, 520), (2, 1024), (2, 2056), (2, 4096), (3, 8192),
+               (2, 8200), (2, 16384), (2, 20000), (3, 7), (2, 1001)]
+
+
+@pytest.mark.parametrize("rows,cols", BF16_SHAPES)
+def test_per_token_bf16_shapes(gpu, oracle, rows, cols):
+    x, _ = outlier_activations(rows, cols, 0.01, 50.0, seed=rows * 7919 + cols)
+    xb = f32_to_bf16_bits(x)
+    q, s = _per_token_bf16(gpu, xb)
+    eq, es = oracle.quantize_fp8_per_token_bf16(xb)
+    np.testing.assert_array_equal(s.view(np.uint32), es.view(np.uint32))
+    _assert_codes_equal(q, eq)
+
+
+@pytest.mark.parametrize("rows,cols", [(2, 520), (3, 4096), (2, 8192), (2, 8200), (2, 20000)])
+@pytest.mark.parametrize("mode", ["div", "mul"])
+def test_smooth_bf16_shapes(gpu, oracle, rows, cols, mode):
+    x, _ = outlier_activations(rows, cols, 0.005, 100.0, seed=rows * 131 + cols)
+    xb = f32_to_bf16_bits(x)
+    sm = np.random.default_rng(cols).uniform(0.05, 30.0, cols).astype(np.float32)
+    q, s = _per_token_bf16(gpu, xb, sm, mode)
+    if mode == "div":
+        eq, es = oracle.quantize_fp8_smooth_div(xb, sm)
+    else:
+        eq, es = oracle.quantize_fp8_smooth_mul_bf16(xb, sm)
+    np.testing.assert_array_equal(s.view(np.uint32), es.view(np.uint32))
+    _assert_codes_equal(q, eq)
+
+
+def test_per_token_bf16_special_values(gpu, oracle):
+    """bf16 rows with zeros, -0, NaN, inf, denormals and tiny absmax values
+    (the scale routes that divide exactly) through the one-wave kernel."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((10, 512)).astype(np.float32)
+    x[0] = 0.0
+    x[1] = -0.0
+    x[2, ::5] = np.nan
+    x[3, 7] = np.inf
+    x[4] = np.float32(2.0 ** -130) * np.sign(rng.standard_normal(512)).astype(np.float32)  # denormal bf16
+    x[5] = np.float32(2.0 ** -70) * rng.standard_normal(512).astype(np.float32)          # absmax < 2^-60
+    x[6] = np.float32(3e38) * rng.uniform(-1, 1, 512).astype(np.float32)
+    x[7, :] = np.nan
+    x[8] = np.float32(2.0 ** -100) * rng.standard_normal(512).astype(np.float32)
+    x[8, 3] = 1.0                                # tiny elements under a normal absmax
+    x[9] = np.float32(2.0) ** rng.integers(-40, 40, 512).astype(np.float32)
+    xb = f32_to_bf16_bits(x)
+    q, s = _per_token_bf16(gpu, xb)
+    eq, es = oracle.quantize_fp8_per_token_bf16(xb)
+    np.testing.assert_array_equal(s.view(np.uint32), es.view(np.uint32))
+    _assert_codes_equal(q, eq)
+
+
 def test_per_token_special_values(gpu, oracle):
     rng = np.random.default_rng(7)
     x = rng.standard_normal((15, 256)).astype(np.float32)

@@ -1,7 +1,8 @@
 """The FP8 quantizer divides by the row scale with Markstein's correction step
 instead of an IEEE division (fp8_quant.hip, row_div).  This pins that the two
-give the same E4M3 codes: bitwise-equal quotients for |x| >= 2^-103 and
-same-sign values far below the smallest E4M3 step otherwise.  The check is a
+give the same E4M3 codes: bitwise-equal quotients for |x| >= 2^-103 when
+the quotient is a normal number, and same-sign values far below the smallest
+E4M3 step otherwise.  The check is a
 C program (tests/csrc/markstein_check.c) built with gcc, because numpy has no
 fused multiply-add.  KC_SLOW=1 adds exhaustive sweeps over all 2^32 x for six
 scales (about a minute each)."""
