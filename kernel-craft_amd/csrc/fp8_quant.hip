@@ -402,7 +402,8 @@ __global__ __launch_bounds__(kThreads) void smooth_div_kernel(
 // max (non-negative fp32 values order like their bit patterns; fmaxf from 0
 // keeps NaN out).  d_amax is cleared by a fill kernel first.
 // ---------------------------------------------------------------------------
-constexpr int kAbsmaxRowsPerBlock = 64;
+constexpr int kAbsmaxRowsPerBlock = 256;
+constexpr int kAbsmaxUnroll = 4;  // row loads in flight per thread
 
 __global__ __launch_bounds__(kThreads) void fill_zero_kernel(float* __restrict__ p, int64_t n) {
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
@@ -410,48 +411,84 @@ __global__ __launch_bounds__(kThreads) void fill_zero_kernel(float* __restrict__
         p[i] = 0.0f;
 }
 
+// A block covers a band of kAbsmaxRowsPerBlock rows and 32 16-byte column
+// slots (256 bf16 or 128 fp32 columns).  Thread t reads slot t % 32 of rows
+// t / 32, t / 32 + 8, ... (kAbsmaxUnroll loads in flight); the 8 row groups
+// are max-reduced in LDS and each column gets one atomicMax per band.  The
+// atomics, not the loads, limited the first version (64-row bands): the
+// fewer per column, the faster.
 template <bool BF16>
 __global__ __launch_bounds__(kThreads) void col_absmax_kernel(const void* __restrict__ in,
                                                               float* __restrict__ amax,
                                                               int64_t rows, int64_t cols,
-                                                              int64_t tiles_per_row, bool vec) {
-    const int64_t band = blockIdx.x / tiles_per_row;
-    const int64_t tile = blockIdx.x - band * tiles_per_row;
-    const int64_t c = tile * 1024 + 4 * static_cast<int64_t>(threadIdx.x);
+                                                              int64_t tiles_per_band, bool vec) {
+    constexpr int kVals = BF16 ? 8 : 4;              // columns per 16-byte slot
+    constexpr int kTileCols = 32 * kVals;
+    __shared__ float red[8][kTileCols];
+    const int64_t band = blockIdx.x / tiles_per_band;
+    const int64_t tile = blockIdx.x - band * tiles_per_band;
+    const int cg = threadIdx.x & 31, rg = threadIdx.x >> 5;
+    const int64_t c = tile * kTileCols + cg * kVals;
     const int64_t r0 = band * kAbsmaxRowsPerBlock;
     const int64_t r1 = std::min(r0 + kAbsmaxRowsPerBlock, rows);
-    float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f;
-    if (vec && c + 4 <= cols) {
-        for (int64_t r = r0; r < r1; ++r) {
-            f32x4 v;
-            if constexpr (BF16) {
-                const u32x2 d = __builtin_nontemporal_load(
-                    reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(in) + r * cols + c));
-                v = bf16x4_to_f32(d.x, d.y);
-            } else {
-                v = __builtin_nontemporal_load(
-                    reinterpret_cast<const f32x4*>(static_cast<const float*>(in) + r * cols + c));
+    float m[kVals];
+#pragma unroll
+    for (int k = 0; k < kVals; ++k) m[k] = 0.0f;
+    if (vec && c + kVals <= cols) {
+        for (int64_t r = r0 + rg; r < r1; r += 8 * kAbsmaxUnroll) {
+            u32x4 d[kAbsmaxUnroll];
+#pragma unroll
+            for (int u = 0; u < kAbsmaxUnroll; ++u) {  // rows past the band re-read its last row
+                const int64_t rr = std::min(r + 8 * u, r1 - 1);
+                const char* base = static_cast<const char*>(in) + (rr * cols + c) * (BF16 ? 2 : 4);
+                d[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base));
             }
-            m0 = fmaxf(m0, fabsf(v.x));
-            m1 = fmaxf(m1, fabsf(v.y));
-            m2 = fmaxf(m2, fabsf(v.z));
-            m3 = fmaxf(m3, fabsf(v.w));
+#pragma unroll
+            for (int u = 0; u < kAbsmaxUnroll; ++u) {
+                // quieted: a signaling NaN must not win the max
+                if constexpr (BF16) {
+                    const f32x4 v0 = quiet4(bf16x4_to_f32(d[u].x, d[u].y));
+                    const f32x4 v1 = quiet4(bf16x4_to_f32(d[u].z, d[u].w));
+                    m[0] = fmaxf(m[0], fabsf(v0.x));
+                    m[1] = fmaxf(m[1], fabsf(v0.y));
+                    m[2] = fmaxf(m[2], fabsf(v0.z));
+                    m[3] = fmaxf(m[3], fabsf(v0.w));
+                    m[4] = fmaxf(m[4], fabsf(v1.x));
+                    m[5] = fmaxf(m[5], fabsf(v1.y));
+                    m[6] = fmaxf(m[6], fabsf(v1.z));
+                    m[7] = fmaxf(m[7], fabsf(v1.w));
+                } else {
+                    const f32x4 v0 = quiet4(__builtin_bit_cast(f32x4, d[u]));
+                    m[0] = fmaxf(m[0], fabsf(v0.x));
+                    m[1] = fmaxf(m[1], fabsf(v0.y));
+                    m[2] = fmaxf(m[2], fabsf(v0.z));
+                    m[3] = fmaxf(m[3], fabsf(v0.w));
+                }
+            }
         }
-        atomicMax(reinterpret_cast<unsigned int*>(amax) + c, __float_as_uint(m0));
-        atomicMax(reinterpret_cast<unsigned int*>(amax) + c + 1, __float_as_uint(m1));
-        atomicMax(reinterpret_cast<unsigned int*>(amax) + c + 2, __float_as_uint(m2));
-        atomicMax(reinterpret_cast<unsigned int*>(amax) + c + 3, __float_as_uint(m3));
     } else {
-        for (int64_t k = c; k < std::min(c + 4, cols); ++k) {
-            float m = 0.f;
-            for (int64_t r = r0; r < r1; ++r) {
+        // unaligned input, or the partial last slot of a row
+        for (int64_t r = r0 + rg; r < r1; r += 8) {
+#pragma unroll
+            for (int k = 0; k < kVals; ++k) {
+                if (c + k >= cols) break;
                 float v;
-                if constexpr (BF16) v = kc::bf16_to_f32(static_cast<const uint16_t*>(in)[r * cols + k]);
-                else v = static_cast<const float*>(in)[r * cols + k];
-                m = fmaxf(m, fabsf(v));
+                if constexpr (BF16) v = kc::bf16_to_f32(static_cast<const uint16_t*>(in)[r * cols + c + k]);
+                else v = static_cast<const float*>(in)[r * cols + c + k];
+                m[k] = fmaxf(m[k], fabsf(quiet(v)));
             }
-            atomicMax(reinterpret_cast<unsigned int*>(amax) + k, __float_as_uint(m));
         }
+    }
+#pragma unroll
+    for (int k = 0; k < kVals; ++k) red[rg][cg * kVals + k] = m[k];
+    __syncthreads();
+    for (int col = threadIdx.x; col < kTileCols; col += kThreads) {
+        const int64_t gc = tile * kTileCols + col;
+        if (gc >= cols) break;
+        float v = red[0][col];
+#pragma unroll
+        for (int g = 1; g < 8; ++g) v = fmaxf(v, red[g][col]);
+        atomicMax(reinterpret_cast<unsigned int*>(amax) + gc, __float_as_uint(v));
     }
 }
 
@@ -614,11 +651,12 @@ int col_absmax(const char* fn, const void* in, float* amax, int64_t rows, int64_
     fill_zero_kernel<<<static_cast<unsigned>(fill_blocks), kThreads, 0, stream>>>(amax, cols);
     if ((st = kc::check_launch(fn)) != KC_SUCCESS) return st;
     if (rows == 0) return KC_SUCCESS;
-    const int64_t tiles = (cols + 1023) / 1024;
+    constexpr int64_t kCols = 32 * (BF16 ? 8 : 4);  // columns per block
+    const int64_t tiles = (cols + kCols - 1) / kCols;
     const int64_t bands = (rows + kAbsmaxRowsPerBlock - 1) / kAbsmaxRowsPerBlock;
     if (bands * tiles > INT32_MAX)
         return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: tensor too large", fn);
-    const bool vec = cols % 4 == 0 && (BF16 ? kc::aligned(in, 8) : kc::aligned(in, 16));
+    const bool vec = cols % (BF16 ? 8 : 4) == 0 && kc::aligned(in, 16);
     col_absmax_kernel<BF16><<<static_cast<unsigned>(bands * tiles), kThreads, 0, stream>>>(
         in, amax, rows, cols, tiles, vec);
     return kc::check_launch(fn);

@@ -362,6 +362,37 @@ def _smooth_pipeline(torch, xb, wb):
     return ax, aw, s, qx, sx, qw, sw
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("rows,cols", [(1, 8), (130, 2048), (257, 4104), (64, 1000), (300, 20), (7, 16392)])
+def test_col_absmax_shapes(gpu, oracle, dtype, rows, cols):
+    """Column absmax (SmoothQuant statistics) over band and tile tails, the
+    scalar path (cols not a multiple of the 16-byte slot) and special values:
+    NaN and signaling NaN are ignored, inf wins, -0 counts as 0."""
+    torch = gpu
+    rng = np.random.default_rng(rows * 31 + cols)
+    x = (rng.standard_normal((rows, cols)) * rng.uniform(0.1, 50.0, cols)).astype(np.float32)
+    x[rng.integers(0, rows, 5), rng.integers(0, cols, 5)] = np.nan
+    snan = np.array([0x7F800001, 0xFFA00000], np.uint32).view(np.float32)
+    x[rows - 1, 0] = snan[0]
+    x[0, cols - 1] = snan[1]
+    if cols > 3:
+        x[:, 3] = -0.0
+        x[rows // 2, 2] = -np.inf
+    L = kc_abi.lib()
+    out = torch.full((cols,), float("nan"), dtype=torch.float32, device="cuda")
+    if dtype == "bf16":
+        xb = f32_to_bf16_bits(x)
+        dx = _dev_bf16(torch, xb)
+        st = L.kc_col_absmax_bf16(ptr(dx), ptr(out), rows, cols, stream())
+        exp = oracle.col_absmax(xb)
+    else:
+        dx = _dev(torch, x)
+        st = L.kc_col_absmax_f32(ptr(dx), ptr(out), rows, cols, stream())
+        exp = oracle.col_absmax(x)
+    kc_abi.check("col_absmax", st)
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), exp.view(np.uint32))
+
+
 def test_smoothquant_fused_small(gpu, oracle):
     """cfg4 distributions at a size the oracle runs in seconds; every output
     bit-exact (absmax, factors, codes, scales)."""
