@@ -52,6 +52,15 @@ __device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
     return static_cast<uint32_t>(v);
 }
 
+// The same for NaN-free input: the clamp is one median (v_med3_f32, which
+// would not map NaN to +448).
+__device__ __forceinline__ uint32_t e4m3x4_finite(float a, float b, float c, float d) {
+    auto clamp = [](float v) { return __builtin_amdgcn_fmed3f(v, -kE4M3Max, kE4M3Max); };
+    int v = __builtin_amdgcn_cvt_pk_fp8_f32(clamp(a), clamp(b), 0, false);
+    v = __builtin_amdgcn_cvt_pk_fp8_f32(clamp(c), clamp(d), v, true);
+    return static_cast<uint32_t>(v);
+}
+
 __device__ __forceinline__ uint8_t e4m3x1(float a) {
     return static_cast<uint8_t>(__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(a), 0.0f, 0, false) & 0xFF);
 }
@@ -64,16 +73,16 @@ __device__ __forceinline__ float row_scale(float amax) {
 // row's scale with an IEEE division (fp8_quant.cu:126).  With r = RN(1/s),
 // computed once per row by a correctly rounded division, Markstein's
 // correction step
-//     q0 = RN(x * r),   e = x - s * q0 (exact: one FMA),   q = RN(q0 + e * r)
-// returns RN(x / s) whenever the residual e is exactly representable and the
-// quotient is a normal number, which holds for |x| >= 2^-103 and
-// |x/s| >= 2^-126.  It is used for rows with 2^-60 <= absmax <= FLT_MAX:
-// there r is a normal number, and every other element (|x| < 2^-103 gives
-// |x/s| < 2^-34) has a quotient far below the smallest E4M3 step (2^-9), so
-// its code is +0 or -0 on both routes; copysign carries the sign
-// of x through, including -0 (the FMA steps would turn -0 into +0).  Other
-// rows (all-tiny or non-finite absmax) divide exactly.  Three VALU operations
-// instead of the ~10 of a correctly rounded division per element.
+//     q0 = RN(x * r),   e = RN(s * q0 - x) (one FMA),   q = RN(q0 - e * r)
+// returns RN(x / s) whenever the residual is exactly representable and the
+// quotient is a normal number, which holds for |x| >= 2^-102 and
+// |x/s| >= 2^-126 when r is normal.  Every other finite x gets a q with the
+// sign of x (zeros included: -0 gives -0) and |q| <= 2^-102/s + 2^-125.
+// The row route uses it for rows with 2^-60 <= absmax <= FLT_MAX: there r is
+// normal, and an element with |x| < 2^-102 has |x/s| < 2^-33, far below the
+// smallest E4M3 step (2^-9), so its code is +0 or -0 with the sign of x on
+// both routes.  Other rows (all-tiny or non-finite absmax) divide exactly.
+// Three VALU operations instead of the ~10 of a correctly rounded division.
 struct RowDiv {
     float s;      // row scale
     float r;      // RN(1 / s)
@@ -88,15 +97,17 @@ __device__ __forceinline__ RowDiv row_div(float amax) {
     return d;
 }
 
+// RN(x / s) for the element ranges stated above; r = RN(1/s).
+__device__ __forceinline__ float markstein(float x, float s, float r) {
+    const float q0 = __fmul_rn(x, r);
+    const float e = fmaf(s, q0, -x);
+    return fmaf(-e, r, q0);
+}
+
 template <bool FAST>
 __device__ __forceinline__ float div_scale(float x, const RowDiv& d) {
-    if constexpr (FAST) {
-        const float q0 = __fmul_rn(x, d.r);
-        const float e = fmaf(-d.s, q0, x);
-        return copysignf(fmaf(e, d.r, q0), x);
-    } else {
-        return x / d.s;
-    }
+    if constexpr (FAST) return markstein(x, d.s, d.r);
+    else return x / d.s;
 }
 
 template <bool FAST>
@@ -287,6 +298,254 @@ __global__ __launch_bounds__(kWave) void quant_rows_wave_kernel(
     };
     if (d.fast) emit(std::true_type{});
     else emit(std::false_type{});
+}
+
+// ---------------------------------------------------------------------------
+// SmoothQuant quantizer, persistent: one 256-thread workgroup per row, the
+// grid sized to what the device holds at once; workgroup b takes rows b,
+// b + G, b + 2G, ...  Thread t owns the 16-byte column slots t, t + 256, ...
+// (NV of them).  Its smoothing factors (and, for the division, their
+// reciprocals) are loaded once and stay in registers, so the factor vector
+// is read once per workgroup instead of once per row; the slots of the next
+// P-1 rows are in flight while a row is reduced and written.
+//
+// Division by the factors (fp8_quant.cu:183) uses the same Markstein step as
+// the row scale (markstein() above).  It returns RN(x / s) for |x| >= 2^-102
+// and a normal quotient when s lies in [2^-120, 2^120] (then r is normal),
+// and a quotient with the sign of x otherwise.  Every inexact finite element
+// has |q| and |x / s| below Q = max(2^-101 / s_min, 2^-125).  A row keeps
+// these quotients when the maximum of their magnitude bits (an integer
+// maximum, so a NaN or an infinity -- which only a non-finite x or an
+// overflowing quotient produce -- exceeds every finite value) lies in
+// [T, 2^126] with T = max(2^-60, 2^20 Q): the maximum is then an exact
+// element, so the row scale is the reference's, and every inexact element is
+// below 2^-20 absmax and encodes to +-0 with the sign of x on both routes.
+// Such a row has no NaN, so the clamp to +-448 is one median.  Other rows are
+// recomputed with IEEE divisions.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+        v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off, kWave)));
+    return v;
+}
+
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fminf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+__device__ __forceinline__ uint32_t abs_bits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
+
+// The smoothing division's exact route for one row (rows that the check
+// above rejects): IEEE divisions, as apply_smooth, re-reading the row and the
+// factors slot by slot, so that this rare route adds no registers to the
+// unrolled fast route.  Every thread of the workgroup calls it.
+template <int NV, bool BF16>
+__device__ void smooth_div_row_exact(const void* __restrict__ in, const float* __restrict__ smooth,
+                                     int8_t* __restrict__ out, float* __restrict__ scales,
+                                     int64_t r, int64_t cols, uint32_t* red) {
+    constexpr int kVals = BF16 ? 8 : 4;
+    constexpr int kF4 = kVals / 4;
+    const int tid = threadIdx.x;
+    const int nslots = static_cast<int>(cols / kVals);
+    const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const char*>(in) +
+                                                      r * cols * (BF16 ? 2 : 4));
+    auto smoothed = [&](int i, int h) -> f32x4 {
+        const u32x4 d = src[i];
+        f32x4 x;
+        if constexpr (BF16) x = h == 0 ? bf16x4_to_f32(d.x, d.y) : bf16x4_to_f32(d.z, d.w);
+        else x = __builtin_bit_cast(f32x4, d);
+        return apply_smooth<Smooth::kDiv>(quiet4(x), smooth, int64_t{i} * kVals + 4 * h);
+    };
+    float m = 0.0f;
+#pragma unroll 1
+    for (int j = 0; j < NV * kF4; ++j) {  // one float4 at a time
+        const int i = tid + (j / kF4) * kThreads;
+        if (i >= nslots) break;
+        m = absmax4(m, smoothed(i, j % kF4));
+    }
+    m = kc::wave_max(m);
+    if ((tid & (kWave - 1)) == 0) red[tid / kWave] = __float_as_uint(m);
+    __syncthreads();
+    const RowDiv d = row_div(__uint_as_float(max(max(red[0], red[1]), max(red[2], red[3]))));
+    if (tid == 0) scales[r] = d.s;
+    auto emit = [&](auto fast) {
+#pragma unroll 1
+        for (int j = 0; j < NV * kF4; ++j) {  // one float4 at a time
+            const int i = tid + (j / kF4) * kThreads, h = j % kF4;
+            if (i >= nslots) break;
+            reinterpret_cast<uint32_t*>(out + r * cols + int64_t{i} * kVals)[h] =
+                e4m3x4_div<decltype(fast)::value>(smoothed(i, h), d);
+        }
+    };
+    if (d.fast) emit(std::true_type{});
+    else emit(std::false_type{});
+}
+
+template <int NV, bool BF16, Smooth S, int P, bool FULL>
+__global__ __launch_bounds__(kThreads) void quant_rows_smooth_kernel(
+    const void* __restrict__ in, const float* __restrict__ smooth, int8_t* __restrict__ out,
+    float* __restrict__ scales, int64_t rows, int64_t cols) {
+    static_assert(S != Smooth::kNone, "smoothing variants only");
+    constexpr int kVals = BF16 ? 8 : 4;  // values per 16-byte slot
+    constexpr int kF4 = kVals / 4;       // float4 per slot
+    constexpr int kWaves = kThreads / kWave;
+    constexpr bool kDivide = S == Smooth::kDiv;
+    __shared__ uint32_t red[2][kWaves];  // row maxima, alternating rows
+    __shared__ uint32_t red_exact[kWaves];
+    __shared__ float red_min[kWaves];
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const bool lead = (tid & (kWave - 1)) == 0;
+    const int nslots = static_cast<int>(cols / kVals);
+    const int64_t grid = gridDim.x;
+    const int64_t row_bytes = cols * (BF16 ? 2 : 4);
+    auto valid = [&](int j) { return FULL || tid + j * kThreads < nslots; };
+
+    // Factors (quieted, as apply_smooth does) and their reciprocals.
+    f32x4 f[NV * kF4];
+    f32x4 rf[kDivide ? NV * kF4 : 1];
+    float smin = __builtin_inff();  // -1 once a factor is outside [2^-120, 2^120]
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+#pragma unroll
+        for (int h = 0; h < kF4; ++h) {
+            f32x4 v = f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+            if (valid(j))
+                v = quiet4(*reinterpret_cast<const f32x4*>(
+                    smooth + int64_t{tid + j * kThreads} * kVals + 4 * h));
+            f[j * kF4 + h] = v;
+            if constexpr (kDivide) {
+                rf[j * kF4 + h] = f32x4{1.0f / v.x, 1.0f / v.y, 1.0f / v.z, 1.0f / v.w};
+                if (valid(j)) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        smin = v[c] >= 0x1p-120f && v[c] <= 0x1p120f ? fminf(smin, v[c]) : -1.0f;
+                }
+            }
+        }
+    }
+    uint32_t tlo_bits = 0;  // T above
+    bool factors_ok = true;
+    if constexpr (kDivide) {
+        float m = wave_min(smin);
+        if (lead) red_min[wave] = m;
+        __syncthreads();
+        m = fminf(fminf(red_min[0], red_min[1]), fminf(red_min[2], red_min[3]));
+        factors_ok = m > 0.0f;
+        tlo_bits = __float_as_uint(fmaxf(0x1p-60f, 0x1p-81f / m));
+    }
+
+    auto load_row = [&](u32x4 (&b)[NV], int64_t r) {
+        const u32x4* src =
+            reinterpret_cast<const u32x4*>(static_cast<const char*>(in) + r * row_bytes);
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            b[j] = __builtin_nontemporal_load(src + (valid(j) ? tid + j * kThreads : 0));
+    };
+    auto values = [](const u32x4& d, int h) -> f32x4 {  // float4 h of a slot
+        if constexpr (BF16) return h == 0 ? bf16x4_to_f32(d.x, d.y) : bf16x4_to_f32(d.z, d.w);
+        else return __builtin_bit_cast(f32x4, d);
+    };
+    auto store = [&](int64_t r, int j, const uint32_t (&o)[kF4]) {
+        const int i = tid + j * kThreads;
+        if constexpr (BF16)
+            __builtin_nontemporal_store(u32x2{o[0], o[1]}, reinterpret_cast<u32x2*>(out + r * cols) + i);
+        else
+            __builtin_nontemporal_store(o[0], reinterpret_cast<uint32_t*>(out + r * cols) + i);
+    };
+    auto block_max = [&](uint32_t m, uint32_t* slot) {  // of non-negative floats' bits
+        m = wave_max_u32(m);
+        if (lead) slot[wave] = m;
+        __syncthreads();
+        return max(max(slot[0], slot[1]), max(slot[2], slot[3]));
+    };
+
+    int par = 0;
+    auto process = [&](const u32x4 (&b)[NV], int64_t r) {
+        f32x4 q[NV * kF4];
+        uint32_t um = 0;
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+#pragma unroll
+            for (int h = 0; h < kF4; ++h) {
+                const f32x4 x = values(b[j], h);
+                const f32x4 s = f[j * kF4 + h];
+                f32x4 v;
+                if constexpr (kDivide) {
+                    const f32x4 rr = rf[j * kF4 + h];
+                    v = f32x4{markstein(x.x, s.x, rr.x), markstein(x.y, s.y, rr.y),
+                              markstein(x.z, s.z, rr.z), markstein(x.w, s.w, rr.w)};
+                    if (valid(j))
+                        um = max(max(um, max(abs_bits(v.x), abs_bits(v.y))),
+                                 max(abs_bits(v.z), abs_bits(v.w)));
+                } else {
+                    v = f32x4{x.x * s.x, x.y * s.y, x.z * s.z, x.w * s.w};  // fp8_quant.cu:183
+                    if (valid(j)) m = absmax4(m, v);
+                }
+                q[j * kF4 + h] = v;
+            }
+        }
+        if constexpr (!kDivide) um = __float_as_uint(m);
+        um = block_max(um, red[par]);
+        par ^= 1;
+        if constexpr (kDivide) {
+            if (factors_ok && um >= tlo_bits && um <= 0x7E800000u) {  // 2^126
+                const float sr = __uint_as_float(um) / kE4M3Max, rr = 1.0f / sr;
+                if (tid == 0) scales[r] = sr;
+#pragma unroll
+                for (int j = 0; j < NV; ++j) {
+                    if (!valid(j)) continue;
+                    uint32_t o[kF4];
+#pragma unroll
+                    for (int h = 0; h < kF4; ++h) {
+                        const f32x4 v = q[j * kF4 + h];
+                        o[h] = e4m3x4_finite(markstein(v.x, sr, rr), markstein(v.y, sr, rr),
+                                             markstein(v.z, sr, rr), markstein(v.w, sr, rr));
+                    }
+                    store(r, j, o);
+                }
+                return;
+            }
+            smooth_div_row_exact<NV, BF16>(in, smooth, out, scales, r, cols, red_exact);
+        } else {
+            const RowDiv d = row_div(__uint_as_float(um));
+            if (tid == 0) scales[r] = d.s;
+            auto emit = [&](auto fast) {
+#pragma unroll
+                for (int j = 0; j < NV; ++j) {
+                    if (!valid(j)) continue;
+                    uint32_t o[kF4];
+#pragma unroll
+                    for (int h = 0; h < kF4; ++h)
+                        o[h] = e4m3x4_div<decltype(fast)::value>(q[j * kF4 + h], d);
+                    store(r, j, o);
+                }
+            };
+            if (d.fast) emit(std::true_type{});
+            else emit(std::false_type{});
+        }
+    };
+
+    u32x4 buf[P][NV];
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        const int64_t r = blockIdx.x + k * grid;
+        if (r < rows) load_row(buf[k], r);
+    }
+    for (int64_t base = blockIdx.x; base < rows; base += P * grid) {
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            const int64_t r = base + k * grid;
+            if (r >= rows) break;
+            process(buf[k], r);
+            const int64_t nr = r + P * grid;
+            if (nr < rows) load_row(buf[k], nr);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -519,6 +778,63 @@ int check_rows(const char* fn, const void* in, const void* out, const void* scal
     return KC_SUCCESS;
 }
 
+int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// Rows held by each workgroup of the persistent smoothing quantizer: the one
+// being reduced and kSmoothDepth - 1 in flight.  Its grid is kSmoothWaves
+// times what the device holds at once; with more row slots in flight
+// (depth 3-4) or exactly one resident round the 8192-column cases measured
+// the same or up to 3 % slower.
+constexpr int kSmoothDepth = 2;
+constexpr int kSmoothWaves = 2;
+
+template <int NV, bool BF16, Smooth S, bool FULL>
+int launch_smooth(const char* fn, const void* in, const float* smooth, int8_t* out, float* scales,
+                  int64_t rows, int64_t cols, hipStream_t stream) {
+    auto kernel = quant_rows_smooth_kernel<NV, BF16, S, kSmoothDepth, FULL>;
+    static const int per_cu = [&] {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kThreads, 0) != hipSuccess || n < 1)
+            n = 1;
+        return n;
+    }();
+    const int64_t grid = std::min<int64_t>(rows, int64_t{kSmoothWaves} * per_cu * device_cus());
+    kernel<<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(in, smooth, out, scales, rows, cols);
+    return kc::check_launch(fn);
+}
+
+// Persistent route for smoothing: rows of 256..1024 16-byte slots.  Returns
+// false when the shape takes another route.
+template <bool BF16, Smooth S>
+bool try_smooth_persistent(const char* fn, const void* in, const float* smooth, int8_t* out,
+                           float* scales, int64_t rows, int64_t cols, hipStream_t stream, int* st) {
+    if constexpr (S == Smooth::kNone) {
+        return false;
+    } else {
+        const int64_t nslots = cols / (BF16 ? 8 : 4);
+        if (nslots < kThreads || nslots > 4 * kThreads) return false;
+        const bool full = nslots % kThreads == 0;
+        const int64_t nv = (nslots + kThreads - 1) / kThreads;
+        if (nv == 1) *st = launch_smooth<1, BF16, S, true>(fn, in, smooth, out, scales, rows, cols, stream);
+        else if (nv == 2 && full) *st = launch_smooth<2, BF16, S, true>(fn, in, smooth, out, scales, rows, cols, stream);
+        else if (nv == 2) *st = launch_smooth<2, BF16, S, false>(fn, in, smooth, out, scales, rows, cols, stream);
+        else if (full) *st = launch_smooth<4, BF16, S, true>(fn, in, smooth, out, scales, rows, cols, stream);
+        else *st = launch_smooth<4, BF16, S, false>(fn, in, smooth, out, scales, rows, cols, stream);
+        return true;
+    }
+}
+
 template <Smooth S>
 int quant_rows_f32(const char* fn, const float* in, const float* smooth, int8_t* out,
                    float* scales, int64_t rows, int64_t cols, hipStream_t stream) {
@@ -530,6 +846,8 @@ int quant_rows_f32(const char* fn, const float* in, const float* smooth, int8_t*
     const unsigned grid = static_cast<unsigned>(rows);
     const bool vec = cols > 0 && cols % 4 == 0 && kc::aligned(in, 16) && kc::aligned(out, 4) &&
                      (S == Smooth::kNone || kc::aligned(smooth, 16));
+    if (vec && try_smooth_persistent<false, S>(fn, in, smooth, out, scales, rows, cols, stream, &st))
+        return st;
     const int64_t slots = (cols / 4 + kWave - 1) / kWave;  // 16-byte slots per lane, one wave per row
     if (vec && slots <= 16) {
         if (slots <= 1) quant_rows_wave_kernel<1, false, S><<<grid, kWave, 0, stream>>>(in, smooth, out, scales, cols);
@@ -565,6 +883,8 @@ int quant_rows_bf16(const char* fn, const uint16_t* in, const float* smooth, int
     const unsigned grid = static_cast<unsigned>(rows);
     const bool vec = cols > 0 && cols % 8 == 0 && kc::aligned(in, 16) && kc::aligned(out, 8) &&
                      (S == Smooth::kNone || kc::aligned(smooth, 16));
+    if (vec && try_smooth_persistent<true, S>(fn, in, smooth, out, scales, rows, cols, stream, &st))
+        return st;
     const int64_t slots = (cols / 8 + kWave - 1) / kWave;  // 16-byte slots per lane, one wave per row
     if (vec && slots <= 16) {
         if (slots <= 1) quant_rows_wave_kernel<1, true, S><<<grid, kWave, 0, stream>>>(in, smooth, out, scales, cols);

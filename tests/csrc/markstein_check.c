@@ -1,20 +1,28 @@
 /*
- * markstein_check.c -- CPU check of the FP8 quantizer's division by the row
- * scale (kernel-craft_amd/csrc/fp8_quant.hip: row_div / div_scale<true>).
+ * markstein_check.c -- CPU check of the FP8 quantizer's divisions
+ * (kernel-craft_amd/csrc/fp8_quant.hip: markstein(), row_div, and the
+ * SmoothQuant route of quant_rows_smooth_kernel).
  *
- * The reference divides each element by the row scale s = absmax / 448 with
- * an IEEE division (fp8_quant.cu:121,126).  The kernel instead computes, with
- * r = RN(1/s),
- *     q0 = RN(x*r);  e = RN(x - s*q0) (one FMA);  q = copysign(RN(q0 + e*r), x)
- * for rows with 2^-60 <= absmax <= FLT_MAX.  Claim checked here, for such s:
- *   (a) |x| >= 2^-103 and RN(x/s) normal:  q == RN(x/s) bit for bit;
- *   (b) otherwise:  |q| < 2^-30 and |RN(x/s)| < 2^-30, both with the sign of
- *       x (both encode to E4M3 +-0, whose smallest nonzero step is 2^-9).
+ * The reference divides with IEEE divisions (fp8_quant.cu:121,126,183).  The
+ * kernels instead compute, with r = RN(1/s),
+ *     q0 = RN(x*r);  e = RN(s*q0 - x) (one FMA);  q = RN(q0 - e*r)
+ * Claim checked by modes 0 and 1, for s in [2^-120, 2^120]:
+ *   (a) |x| >= 2^-102 and RN(x/s) normal:  q == RN(x/s) bit for bit;
+ *   (b) otherwise (finite x, |x/s| <= 2^126): q and RN(x/s) have the sign of
+ *       x, zeros included, and magnitudes <= 2^-102/s + 2^-125.
+ * Mode 2 checks the SmoothQuant route as a whole: rows are smoothed by the
+ * Markstein step, kept when the largest quotient magnitude lies in
+ * [max(2^-60, 2^-81/s_min), 2^126] with every factor in [2^-120, 2^120], and
+ * then encoded with a Markstein division by the row scale; the E4M3 codes
+ * and row scales of every kept row must equal those of the reference's
+ * two-step pipeline (IEEE x/s, absmax, IEEE division by absmax/448).
  *
  * usage: markstein_check <mode> <n> <seed>
- *   mode 0: n random rows' scales (absmax from a wide exponent range and
- *           mantissa patterns), 2^16 random x each plus edge cases
+ *   mode 0: n random scales (row scales absmax/448 with absmax in
+ *           [2^-60, 2^127], and factors in [2^-120, 2^120]), 2^16 x each
+ *           plus edge cases
  *   mode 1: exhaustive over all 2^32 x for the n-th fixed scale
+ *   mode 2: n random rows of 512 elements through the SmoothQuant route
  * Prints "mismatches <count>" and exits 0 when there are none.
  */
 #include <math.h>
@@ -36,31 +44,111 @@ static uint64_t next_u64(void) {  /* splitmix64 */
 
 static float kernel_div(float x, float s, float r) {
     volatile float q0 = x * r;          /* volatile: no contraction into the FMA */
-    float e = fmaf(-s, q0, x);
-    return copysignf(fmaf(e, r, q0), x);
+    volatile float e = fmaf(s, q0, -x);
+    return fmaf(-e, r, q0);
 }
 
-static long check(float x, float absmax) {
-    if (isnan(x) || fabsf(x) > absmax) return 0;  /* a row never holds |x| > absmax */
-    const float s = absmax / 448.0f, r = 1.0f / s;
-    const float want = x / s, got = kernel_div(x, s, r);
-    if (fabsf(x) >= 0x1p-103f && fabsf(want) >= 0x1p-126f) {
+static long check(float x, float s) {
+    const float r = 1.0f / s;
+    const float want = x / s;
+    if (!isfinite(x) || !(fabsf(want) <= 0x1p126f)) return 0;  /* such rows divide exactly */
+    const float got = kernel_div(x, s, r);
+    if (fabsf(x) >= 0x1p-102f && fabsf(want) >= 0x1p-126f) {
         if (f_to_bits(want) != f_to_bits(got)) {
-            fprintf(stderr, "absmax=%a x=%a: x/s=%a kernel=%a\n", absmax, x, want, got);
+            fprintf(stderr, "s=%a x=%a: x/s=%a kernel=%a\n", s, x, want, got);
             return 1;
         }
     } else {
-        if (!(fabsf(got) < 0x1p-30f && fabsf(want) < 0x1p-30f && signbit(got) == signbit(x) &&
+        const float bound = 0x1p-102f / s + 0x1p-125f;
+        if (!(fabsf(got) <= bound && fabsf(want) <= bound && signbit(got) == signbit(x) &&
               signbit(want) == signbit(x))) {
-            fprintf(stderr, "tiny absmax=%a x=%a: x/s=%a kernel=%a\n", absmax, x, want, got);
+            fprintf(stderr, "tiny s=%a x=%a: x/s=%a kernel=%a\n", s, x, want, got);
             return 1;
         }
     }
     return 0;
 }
 
-static const float kFixed[] = {448.0f, 3.0f, 1.0f, 235.0f, 5.5104f, 0x1p-60f, 3.40282347e38f,
-                               1e-10f, 1e30f, 0.75f, 0x1.fffffep+0f, 0x1.000002p-30f};
+/* OCP E4M3 (no infinities, max 448), round to nearest even, of |v| <= 448. */
+static uint8_t e4m3(float v) {
+    static float mag[127];
+    static int init = 0;
+    if (!init) {
+        for (int c = 0; c < 127; ++c) {
+            const int e = c >> 3, m = c & 7;
+            mag[c] = e == 0 ? ldexpf((float)m, -9) : ldexpf(1.0f + m / 8.0f, e - 7);
+        }
+        init = 1;
+    }
+    const uint8_t sign = signbit(v) ? 0x80 : 0;
+    const float a = fabsf(v);
+    int c = 0;
+    while (c < 126 && mag[c + 1] <= a) ++c;      /* largest magnitude <= a */
+    if (c < 126) {
+        const double lo = a - mag[c], hi = mag[c + 1] - a;
+        if (hi < lo || (hi == lo && (c & 1))) ++c;
+    }
+    return sign | (uint8_t)c;
+}
+
+static float clamp448(float v) {  /* fmaxf/fminf: NaN -> +448 */
+    return fmaxf(-448.0f, fminf(448.0f, v));
+}
+
+#define ROW 512
+static long fused_rows, fused_fast;
+
+static long check_row(const float* x, const float* s) {
+    /* reference: smooth, absmax, row scale, divide, clamp, encode */
+    float q[ROW], amax = 0.0f;
+    uint8_t want[ROW];
+    for (int i = 0; i < ROW; ++i) { q[i] = x[i] / s[i]; amax = fmaxf(amax, fabsf(q[i])); }
+    const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
+    for (int i = 0; i < ROW; ++i) want[i] = e4m3(clamp448(q[i] / scale));
+    /* kernel route */
+    float smin = INFINITY;
+    int factors_ok = 1;
+    for (int i = 0; i < ROW; ++i) {
+        if (!(s[i] >= 0x1p-120f && s[i] <= 0x1p120f)) factors_ok = 0;
+        smin = fminf(smin, s[i]);
+    }
+    const uint32_t tlo = f_to_bits(fmaxf(0x1p-60f, 0x1p-81f / smin));
+    float k[ROW];
+    uint32_t um = 0;
+    for (int i = 0; i < ROW; ++i) {
+        k[i] = kernel_div(x[i], s[i], 1.0f / s[i]);
+        const uint32_t b = f_to_bits(k[i]) & 0x7FFFFFFFu;
+        if (b > um) um = b;
+    }
+    ++fused_rows;
+    if (!(factors_ok && um >= tlo && um <= 0x7E800000u)) return 0;  /* exact route */
+    ++fused_fast;
+    const float sr = bits_to_f(um) / 448.0f, rr = 1.0f / sr;
+    if (f_to_bits(sr) != f_to_bits(scale)) {
+        fprintf(stderr, "row scale %a, reference %a\n", sr, scale);
+        return 1;
+    }
+    for (int i = 0; i < ROW; ++i) {
+        const float y = kernel_div(k[i], sr, rr);
+        const uint8_t got = e4m3(fmaxf(-448.0f, fminf(448.0f, y)));  /* NaN-free: the median */
+        if (got != want[i]) {
+            fprintf(stderr, "x=%a s=%a: code %02x, reference %02x\n", x[i], s[i], got, want[i]);
+            return 1;
+        }
+    }
+    return 0;
+}
+
+static float random_exp(int lo, int hi) {
+    const int ex = lo + (int)(next_u64() % (uint64_t)(hi - lo + 1));
+    const float v = ldexpf(1.0f + (float)(next_u64() & 0x7FFFFF) / 8388608.0f, ex);
+    return (next_u64() & 1) ? -v : v;
+}
+
+static const float kFixed[] = {448.0f / 448.0f,  3.0f / 448.0f, 0x1p-60f / 448.0f,
+                               3.40282347e38f / 448.0f, 235.0f / 448.0f, 0x1p-120f,
+                               0x1p120f, 1e-5f, 0x1.fffffep-1f, 0x1.000002p+0f,
+                               0x1.5555p-3f, 0x1.234567p-100f};
 
 int main(int argc, char** argv) {
     const int mode = argc > 1 ? atoi(argv[1]) : 0;
@@ -69,33 +157,73 @@ int main(int argc, char** argv) {
     long bad = 0;
     if (mode == 0) {
         for (long k = 0; k < n; ++k) {
-            /* absmax exponent in [-60, 127], random or extreme mantissa */
-            const int ex = -60 + (int)(next_u64() % 188);
             uint32_t man = (uint32_t)(next_u64() & 0x7FFFFF);
             if (k % 4 == 1) man = 0x7FFFFF;
             if (k % 4 == 2) man = 0;
-            float absmax = bits_to_f(((uint32_t)(ex + 127) << 23) | man);
-            if (isinf(absmax)) absmax = 3.40282347e38f;
+            float s;
+            if (k % 2 == 0) {  /* row scale: absmax exponent in [-60, 127] */
+                const int ex = -60 + (int)(next_u64() % 188);
+                float absmax = bits_to_f(((uint32_t)(ex + 127) << 23) | man);
+                if (isinf(absmax)) absmax = 3.40282347e38f;
+                s = absmax / 448.0f;
+            } else {           /* smoothing factor in [2^-120, 2^120] */
+                const int ex = -120 + (int)(next_u64() % 240);
+                s = bits_to_f(((uint32_t)(ex + 127) << 23) | man);
+            }
             for (long i = 0; i < 65536; ++i) {
                 const uint64_t u = next_u64();
                 float x;
                 switch (i & 3) {
                     case 0: x = bits_to_f((uint32_t)u); break;                          /* any pattern */
-                    case 1: x = absmax * (float)((int64_t)(u % 2000001) - 1000000) * 1e-6f; break;
+                    case 1: x = s * 448.0f * (float)((int64_t)(u % 2000001) - 1000000) * 1e-6f; break;
                     case 2: x = ldexpf(1.0f + (float)(u & 0xFFFFF) / 1048576.0f,
                                        (int)((u >> 20) % 140) - 140) * ((u >> 40) & 1 ? -1.0f : 1.0f);
-                            break;                                                         /* near 2^-103 */
-                    default: x = bits_to_f(f_to_bits(absmax) - (uint32_t)(u % 64)) * ((u >> 8) & 1 ? -1.0f : 1.0f);
+                            break;                                                         /* near 2^-102 */
+                    default: x = bits_to_f(f_to_bits(s) + (uint32_t)(u % 64)) * ((u >> 8) & 1 ? -1.0f : 1.0f);
                 }
-                bad += check(x, absmax);
+                bad += check(x, s);
             }
-            const float edge[] = {0.0f, -0.0f, absmax, -absmax, 0x1p-103f, -0x1p-103f,
-                                  0x1.fffffep-104f, 0x1p-149f, -0x1p-149f, 0x1p-126f};
-            for (unsigned i = 0; i < sizeof(edge) / sizeof(edge[0]); ++i) bad += check(edge[i], absmax);
+            const float edge[] = {0.0f, -0.0f, 0x1p-102f, -0x1p-102f, 0x1p-103f, -0x1p-103f,
+                                  0x1.fffffep-103f, 0x1p-149f, -0x1p-149f, 0x1p-126f};
+            for (unsigned i = 0; i < sizeof(edge) / sizeof(edge[0]); ++i) bad += check(edge[i], s);
         }
+    } else if (mode == 1) {
+        const float s = kFixed[n % (long)(sizeof(kFixed) / sizeof(kFixed[0]))];
+        for (uint64_t u = 0; u < (1ull << 32); ++u) bad += check(bits_to_f((uint32_t)u), s);
     } else {
-        const float absmax = kFixed[n % (long)(sizeof(kFixed) / sizeof(kFixed[0]))];
-        for (uint64_t u = 0; u < (1ull << 32); ++u) bad += check(bits_to_f((uint32_t)u), absmax);
+        float x[ROW], s[ROW];
+        for (long k = 0; k < n; ++k) {
+            const int kind = (int)(k % 8);
+            /* factors: the SmoothQuant range, or wide but inside [2^-120, 2^120] */
+            const int slo = kind < 4 ? -17 : -119, shi = kind < 4 ? 10 : 119;
+            for (int i = 0; i < ROW; ++i) s[i] = fabsf(random_exp(slo, shi));
+            if (k % 16 == 13) s[next_u64() % ROW] = 0x1p-121f;  /* outside: exact route */
+            int xlo = -20, xhi = 10;
+            switch (kind) {
+                case 1: xlo = -149; xhi = -90; break;
+                case 2: xlo = -140; xhi = 20; break;
+                case 3: xlo = -70; xhi = -50; break;
+                case 5: xlo = -149; xhi = 127; break;
+                case 6: xlo = -110; xhi = -95; break;
+                default: break;
+            }
+            for (int i = 0; i < ROW; ++i) {
+                const uint64_t u = next_u64();
+                if (u % 50 == 0) x[i] = (u >> 8) & 1 ? -0.0f : 0.0f;
+                else if (u % 53 == 0) x[i] = bits_to_f((uint32_t)next_u64() & 0x807FFFFFu);  /* subnormal */
+                else if (u % 97 == 0) x[i] = random_exp(-110, -100);
+                else x[i] = random_exp(xlo, xhi);
+                if (kind == 2 || kind == 5) x[i] = bits_to_f(f_to_bits(x[i]) & 0xFFFF0000u);  /* bf16 */
+            }
+            if (k % 16 == 9) x[next_u64() % ROW] = NAN;
+            if (k % 16 == 11) x[next_u64() % ROW] = -INFINITY;
+            bad += check_row(x, s);
+        }
+        /* the route must be exercised, not skipped */
+        if (fused_fast * 4 < fused_rows) {
+            fprintf(stderr, "only %ld of %ld rows took the Markstein route\n", fused_fast, fused_rows);
+            ++bad;
+        }
     }
     printf("mismatches %ld\n", bad);
     return bad != 0;

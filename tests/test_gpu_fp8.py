@@ -122,7 +122,11 @@ def test_per_token_bf16_shapes(gpu, oracle, rows, cols):
     _assert_codes_equal(q, eq)
 
 
-@pytest.mark.parametrize("rows,cols", [(2, 520), (3, 4096), (2, 8192), (2, 8200), (2, 20000)])
+# Smoothing routes: one wave per row (520), the persistent kernel for rows of
+# 256..1024 16-byte slots (2048..8192: full and partial slot sets, and more
+# rows than its grid), one workgroup per row (8200), the generic kernel.
+@pytest.mark.parametrize("rows,cols", [(2, 520), (3, 2048), (2, 2056), (3, 4096), (4, 6152),
+                                       (2, 8192), (8000, 2048), (2, 8200), (2, 20000)])
 @pytest.mark.parametrize("mode", ["div", "mul"])
 def test_smooth_bf16_shapes(gpu, oracle, rows, cols, mode):
     x, _ = outlier_activations(rows, cols, 0.005, 100.0, seed=rows * 131 + cols)
@@ -133,6 +137,90 @@ def test_smooth_bf16_shapes(gpu, oracle, rows, cols, mode):
         eq, es = oracle.quantize_fp8_smooth_div(xb, sm)
     else:
         eq, es = oracle.quantize_fp8_smooth_mul_bf16(xb, sm)
+    np.testing.assert_array_equal(s.view(np.uint32), es.view(np.uint32))
+    _assert_codes_equal(q, eq)
+
+
+def _smooth_div_f32(torch, x, sm):
+    rows, cols = x.shape
+    L = kc_abi.lib()
+    dx, dsm = _dev(torch, x), _dev(torch, sm)
+    dq = torch.full((rows, cols), 0x55, dtype=torch.int8, device="cuda")
+    ds = torch.full((max(rows, 1),), float("nan"), dtype=torch.float32, device="cuda")
+    print(f"fp8 f32 div rows={rows} cols={cols}", flush=True)
+    kc_abi.check("kc_quantize_fp8_smooth_div_f32",
+                 L.kc_quantize_fp8_smooth_div_f32(ptr(dx), ptr(dsm), ptr(dq), ptr(ds), rows, cols,
+                                                  stream()))
+    torch.cuda.synchronize()
+    return dq.cpu().numpy(), ds.cpu().numpy()[:rows]
+
+
+@pytest.mark.parametrize("rows,cols", [(2, 520), (3, 1024), (2, 1028), (3, 2052), (2, 4096),
+                                       (6000, 1024), (2, 4100)])
+def test_smooth_div_f32_shapes(gpu, oracle, rows, cols):
+    x, _ = outlier_activations(rows, cols, 0.005, 100.0, seed=rows * 17 + cols)
+    sm = np.random.default_rng(cols + 1).uniform(0.05, 30.0, cols).astype(np.float32)
+    q, s = _smooth_div_f32(gpu, x, sm)
+    eq, es = oracle.quantize_fp8_smooth_div(x, sm)
+    np.testing.assert_array_equal(s.view(np.uint32), es.view(np.uint32))
+    _assert_codes_equal(q, eq)
+
+
+def _special_rows(rng, cols):
+    """Rows that leave the smoothing division's fast route, between ordinary
+    rows: zeros, -0, NaN, infinities, quotients that overflow, all-tiny rows,
+    tiny elements under a normal maximum, and a wide exponent spread."""
+    x = rng.standard_normal((16, cols)).astype(np.float32)
+    x[1] = 0.0
+    x[2] = -0.0
+    x[3, ::7] = np.nan
+    x[4, 5] = np.inf
+    x[5, 9] = -np.inf
+    x[6] = np.float32(3e38) * rng.uniform(-1, 1, cols).astype(np.float32)    # x / s overflows
+    x[7] = np.float32(2.0 ** -110) * rng.standard_normal(cols).astype(np.float32)
+    x[8] = np.float32(2.0 ** -135) * np.sign(rng.standard_normal(cols)).astype(np.float32)
+    x[9] = np.float32(2.0 ** -100) * rng.standard_normal(cols).astype(np.float32)
+    x[9, 3] = 1.0
+    x[10] = np.float32(2.0) ** rng.integers(-126, 127, cols).astype(np.float32)
+    x[11, :] = np.nan
+    x[12] = np.float32(2.0 ** -70) * rng.standard_normal(cols).astype(np.float32)
+    x[13, ::3] = -0.0
+    return x
+
+
+def _special_factors(rng, cols, kind):
+    if kind == "normal":
+        return rng.uniform(0.05, 30.0, cols).astype(np.float32)
+    if kind == "wide":
+        return (np.float32(2.0) ** rng.integers(-119, 120, cols)).astype(np.float32)
+    s = rng.uniform(0.05, 30.0, cols).astype(np.float32)
+    s[[1, 5, 9, 13, 17, 21, 25]] = [0.0, 2.0 ** -125, np.inf, np.nan, -2.0, 2.0 ** 125, 1e-45]
+    return s
+
+
+@pytest.mark.parametrize("factors", ["normal", "wide", "outside"])
+@pytest.mark.parametrize("dtype,cols", [("bf16", 2048), ("bf16", 4104), ("f32", 1024),
+                                        ("f32", 2052)])
+@pytest.mark.parametrize("mode", ["div", "mul"])
+def test_smooth_special_values(gpu, oracle, mode, dtype, cols, factors):
+    """Special rows and factors through the persistent smoothing kernel,
+    including the rows and factor vectors that its Markstein check sends to
+    the IEEE route."""
+    if mode == "mul" and dtype == "f32":
+        pytest.skip("the smoothing multiply takes bf16 weights")
+    rng = np.random.default_rng(cols * 7 + len(factors))
+    x = _special_rows(rng, cols)
+    sm = _special_factors(rng, cols, factors)
+    if dtype == "bf16":
+        xb = f32_to_bf16_bits(x)
+        q, s = _per_token_bf16(gpu, xb, sm, mode)
+        if mode == "div":
+            eq, es = oracle.quantize_fp8_smooth_div(xb, sm)
+        else:
+            eq, es = oracle.quantize_fp8_smooth_mul_bf16(xb, sm)
+    else:
+        q, s = _smooth_div_f32(gpu, x, sm)
+        eq, es = oracle.quantize_fp8_smooth_div(x, sm)
     np.testing.assert_array_equal(s.view(np.uint32), es.view(np.uint32))
     _assert_codes_equal(q, eq)
 
