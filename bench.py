@@ -9,7 +9,10 @@ N 6144), O (4096, 4096), fused gate/up (4096, 28672), down (14336, 4096).
 nibbles + x + y: 116 858 880 B) times steps over the wall-clock time of the
 timed steps, bracketed by torch.cuda.synchronize().  Inputs are resident in
 HBM and rotate over enough copies (> 1 GiB) that the 256 MB Infinity Cache
-cannot hold them; each step replays a HIP graph of the four launches.
+cannot hold them.  A step is timed two ways -- one kc_gemv_int4_bf16_chain
+call (the four launches back to back from native code) and a HIP graph
+replay of the four launches -- and `value` is the faster; both are in
+`config.launch_modes_GBps`.
 
 `roofline` is for the dominant kernel (the gate/up GEMV): its algorithmic
 bytes per launch over its average duration, timed with HIP events on the
@@ -201,7 +204,25 @@ def main() -> int:
             return 1
         log(f"# parity {name}: rel L2 {err:.2e}")
 
-    # ---- one HIP graph per rotation copy (the four launches of a layer) ----
+    # ---- a step: the layer's four GEMVs from one native call ---------------
+    # (kc_gemv_int4_bf16_chain launches them back to back), and the same four
+    # launches replayed from a HIP graph; `value` is the faster of the two.
+    import ctypes
+    chains = []
+    for r in range(copies):
+        arr = (ops.GemvOp * len(LLAMA))()
+        for i, (_, n, k) in enumerate(LLAMA):
+            p, s, z = layers[r][i]
+            arr[i] = ops.GemvOp(p.data_ptr(), s.data_ptr(), z.data_ptr(), xs[i].data_ptr(),
+                                ys[i].data_ptr(), n, k, GS, 0)
+        chains.append(arr)
+
+    def step_chain(j: int) -> None:
+        st = lib.kc_gemv_int4_bf16_chain(ctypes.cast(chains[j % copies], ctypes.c_void_p),
+                                         len(LLAMA), torch.cuda.current_stream().cuda_stream)
+        if st:
+            raise RuntimeError(f"kc_gemv_int4_bf16_chain failed: {lib.kc_last_error_string().decode()}")
+
     graphs = None
     if not args.no_graph:
         try:
@@ -217,29 +238,33 @@ def main() -> int:
                     graphs.append(gph)
             torch.cuda.current_stream().wait_stream(side)
         except Exception as e:  # pragma: no cover - depends on the runtime
-            log(f"# graph capture unavailable ({e}); eager launches")
+            log(f"# graph capture unavailable ({e})")
             graphs = None
 
-    def step(j: int) -> None:
-        r = j % copies
-        if graphs is not None:
-            graphs[r].replay()
-        else:
-            for i in range(len(LLAMA)):
-                launch(r, i)
+    def step_graph(j: int) -> None:
+        graphs[j % copies].replay()
 
-    torch.cuda.synchronize()
-    for j in range(args.warmup):
-        step(j)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for j in range(args.steps):
-        step(args.warmup + j)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    def timed(step) -> float:
+        torch.cuda.synchronize()
+        for j in range(args.warmup):
+            step(j)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for j in range(args.steps):
+            step(args.warmup + j)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    modes = {"native_chain": timed(step_chain)}
+    if graphs is not None:
+        modes["hip_graph"] = timed(step_graph)
+    for m, t in modes.items():
+        log(f"# {m}: {args.steps} steps in {t * 1e3:.3f} ms -> "
+            f"{layer_bytes * args.steps / t / 1e9:.1f} GB/s")
+    launch_mode = min(modes, key=modes.get)
+    elapsed = modes[launch_mode]
     value = layer_bytes * args.steps / elapsed / 1e9
-    log(f"# timed {args.steps} steps in {elapsed * 1e3:.3f} ms -> {value:.1f} GB/s "
-        f"({'graph' if graphs is not None else 'eager'})")
+    modes_gbs = {m: round(layer_bytes * args.steps / t / 1e9, 1) for m, t in modes.items()}
 
     # ---- per-kernel durations with HIP events (launch stream, backlogged) ---
     reps = 100
@@ -420,7 +445,7 @@ def main() -> int:
         "config": {"workload": "int4_gemv_llama3_8b_decode_layer",
                    "shapes_NK": [[n, k] for _, n, k in LLAMA], "group_size": GS, "M": 1,
                    "bytes_per_step": layer_bytes, "rotation_copies": copies,
-                   "launch": "hip_graph" if graphs is not None else "eager"},
+                   "launch": launch_mode, "launch_modes_GBps": modes_gbs},
         "pct_of_peak": round(100.0 * value / PEAK_HBM_GBS, 2),
         "roofline": roofline,
         "kernel_us": {k: round(v, 3) for k, v in kernel_us.items()},

@@ -113,6 +113,23 @@ int kc_gemv_int4_bf16(const uint8_t* d_packed, const float* d_scales,
                       uint16_t* d_y, int rows, int cols, int group_size,
                       kc_stream_t stream);
 
+/* A decode step's INT4 GEMVs from one call (no counterpart in the
+ * reference, whose decode loop calls launch_gemv_int4 once per projection,
+ * quant_int4.cu:221-234).  Each op is one kc_gemv_int4_bf16; the ops are
+ * launched back to back on the stream, so an op may read what earlier ops
+ * wrote (its x may be an earlier op's y).  Every op is validated before the
+ * first launch. */
+#define KC_GEMV_CHAIN_MAX_OPS 8
+typedef struct kc_gemv_op {
+    const uint8_t* packed;
+    const float* scales;
+    const uint8_t* zeros;
+    const uint16_t* x;
+    uint16_t* y;
+    int rows, cols, group_size, reserved;
+} kc_gemv_op;
+int kc_gemv_int4_bf16_chain(const kc_gemv_op* ops, int n_ops, kc_stream_t stream);
+
 /* Small-batch INT4 GEMM on MFMA: Y[m, n] = sum_k X[m,k] W[n,k].
  * X [m, cols] bf16 row-major, Y [m, rows] bf16 row-major, 1 <= m <= 64. */
 int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,

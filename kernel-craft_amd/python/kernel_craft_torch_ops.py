@@ -111,6 +111,7 @@ PROTOTYPES = {
     "kc_gemv_int4_f32_async": ([_vp] * 5 + [_i, _i, _i, _vp], _i),
     "kc_gemv_int4_bf16": ([_vp] * 5 + [_i, _i, _i, _vp], _i),
     "kc_gemm_int4_bf16": ([_vp] * 5 + [_i, _i, _i, _i, _vp], _i),
+    "kc_gemv_int4_bf16_chain": ([_vp, _i, _vp], _i),
     "kc_quantize_fp8_per_token_f32": ([_vp, _vp, _vp, _i64, _i64, _vp], _i),
     "kc_quantize_fp8_per_tensor_f32": ([_vp, _vp, _vp, _i64, _i64, _vp], _i),
     "kc_quantize_fp8_per_token_bf16": ([_vp, _vp, _vp, _i64, _i64, _vp], _i),
@@ -338,6 +339,32 @@ def int4_gemv_bf16(packed, scales, zeros, x, rows: int, cols: int, group_size: i
                                           _ptr(y), rows, cols, group_size, _stream())
     _check("int4_gemv_bf16", st)
     return y
+
+
+class GemvOp(ctypes.Structure):
+    """kc_gemv_op (include/kernel_craft.h): one GEMV of a chain."""
+    _fields_ = [("packed", ctypes.c_void_p), ("scales", ctypes.c_void_p),
+                ("zeros", ctypes.c_void_p), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                ("rows", ctypes.c_int), ("cols", ctypes.c_int), ("group_size", ctypes.c_int),
+                ("reserved", ctypes.c_int)]
+
+
+def int4_gemv_bf16_chain(ops) -> None:
+    """Runs int4_gemv_bf16 for each op in order, from one call: ops is a list
+    of (packed, scales, zeros, x, y, rows, cols, group_size) with bf16 x and
+    y tensors already allocated; an op may take an earlier op's y (or a
+    contiguous slice of it) as its x."""
+    arr = (GemvOp * max(1, len(ops)))()
+    for i, (packed, scales, zeros, x, y, rows, cols, gs) in enumerate(ops):
+        for t in (packed, scales, zeros, x, y):
+            if not t.is_contiguous():
+                raise ValueError("int4_gemv_bf16_chain: tensors must be contiguous")
+        _on_gpu(packed, scales, zeros, x, y)
+        arr[i] = GemvOp(_ptr(packed), _ptr(scales), _ptr(zeros), _ptr(x), _ptr(y), rows, cols, gs, 0)
+    with kernel_span("int4_gemv_bf16_chain", ops=len(ops)):
+        st = _get_lib().kc_gemv_int4_bf16_chain(ctypes.cast(arr, ctypes.c_void_p), len(ops),
+                                                _stream())
+    _check("int4_gemv_bf16_chain", st)
 
 
 def int4_gemm_bf16(packed, scales, zeros, x, rows: int, cols: int, group_size: int = 128):

@@ -271,3 +271,86 @@ def test_gemm_shapes(gpu, oracle, m, rows, cols, gs):
     y, _ = _gemm(gpu, packed, scales, zeros, xb, m, rows, cols, gs)
     truth = oracle.gemm_int4_bf16_f64(packed, scales, zeros.reshape(-1), xb, m, rows, cols, gs)
     assert rel_l2(y, truth) < 3e-3
+
+
+# ---------------------------------------------------------------------------
+# A decode step's GEMVs in one launch (kc_gemv_int4_bf16_chain)
+# ---------------------------------------------------------------------------
+
+def _run_chain(torch, specs, wire, seed=3000):
+    """specs: (rows, cols, gs) per op; wire[i] = j takes op i's x from the
+    first cols entries of op j's y (j < i), -1 a fresh random x.  Runs the
+    chain and returns, per op, its weights, the x it read and its y."""
+    import kernel_craft_torch_ops as ops
+    dev_ops, weights, ys = [], [], []
+    for i, (rows, cols, gs) in enumerate(specs):
+        packed, scales, zeros = make_int4(rows, cols, gs, seed=seed + 7 * i + rows + cols)
+        if wire[i] < 0:
+            x = _dev_bf16(torch, normal_bf16(cols, seed=seed + 100 + i))
+        else:
+            x = ys[wire[i]][:cols]
+            assert x.numel() == cols, "an op's x must fit in the earlier op's y"
+        y = torch.full((rows,), float("nan"), dtype=torch.bfloat16, device="cuda")
+        ys.append(y)
+        dev_ops.append((_dev(torch, packed), _dev(torch, scales), _dev(torch, zeros), x, y,
+                        rows, cols, gs))
+        weights.append((packed, scales, zeros))
+    print(f"chain specs={specs} wire={wire}", flush=True)
+    ops.int4_gemv_bf16_chain(dev_ops)
+    torch.cuda.synchronize()
+    return [(w, _host_bf16_bits(d[3]), bf16_bits_to_f32(_host_bf16_bits(d[4])))
+            for w, d in zip(weights, dev_ops)]
+
+
+def _check_chain(oracle, specs, results, tol=3e-3):
+    for (rows, cols, gs), ((packed, scales, zeros), xb, y) in zip(specs, results):
+        truth = oracle.gemv_int4_f64(packed, scales, zeros.reshape(-1), bf16_bits_to_f32(xb),
+                                     rows, cols, gs)
+        assert np.all(np.isfinite(y)), (rows, cols, gs)
+        assert rel_l2(y, truth) < tol, (rows, cols, gs, rel_l2(y, truth))
+
+
+def test_chain_llama_decode_layer(gpu, oracle):
+    """QKV -> O -> gate/up -> down from one call, each op reading the previous
+    op's output."""
+    specs = [(6144, 4096, 128), (4096, 4096, 128), (28672, 4096, 128), (4096, 14336, 128)]
+    _check_chain(oracle, specs, _run_chain(gpu, specs, [-1, 0, 1, 2]))
+
+
+# the standalone kernel's chunks-per-lane counts 1..8 and group sizes 128..4096
+CHAIN_SHAPES = [(13001, 2048, 128), (3, 128, 128), (12288, 4096, 256), (50, 4096, 128),
+                (6150, 6144, 128), (6200, 8192, 512), (777, 10240, 128), (300, 12288, 1024),
+                (4096, 14336, 128), (9, 16384, 128), (64, 4096, 4096)]
+
+
+@pytest.mark.parametrize("rows,cols,gs", CHAIN_SHAPES)
+def test_chain_shapes(gpu, oracle, rows, cols, gs):
+    specs = [(rows, cols, gs)]
+    _check_chain(oracle, specs, _run_chain(gpu, specs, [-1], seed=rows + cols))
+
+
+def test_chain_eight_ops_in_a_line(gpu, oracle):
+    specs = [(2048, 1024, 128), (4096, 2048, 128), (1024, 4096, 256), (8192, 1024, 128),
+             (512, 8192, 128), (3000, 512, 128), (640, 3000 - 3000 % 128, 128), (100, 640, 128)]
+    wire = [-1, 0, 1, 2, 3, 4, 5, 6]
+    _check_chain(oracle, specs, _run_chain(gpu, specs, wire, seed=77))
+
+
+def test_chain_other_group_sizes_and_long_rows(gpu, oracle):
+    """Group size 64 and cols above 16384 (the generic and wide GEMV routes)."""
+    specs = [(300, 2048, 64), (500, 16512, 128), (200, 256, 128)]
+    _check_chain(oracle, specs, _run_chain(gpu, specs, [-1, -1, 0], seed=5))
+
+
+def test_chain_argument_errors(gpu):
+    import kernel_craft_torch_ops as ops
+    L = kc_abi.lib()
+    arr = (ops.GemvOp * 9)()
+    assert L.kc_gemv_int4_bf16_chain(ctypes.cast(arr, ctypes.c_void_p), 9, stream()) == 1
+    assert L.kc_gemv_int4_bf16_chain(None, 1, stream()) == 1
+    arr[0].rows, arr[0].cols, arr[0].group_size = 4, 256, 100
+    assert L.kc_gemv_int4_bf16_chain(ctypes.cast(arr, ctypes.c_void_p), 1, stream()) == 1
+    arr[0].group_size = 128
+    assert L.kc_gemv_int4_bf16_chain(ctypes.cast(arr, ctypes.c_void_p), 1, stream()) == 1  # nulls
+    assert L.kc_gemv_int4_bf16_chain(None, 0, stream()) == 0
+    L.kc_get_last_error()
