@@ -1,0 +1,175 @@
+"""The kernel_craft_transformer pybind11 module (kernel-craft_amd/python/
+pybind_transformer.cpp) against the reference module's registered API
+(pybind_transformer.cpp:801-882): names, argument names and defaults, the
+out-of-scope functions, argument validation (CPU, no kernel launched), and
+on the GPU the reference's own binding tests (test_transformer_bindings.py:
+172-238) plus bit-exact comparisons with the oracle."""
+import re
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+BUILD = ROOT / "build"
+
+
+@pytest.fixture(scope="module")
+def kct():
+    if str(BUILD) not in sys.path:
+        sys.path.insert(0, str(BUILD))
+    if not list(BUILD.glob("kernel_craft_transformer*.so")):
+        pytest.fail("build/kernel_craft_transformer*.so missing: run __graft_entry__.build() first")
+    import kernel_craft_transformer
+    return kernel_craft_transformer
+
+
+# (name, [(arg, default or None)]) for the reference's registered quantization
+# functions and the two its docstring advertises (gemv_int4, smoothquant_scale)
+SIGNATURES = {
+    "quant_int4_dequant": [("packed", None), ("scales", None), ("zeros", None), ("rows", None),
+                           ("cols", None), ("group_size", "128")],
+    "fp8_quantize": [("input", None), ("per_token", "True")],
+    "fp8_dequantize": [("quantized", None), ("scales", None), ("rows", None), ("cols", None),
+                       ("per_token", "True")],
+    "gemv_int4": [("packed", None), ("scales", None), ("zeros", None), ("x", None), ("rows", None),
+                  ("cols", None), ("group_size", "128")],
+    "smoothquant_scale": [("input", None), ("smooth_scales", None)],
+}
+OUT_OF_SCOPE = ["flash_attention", "paged_attention", "speculative_decode", "ring_allreduce",
+                "allgather", "col_parallel_linear", "row_parallel_linear", "nccl_comm_init",
+                "nccl_comm_destroy", "nccl_allreduce", "nccl_group_start", "nccl_group_end",
+                "selective_scan", "depthwise_conv1d", "rmsnorm"]
+
+
+def _args(fn):
+    sig = fn.__doc__.splitlines()[0]
+    inner = sig[sig.index("(") + 1:sig.rindex(")")]
+    out = []
+    depth, cur = 0, ""
+    for ch in inner:  # split on top-level commas
+        depth += ch in "[("
+        depth -= ch in "])"
+        if ch == "," and depth == 0:
+            out.append(cur.strip())
+            cur = ""
+        else:
+            cur += ch
+    out.append(cur.strip())
+    res = []
+    for a in out:
+        name = a.split(":")[0].strip()
+        default = a.split("=")[-1].strip() if "=" in a else None
+        res.append((name, default))
+    return res
+
+
+@pytest.mark.parametrize("name", sorted(SIGNATURES))
+def test_signatures_match_reference(kct, name):
+    assert _args(getattr(kct, name)) == SIGNATURES[name]
+
+
+@pytest.mark.parametrize("name", OUT_OF_SCOPE)
+def test_out_of_scope_functions_raise(kct, name):
+    with pytest.raises(NotImplementedError, match=name):
+        getattr(kct, name)(1, 2, 3)
+
+
+def test_have_nccl_false(kct):
+    assert kct.HAVE_NCCL is False
+
+
+def test_argument_validation_before_any_launch(kct):
+    packed = np.zeros((4, 8), np.uint8)
+    scales = np.ones((4, 2), np.float32)
+    zeros = np.zeros((4, 1), np.uint8)
+    with pytest.raises(ValueError, match="packed"):
+        kct.quant_int4_dequant(packed, scales, zeros, 5, 16, 8)
+    with pytest.raises(ValueError, match="scales"):
+        kct.quant_int4_dequant(packed, scales[:3], zeros, 4, 16, 8)
+    with pytest.raises(ValueError, match="multiple of group_size"):
+        kct.quant_int4_dequant(packed, scales, zeros, 4, 16, 6)
+    with pytest.raises(ValueError, match="zeros"):
+        kct.quant_int4_dequant(packed, scales, zeros[:2], 4, 16, 8)
+    with pytest.raises(ValueError, match="x holds"):
+        kct.gemv_int4(packed, scales, zeros, np.zeros(8, np.float32), 4, 16, 8)
+    with pytest.raises(ValueError, match="2-D"):
+        kct.fp8_quantize(np.zeros(8, np.float32))
+    with pytest.raises(ValueError, match="too few scales"):
+        kct.fp8_dequantize(np.zeros((4, 8), np.int8), np.ones(3, np.float32), 4, 8, True)
+    with pytest.raises(ValueError, match="smooth_scales"):
+        kct.smoothquant_scale(np.zeros((4, 8), np.float32), np.ones(7, np.float32))
+
+
+# ---------------------------------------------------------------------------
+# GPU: the reference's binding tests, re-expressed, and the oracle
+# ---------------------------------------------------------------------------
+
+def _pack(w):
+    lo = (w[:, 0::2].astype(np.int32) & 0xF)
+    hi = (w[:, 1::2].astype(np.int32) & 0xF)
+    return (lo | (hi << 4)).astype(np.uint8)
+
+
+@pytest.mark.gpu
+def test_reference_dequant_roundtrip(gpu, kct):
+    rows, cols, gs = 4, 16, 8
+    weights = np.random.default_rng(42).integers(-7, 8, (rows, cols), dtype=np.int8)
+    sc = cols // gs
+    scales = np.full((rows, sc), 0.125, np.float32)
+    zeros = np.zeros((rows, sc // 2 + sc % 2), np.uint8)
+    print("pybind quant_int4_dequant 4x16", flush=True)
+    result = kct.quant_int4_dequant(_pack(weights), scales, zeros, rows, cols, gs)
+    np.testing.assert_allclose(result, weights.astype(np.float32) * 0.125, atol=1e-5)
+    out = kct.quant_int4_dequant(np.zeros((8, 16), np.uint8), np.ones((8, 4), np.float32),
+                                 np.zeros((8, 3), np.uint8), 8, 32, 8)
+    assert out.shape == (8, 32)
+
+
+@pytest.mark.gpu
+def test_reference_fp8_roundtrips_and_shapes(gpu, kct):
+    inp = np.random.default_rng(42).uniform(-1, 1, (8, 64)).astype(np.float32)
+    print("pybind fp8 round trips", flush=True)
+    q, scales = kct.fp8_quantize(inp, per_token=True)
+    out = kct.fp8_dequantize(q, scales, 8, 64, per_token=True)
+    nz = np.abs(inp) > 1e-6
+    assert (np.abs(out[nz] - inp[nz]) / np.abs(inp[nz])).max() < 0.15
+    z = np.zeros((4, 32), np.float32)
+    q, scales = kct.fp8_quantize(z, per_token=True)
+    np.testing.assert_allclose(kct.fp8_dequantize(q, scales, 4, 32, per_token=True), 0.0, atol=1e-6)
+    q, scales = kct.fp8_quantize(np.ones((16, 128), np.float32), per_token=True)
+    assert q.shape == (16, 128) and q.dtype == np.int8 and scales.shape == (16,)
+    q, scales = kct.fp8_quantize(np.ones((8, 64), np.float32), per_token=False)
+    assert q.shape == (8, 64) and scales.shape == (1,)
+
+
+@pytest.mark.gpu
+def test_module_matches_oracle(gpu, kct, oracle):
+    from kc_data import make_int4
+    rng = np.random.default_rng(7)
+    rows, cols, gs = 300, 1024, 128
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=5)
+    print("pybind vs oracle", flush=True)
+    np.testing.assert_array_equal(kct.quant_int4_dequant(packed, scales, zeros, rows, cols, gs),
+                                  oracle.dequantize_int4(packed, scales, zeros.reshape(-1), rows, cols, gs))
+    x = rng.standard_normal(cols).astype(np.float32)
+    y = kct.gemv_int4(packed, scales, zeros, x, rows, cols, gs)
+    truth = oracle.gemv_int4_f64(packed, scales, zeros.reshape(-1), x, rows, cols, gs)
+    assert np.linalg.norm(y - truth) / np.linalg.norm(truth) < 1e-5
+    a = (rng.standard_normal((37, 200)) * 3).astype(np.float32)
+    a[3, 5] = np.nan
+    q, s = kct.fp8_quantize(a, per_token=True)
+    eq, es = oracle.quantize_fp8_per_token(a)
+    np.testing.assert_array_equal(q, eq)
+    np.testing.assert_array_equal(s, es)
+    # per-tensor: the scale is the host absmax / 448 (NaN ignored), as the reference binding
+    q, s = kct.fp8_quantize(a, per_token=False)
+    want = np.float32(np.nanmax(np.abs(a))) / np.float32(448.0)
+    assert s.shape == (1,) and s[0] == want
+    eq = oracle.quantize_fp8_per_tensor(a, s[0])
+    np.testing.assert_array_equal(q, eq)
+    np.testing.assert_array_equal(kct.fp8_dequantize(q, s, 37, 200, per_token=False),
+                                  oracle.dequantize_fp8(q, s, 37, 200, per_token=False))
+    sm = rng.uniform(0.1, 10.0, 200).astype(np.float32)
+    np.testing.assert_array_equal(kct.smoothquant_scale(a, sm), oracle.smoothquant_scale(a, sm))
