@@ -22,7 +22,8 @@ beside it, each as algorithmic bytes over the average launch duration:
 `gemv_cfg0` (fp32 reference-ABI GEMV, 4096 x 4096), `gemm_cfg3` (MFMA
 small-batch GEMM, M = 4/16/64, K 8192, N 28672), `fp8_quant` (cfg1 per-token X
 and per-channel W, fp32 [4096, 4096]) and `fp8_cfg4` (SmoothQuant statistics
-and the two fused quantizers on bf16 X [16384, 8192] and W [28672, 8192]).
+and the two fused quantizers on bf16 X [16384, 8192] and W [28672, 8192]), and
+`convert_int4` (GPTQ and AWQ checkpoints of the gate/up layer to the layout).
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20]
 """
@@ -411,6 +412,42 @@ def main() -> int:
         f"({fp8_cfg4['quantize_w']['GBps']} GB/s), total {fp8_cfg4['total']['GBps']} GB/s")
     del X4, W4, qx, qw
 
+    # ---- checkpoint conversion: GPTQ and AWQ gate/up layer to the layout ----
+    kc_, nc_, gc_ = 4096, 28672, 4096 // GS
+    conv_b = (kc_ * nc_ // 2 + gc_ * nc_ // 2 + gc_ * nc_ * 2      # qweight, qzeros, fp16 scales
+              + nc_ * kc_ // 2 + nc_ * gc_ * 4 + nc_ * gc_ // 2)   # packed, fp32 scales, zeros
+    cv_copies = 4
+    srcs = [(torch.randint(-2**31, 2**31 - 1, (kc_ // 8, nc_), dtype=torch.int32, device=dev,
+                           generator=gen),
+             torch.randint(-2**31, 2**31 - 1, (gc_, nc_ // 8), dtype=torch.int32, device=dev,
+                           generator=gen),
+             torch.empty(gc_, nc_, device=dev).uniform_(0.001, 0.05, generator=gen).half())
+            for _ in range(cv_copies)]
+    dsts = [(torch.empty(nc_, kc_ // 2, dtype=torch.uint8, device=dev),
+             torch.empty(nc_, gc_, device=dev),
+             torch.empty(nc_, gc_ // 2, dtype=torch.uint8, device=dev)) for _ in range(cv_copies)]
+
+    def conv_gptq(j: int) -> None:
+        (qw_, qz_, s_), (p_, so_, z_) = srcs[j % cv_copies], dsts[j % cv_copies]
+        ck(lib.kc_convert_gptq_int4(qw_.data_ptr(), qz_.data_ptr(), s_.data_ptr(), None, kc_, nc_,
+                                    GS, 1, p_.data_ptr(), so_.data_ptr(), z_.data_ptr(),
+                                    stream_ptr()), "kc_convert_gptq_int4")
+
+    def conv_awq(j: int) -> None:
+        (qw_, qz_, s_), (p_, so_, z_) = srcs[j % cv_copies], dsts[j % cv_copies]
+        # the same buffers read as AWQ [K, N/8] words (equal byte counts)
+        ck(lib.kc_convert_awq_int4(qw_.data_ptr(), qz_.data_ptr(), s_.data_ptr(), kc_, nc_, GS,
+                                   p_.data_ptr(), so_.data_ptr(), z_.data_ptr(), stream_ptr()),
+           "kc_convert_awq_int4")
+    convert = {"gptq": hbm(conv_b, time_launches(torch, conv_gptq, 20)),
+               "awq": hbm(conv_b, time_launches(torch, conv_awq, 20)),
+               "config": "GPTQ (original format) and AWQ checkpoints of the gate/up layer "
+                         "(K 4096, N 28672, group 128) to the reference layout; bytes read + "
+                         "written"}
+    log(f"# convert gate/up: GPTQ {convert['gptq']['avg_us']} us ({convert['gptq']['GBps']} GB/s), "
+        f"AWQ {convert['awq']['avg_us']} us ({convert['awq']['GBps']} GB/s)")
+    del srcs, dsts
+
     # ---- CPU baseline: the oracle's scalar GEMV, one host thread ----------
     cpu = None
     if args.cpu_seconds > 0:
@@ -459,6 +496,7 @@ def main() -> int:
         "fp8_cfg4": fp8_cfg4,
         "gemv_cfg0": cfg0,
         "gemm_cfg3": cfg3,
+        "convert_int4": convert,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

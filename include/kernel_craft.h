@@ -130,6 +130,31 @@ typedef struct kc_gemv_op {
 } kc_gemv_op;
 int kc_gemv_int4_bf16_chain(const kc_gemv_op* ops, int n_ops, kc_stream_t stream);
 
+/* GPTQ / AWQ INT4 checkpoints to the layout above (no counterpart in the
+ * reference, which only describes its format as GPTQ/AWQ-style,
+ * quant_int4.cu:5).  Sources, device pointers:
+ *   GPTQ: qweight int32 [K/8, N] (nibble i of word (r, n) = input k 8r+i),
+ *         qzeros int32 [K/gs, N/8] (nibble i = column 8c+i, stored minus
+ *         zero_offset: 1 for the original AutoGPTQ format, 0 for v2),
+ *         scales fp16 [K/gs, N]; perm int32 [K] or NULL: output column j
+ *         takes input k = perm[j] (act-order checkpoints: perm sorts k by
+ *         g_idx, and the caller applies the same permutation to x).
+ *   AWQ:  qweight int32 [K, N/8], qzeros int32 [K/gs, N/8] (nibble i =
+ *         column 8c + {0,2,4,6,1,3,5,7}[i]), scales fp16 [K/gs, N].
+ * Outputs: packed [N, K/2] u8, scales [N, K/gs] fp32, zeros [N, K/gs/2] u8,
+ * dequantizing to exactly (u - zu) * s (groups with zu <= 7 are stored with
+ * a negated scale, so their zero weights dequantize to -0).  Requires K, N and group_size
+ * multiples of 8, group_size dividing K, and an even K / group_size. */
+int kc_convert_gptq_int4(const int32_t* d_qweight, const int32_t* d_qzeros,
+                         const uint16_t* d_scales_f16, const int32_t* d_perm,
+                         int K, int N, int group_size, int zero_offset,
+                         uint8_t* d_packed, float* d_scales, uint8_t* d_zeros,
+                         kc_stream_t stream);
+int kc_convert_awq_int4(const int32_t* d_qweight, const int32_t* d_qzeros,
+                        const uint16_t* d_scales_f16, int K, int N, int group_size,
+                        uint8_t* d_packed, float* d_scales, uint8_t* d_zeros,
+                        kc_stream_t stream);
+
 /* Small-batch INT4 GEMM on MFMA: Y[m, n] = sum_k X[m,k] W[n,k].
  * X [m, cols] bf16 row-major, Y [m, rows] bf16 row-major, 1 <= m <= 64. */
 int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,

@@ -112,6 +112,8 @@ PROTOTYPES = {
     "kc_gemv_int4_bf16": ([_vp] * 5 + [_i, _i, _i, _vp], _i),
     "kc_gemm_int4_bf16": ([_vp] * 5 + [_i, _i, _i, _i, _vp], _i),
     "kc_gemv_int4_bf16_chain": ([_vp, _i, _vp], _i),
+    "kc_convert_gptq_int4": ([_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp], _i),
+    "kc_convert_awq_int4": ([_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp], _i),
     "kc_quantize_fp8_per_token_f32": ([_vp, _vp, _vp, _i64, _i64, _vp], _i),
     "kc_quantize_fp8_per_tensor_f32": ([_vp, _vp, _vp, _i64, _i64, _vp], _i),
     "kc_quantize_fp8_per_token_bf16": ([_vp, _vp, _vp, _i64, _i64, _vp], _i),
@@ -365,6 +367,70 @@ def int4_gemv_bf16_chain(ops) -> None:
         st = _get_lib().kc_gemv_int4_bf16_chain(ctypes.cast(arr, ctypes.c_void_p), len(ops),
                                                 _stream())
     _check("int4_gemv_bf16_chain", st)
+
+
+def act_order_permutation(g_idx, group_size: int):
+    """The input-channel order that makes an act-order GPTQ checkpoint's
+    groups contiguous: a stable sort of k by g_idx, checked to give every
+    group exactly group_size channels.  None when g_idx is already k //
+    group_size."""
+    import torch
+    g = g_idx.detach().to("cpu", torch.int64).reshape(-1)
+    K = g.numel()
+    if K % group_size:
+        raise ValueError(f"g_idx has {K} entries, not a multiple of group_size={group_size}")
+    if torch.equal(g, torch.arange(K) // group_size):
+        return None
+    counts = torch.bincount(g, minlength=K // group_size)
+    if counts.numel() != K // group_size or not bool((counts == group_size).all()):
+        raise ValueError("g_idx does not give every group exactly group_size input channels")
+    return torch.sort(g, stable=True).indices.to(torch.int32)
+
+
+def convert_gptq(qweight, qzeros, scales, g_idx=None, group_size: int = 128, zero_offset: int = 1):
+    """A GPTQ checkpoint layer (qweight int32 [K/8, N], qzeros int32 [G, N/8],
+    scales fp16 [G, N], optional g_idx [K]) to the reference layout:
+    returns (packed u8 [N, K/2], scales fp32 [N, G], zeros u8 [N, G/2], perm).
+    perm is None, or an int32 [K] tensor: the converted weights expect
+    x[perm] (act-order checkpoints).  zero_offset is 1 for the original
+    AutoGPTQ format (zero points stored minus one), 0 for its v2."""
+    import torch
+    qweight, qzeros, scales = qweight.contiguous(), qzeros.contiguous(), scales.contiguous()
+    _on_gpu(qweight, qzeros, scales)
+    K, N = qweight.shape[0] * 8, qweight.shape[1]
+    G = K // group_size
+    perm = None if g_idx is None else act_order_permutation(g_idx, group_size)
+    dperm = None if perm is None else perm.to(qweight.device)
+    packed = torch.empty(N, K // 2, dtype=torch.uint8, device=qweight.device)
+    out_s = torch.empty(N, G, dtype=torch.float32, device=qweight.device)
+    zeros = torch.empty(N, G // 2, dtype=torch.uint8, device=qweight.device)
+    with kernel_span("convert_gptq", rows=N, cols=K, group_size=group_size):
+        st = _get_lib().kc_convert_gptq_int4(_ptr(qweight), _ptr(qzeros), _ptr(scales),
+                                             _ptr(dperm) if dperm is not None else None,
+                                             K, N, group_size, zero_offset, _ptr(packed),
+                                             _ptr(out_s), _ptr(zeros), _stream())
+    _check("convert_gptq", st)
+    return packed, out_s, zeros, dperm
+
+
+def convert_awq(qweight, qzeros, scales, group_size: int = 128):
+    """An AWQ (GEMM-format) layer (qweight int32 [K, N/8], qzeros int32
+    [G, N/8], scales fp16 [G, N]) to the reference layout: returns (packed
+    u8 [N, K/2], scales fp32 [N, G], zeros u8 [N, G/2])."""
+    import torch
+    qweight, qzeros, scales = qweight.contiguous(), qzeros.contiguous(), scales.contiguous()
+    _on_gpu(qweight, qzeros, scales)
+    K, N = qweight.shape[0], qweight.shape[1] * 8
+    G = K // group_size
+    packed = torch.empty(N, K // 2, dtype=torch.uint8, device=qweight.device)
+    out_s = torch.empty(N, G, dtype=torch.float32, device=qweight.device)
+    zeros = torch.empty(N, G // 2, dtype=torch.uint8, device=qweight.device)
+    with kernel_span("convert_awq", rows=N, cols=K, group_size=group_size):
+        st = _get_lib().kc_convert_awq_int4(_ptr(qweight), _ptr(qzeros), _ptr(scales), K, N,
+                                            group_size, _ptr(packed), _ptr(out_s), _ptr(zeros),
+                                            _stream())
+    _check("convert_awq", st)
+    return packed, out_s, zeros
 
 
 def int4_gemm_bf16(packed, scales, zeros, x, rows: int, cols: int, group_size: int = 128):

@@ -230,3 +230,91 @@ def quantize_fp8_smooth_mul_bf16(w_bf16, s):
 
 def lib_path() -> str:
     return os.fspath(_LIB_PATH)
+
+
+# ---- GPTQ / AWQ checkpoint formats ------------------------------------------
+# Restated from the published packing of AutoGPTQ 0.7 and AutoAWQ 0.2 (the
+# reference ships no converter; it calls its own layout "GPTQ/AWQ-style",
+# quant_int4.cu:5).  Both dequantize as W[k, n] = (u - zu) * s with unsigned
+# nibbles u, zu in 0..15 (GPTQ's original format stores zu - 1).
+
+AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)  # nibble i of a word holds column 8c + AWQ_ORDER[i]
+
+
+def _nibbles(words):
+    w = np.ascontiguousarray(words).view(np.uint32)
+    return ((w[..., None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).astype(np.uint8)
+
+
+def gptq_unpack(qweight, qzeros, zero_offset=1):
+    """qweight int32 [K/8, N], qzeros int32 [G, N/8] -> u [K, N], zu [G, N]."""
+    u = _nibbles(qweight)                      # [K/8, N, 8]: nibble i = k 8r + i
+    u = u.transpose(0, 2, 1).reshape(-1, u.shape[1])
+    z = _nibbles(qzeros).reshape(qzeros.shape[0], -1).astype(np.int32) + zero_offset
+    return u, z
+
+
+def gptq_pack(u, zu, zero_offset=1):
+    """Inverse of gptq_unpack (zu - zero_offset must fit a nibble)."""
+    K, N = u.shape
+    uu = u.astype(np.uint32).reshape(K // 8, 8, N)
+    qweight = np.zeros((K // 8, N), np.uint32)
+    for i in range(8):
+        qweight |= uu[:, i, :] << np.uint32(4 * i)
+    zs = (zu - zero_offset).astype(np.int64)
+    assert zs.min() >= 0 and zs.max() <= 15
+    zz = zs.astype(np.uint32).reshape(zu.shape[0], N // 8, 8)
+    qzeros = np.zeros((zu.shape[0], N // 8), np.uint32)
+    for i in range(8):
+        qzeros |= zz[:, :, i] << np.uint32(4 * i)
+    return qweight.view(np.int32), qzeros.view(np.int32)
+
+
+def awq_unpack(qweight, qzeros):
+    """qweight int32 [K, N/8], qzeros int32 [G, N/8] -> u [K, N], zu [G, N]."""
+    def cols(words):
+        nib = _nibbles(words)                  # [R, N/8, 8]: nibble i -> column 8c + order[i]
+        out = np.empty_like(nib)
+        out[:, :, list(AWQ_ORDER)] = nib
+        return out.reshape(words.shape[0], -1)
+    return cols(qweight), cols(qzeros).astype(np.int32)
+
+
+def awq_pack(u, zu):
+    def words(vals):
+        R, N = vals.shape
+        v = vals.astype(np.uint32).reshape(R, N // 8, 8)
+        w = np.zeros((R, N // 8), np.uint32)
+        for i in range(8):
+            w |= v[:, :, AWQ_ORDER[i]] << np.uint32(4 * i)
+        return w.view(np.int32)
+    return words(u), words(zu)
+
+
+def int4_source_dequant(u, zu, scales16, g_idx=None, group_size=128):
+    """W [K, N] fp32 = (u - zu[g(k)]) * s[g(k)], one fp32 rounding."""
+    K = u.shape[0]
+    g = np.arange(K) // group_size if g_idx is None else np.asarray(g_idx)
+    s = np.asarray(scales16, np.float16).astype(np.float32)
+    d = (u.astype(np.int32) - zu[g]).astype(np.float32)
+    return d * s[g]
+
+
+def convert_to_reference(u, zu, scales16, perm=None, group_size=128):
+    """Reference layout (packed [N, K/2], scales [N, G] fp32, zeros [N, G/2])
+    of a source checkpoint: output column j takes input k = perm[j].  Groups
+    with zu >= 8 store q = u - 8, z = zu - 8, s; the others q = 7 - u,
+    z = 7 - zu, -s (exact: the integer difference is kept, the scale negated)."""
+    K, N = u.shape
+    kk = np.arange(K) if perm is None else np.asarray(perm)
+    uo = u[kk].T.astype(np.int32)                                 # [N, K]
+    zt = zu.T                                                     # [N, G]
+    up = zt >= 8
+    upk = np.repeat(up, group_size, axis=1)                       # [N, K]
+    q = np.where(upk, uo - 8, 7 - uo) & 0xF
+    packed = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+    z = np.where(up, zt - 8, 7 - zt).astype(np.uint8)
+    zeros = (z[:, 0::2] | (z[:, 1::2] << 4)).astype(np.uint8)
+    s = np.asarray(scales16, np.float16).astype(np.float32).T
+    scales = np.where(up, s, -s).astype(np.float32)
+    return packed, np.ascontiguousarray(scales), zeros
