@@ -114,6 +114,8 @@ PROTOTYPES = {
     "kc_gemv_int4_bf16_chain": ([_vp, _i, _vp], _i),
     "kc_convert_gptq_int4": ([_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp], _i),
     "kc_convert_awq_int4": ([_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp], _i),
+    "kc_gemm_fp8_w8a8_bf16": ([_vp] * 5 + [_i64, _i64, _i64, _vp], _i),
+    "kc_gemm_fp8_w8a8_f32": ([_vp] * 5 + [_i64, _i64, _i64, _vp], _i),
     "kc_quantize_fp8_per_token_f32": ([_vp, _vp, _vp, _i64, _i64, _vp], _i),
     "kc_quantize_fp8_per_tensor_f32": ([_vp, _vp, _vp, _i64, _i64, _vp], _i),
     "kc_quantize_fp8_per_token_bf16": ([_vp, _vp, _vp, _i64, _i64, _vp], _i),
@@ -431,6 +433,28 @@ def convert_awq(qweight, qzeros, scales, group_size: int = 128):
                                             _stream())
     _check("convert_awq", st)
     return packed, out_s, zeros
+
+
+def fp8_gemm_w8a8(qx, sx, qw, sw, out_dtype=None):
+    """Y [M, N] = sx[m] sw[n] sum_k e4m3(qx[m,k]) e4m3(qw[n,k]) on FP8 matrix
+    cores: qx int8 [M, K] / sx fp32 [M] from fp8_quantize_rows on the
+    activations, qw int8 [N, K] / sw fp32 [N] from it on the weights.
+    out_dtype torch.bfloat16 (default) or torch.float32."""
+    import torch
+    out_dtype = torch.bfloat16 if out_dtype is None else out_dtype
+    qx, sx, qw, sw = qx.contiguous(), sx.contiguous(), qw.contiguous(), sw.contiguous()
+    _on_gpu(qx, sx, qw, sw)
+    M, K = qx.shape
+    N = qw.shape[0]
+    if qw.shape[1] != K or sx.numel() != M or sw.numel() != N:
+        raise ValueError("fp8_gemm_w8a8: shapes do not match")
+    y = torch.empty(M, N, dtype=out_dtype, device=qx.device)
+    fn = (_get_lib().kc_gemm_fp8_w8a8_bf16 if out_dtype == torch.bfloat16
+          else _get_lib().kc_gemm_fp8_w8a8_f32)
+    with kernel_span("fp8_gemm_w8a8", m=M, n=N, k=K):
+        st = fn(_ptr(qx), _ptr(sx), _ptr(qw), _ptr(sw), _ptr(y), M, N, K, _stream())
+    _check("fp8_gemm_w8a8", st)
+    return y
 
 
 def int4_gemm_bf16(packed, scales, zeros, x, rows: int, cols: int, group_size: int = 128):

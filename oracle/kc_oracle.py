@@ -318,3 +318,19 @@ def convert_to_reference(u, zu, scales16, perm=None, group_size=128):
     s = np.asarray(scales16, np.float16).astype(np.float32).T
     scales = np.where(up, s, -s).astype(np.float32)
     return packed, np.ascontiguousarray(scales), zeros
+
+
+# ---- FP8 W8A8 GEMM ----------------------------------------------------------
+
+def gemm_fp8_w8a8_f64(qx, sx, qw, sw):
+    """Y[m, n] = sx[m] sw[n] sum_k e4m3(qx[m, k]) e4m3(qw[n, k]) in fp64.
+
+    The reference's FP8 GEMM is the product of the dequantized codes with the
+    per-row scales applied to the result (examples/python/transformer/
+    fp8_quant.py:55-60: quantize W and x, multiply, dequantize with the
+    combined scales); here the codes decode through kco_e4m3_decode
+    (fp8_quant.cu's E4M3 format), qx [M, K] per-token, qw [N, K] per-channel."""
+    table = e4m3_decode_table().astype(np.float64)
+    a = table[np.ascontiguousarray(qx).view(np.uint8)]
+    b = table[np.ascontiguousarray(qw).view(np.uint8)]
+    return (a @ b.T) * np.asarray(sx, np.float64)[:, None] * np.asarray(sw, np.float64)[None, :]

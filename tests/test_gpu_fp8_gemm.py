@@ -1,0 +1,154 @@
+"""W8A8 FP8 GEMM (kc_gemm_fp8_w8a8_*) on the GPU against the oracle.
+
+Y[m, n] = sx[m] sw[n] sum_k e4m3(qx[m, k]) e4m3(qw[n, k]).
+
+The matrix core's accumulation is not IEEE fp32 (measured in-bounds on
+MI355X): the products of each block of 8 consecutive k are aligned to the
+block's largest product and truncated toward zero 14 bits below its leading
+bit before the block sum joins the fp32 accumulator; E4M3 subnormals are
+exact.  So:
+  * integer-valued codes (|value| <= 16: products <= 2^8, truncation step
+    <= 2^-6, every partial sum an integer below 2^24) are exact in any
+    order, and the fp32 output must equal (float32(sum) * sx[m]) * sw[n]
+    bit for bit -- this pins the operand and result layouts of the tiles;
+  * codes over the whole finite E4M3 range: every element within the block
+    truncation bound, 8 terms x 2^-13 of the block's largest |product|
+    <= 2^-10 sum_k |product|, plus fp32 rounding; rel-L2 against the fp64
+    oracle <= 2e-4 for fp32 output (about 5e-5 measured) and <= 1e-2 for
+    bf16 output (bf16 rounding alone is ~2e-3).
+Shapes cover tile tails in M, N and K (K only needs to be a multiple of 16).
+An end-to-end case runs the quantizers' output through the GEMM."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import kc_abi
+from kc_abi import ptr, stream
+from kc_data import bf16_bits_to_f32, normal_bf16, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _finite_codes(rng, shape):
+    c = rng.integers(0, 256, shape, dtype=np.uint8)
+    c[(c & 0x7F) == 0x7F] = 0x7E        # NaN codes -> 448
+    return c.view(np.int8)
+
+
+def _integer_codes(rng, shape, table):
+    vals = np.array([c for c in range(256) if np.isfinite(table[c]) and abs(table[c]) <= 16
+                     and table[c] == np.round(table[c])], np.uint8)
+    return vals[rng.integers(0, vals.size, shape)].view(np.int8)
+
+
+def _gemm(torch, qx, sx, qw, sw, bf16):
+    M, K = qx.shape
+    N = qw.shape[0]
+    dqx, dsx, dqw, dsw = _dev(torch, qx), _dev(torch, sx), _dev(torch, qw), _dev(torch, sw)
+    if bf16:
+        y = torch.full((M, N), -7, dtype=torch.int16, device="cuda")
+        fn = kc_abi.lib().kc_gemm_fp8_w8a8_bf16
+    else:
+        y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        fn = kc_abi.lib().kc_gemm_fp8_w8a8_f32
+    print(f"kc_gemm_fp8_w8a8 {'bf16' if bf16 else 'f32'} M={M} N={N} K={K}", flush=True)
+    st = fn(ptr(dqx), ptr(dsx), ptr(dqw), ptr(dsw), ptr(y), M, N, K, stream())
+    kc_abi.check("kc_gemm_fp8_w8a8", st)
+    out = y.cpu().numpy()
+    return bf16_bits_to_f32(out.view(np.uint16)) if bf16 else out
+
+
+SHAPES = [(128, 128, 128), (1, 1, 16), (16, 16, 128), (200, 300, 272), (37, 513, 1040),
+          (256, 1024, 4096), (1000, 130, 48), (129, 129, 144), (512, 384, 8192)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_integer_codes_bit_exact(gpu, oracle, M, N, K):
+    torch = gpu
+    rng = np.random.default_rng(M * 7 + N * 3 + K)
+    table = oracle.e4m3_decode_table()
+    qx = _integer_codes(rng, (M, K), table)
+    qw = _integer_codes(rng, (N, K), table)
+    sx = rng.uniform(0.001, 2.0, M).astype(np.float32)
+    sw = rng.uniform(0.001, 2.0, N).astype(np.float32)
+    y = _gemm(torch, qx, sx, qw, sw, bf16=False)
+    acc = table[qx.view(np.uint8)].astype(np.float64) @ table[qw.view(np.uint8)].astype(np.float64).T
+    assert np.abs(acc).max() < 2 ** 24
+    want = (acc.astype(np.float32) * sx[:, None]) * sw[None, :]
+    if not np.array_equal(y.view(np.uint32), want.view(np.uint32)):
+        bad = np.argwhere(y.view(np.uint32) != want.view(np.uint32))
+        m, n = bad[0]
+        raise AssertionError(f"{len(bad)} mismatches; first at {(m, n)}: gpu {y[m, n]!r} "
+                             f"want {want[m, n]!r}")
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("bf16", [False, True])
+def test_full_range_codes_vs_oracle(gpu, oracle, M, N, K, bf16):
+    torch = gpu
+    rng = np.random.default_rng(M + N * 5 + K * 11 + bf16)
+    qx = _finite_codes(rng, (M, K))
+    qw = _finite_codes(rng, (N, K))
+    sx = rng.uniform(1e-4, 1e-2, M).astype(np.float32)
+    sw = rng.uniform(1e-4, 1e-2, N).astype(np.float32)
+    y = _gemm(torch, qx, sx, qw, sw, bf16)
+    truth = oracle.gemm_fp8_w8a8_f64(qx, sx, qw, sw)
+    assert np.all(np.isfinite(y))
+    err = rel_l2(y, truth)
+    assert err <= (1e-2 if bf16 else 2e-4), err
+    if not bf16:
+        table = np.abs(oracle.e4m3_decode_table().astype(np.float64))
+        mag = (table[qx.view(np.uint8)] @ table[qw.view(np.uint8)].T) * sx[:, None] * sw[None, :]
+        bound = 2.0 ** -10 * mag + 2.0 ** -22 * np.abs(truth) + 1e-30
+        worst = np.max(np.abs(y - truth) / bound)
+        assert worst <= 1.0, worst
+
+
+def test_quantized_linear_end_to_end(gpu, oracle):
+    """bf16 X [64, 4096] per token and W [1024, 4096] per channel through the
+    GPU quantizer, then the GEMM: equal to the oracle on the same codes, and
+    within FP8's error of the unquantized product."""
+    torch = gpu
+    M, N, K = 64, 1024, 4096
+    xb = normal_bf16((M, K), seed=31)
+    wb = normal_bf16((N, K), seed=32, std=0.02)
+    L = kc_abi.lib()
+
+    def quant(bits):
+        rows, cols = bits.shape
+        d = _dev(torch, bits.view(np.int16))
+        q = torch.empty(rows, cols, dtype=torch.int8, device="cuda")
+        s = torch.empty(rows, dtype=torch.float32, device="cuda")
+        print(f"kc_quantize_fp8_per_token_bf16 rows={rows} cols={cols}", flush=True)
+        st = L.kc_quantize_fp8_per_token_bf16(ptr(d), ptr(q), ptr(s), rows, cols, stream())
+        kc_abi.check("kc_quantize_fp8_per_token_bf16", st)
+        return q.cpu().numpy(), s.cpu().numpy()
+
+    qx, sx = quant(xb)
+    qw, sw = quant(wb)
+    eqx, esx = oracle.quantize_fp8_per_token_bf16(xb)
+    np.testing.assert_array_equal(qx, eqx)
+    np.testing.assert_array_equal(sx, esx)
+    y = _gemm(torch, qx, sx, qw, sw, bf16=True)
+    truth = oracle.gemm_fp8_w8a8_f64(qx, sx, qw, sw)
+    assert rel_l2(y, truth) < 1e-2
+    exact = bf16_bits_to_f32(xb).astype(np.float64) @ bf16_bits_to_f32(wb).astype(np.float64).T
+    assert rel_l2(y, exact) < 0.08
+
+
+def test_argument_errors(gpu):
+    L = kc_abi.lib()
+    d = ctypes.c_void_p(256)
+    for M, N, K, p in [(4, 4, 24, d), (-1, 4, 16, d), (4, 4, 16, None)]:
+        st = L.kc_gemm_fp8_w8a8_f32(p, d, d, d, d, M, N, K, None)
+        assert st == 1, (M, N, K)
+        L.kc_get_last_error()
+    st = L.kc_gemm_fp8_w8a8_bf16(ctypes.c_void_p(258), d, d, d, d, 4, 4, 16, None)
+    assert st == 1
+    L.kc_get_last_error()
+    assert L.kc_gemm_fp8_w8a8_bf16(d, d, d, d, d, 0, 4, 16, None) == 0

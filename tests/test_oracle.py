@@ -237,6 +237,36 @@ def test_e4m3_decode_table_matches_torch(oracle):
     np.testing.assert_array_equal(table[~nan], ref[~nan])
 
 
+def test_gemm_fp8_oracle_brute_force_and_torch(oracle):
+    """The W8A8 GEMM oracle: against a scalar triple loop on a tiny case, and
+    against torch's float8_e4m3fn decode + fp64 matmul with the scales
+    applied on the other side."""
+    rng = np.random.default_rng(5)
+    M, N, K = 3, 4, 16
+    qx = rng.integers(0, 256, (M, K), dtype=np.uint8)
+    qw = rng.integers(0, 256, (N, K), dtype=np.uint8)
+    qx[(qx & 0x7F) == 0x7F] = 1
+    qw[(qw & 0x7F) == 0x7F] = 2
+    sx = rng.uniform(0.1, 2, M).astype(np.float32)
+    sw = rng.uniform(0.1, 2, N).astype(np.float32)
+    y = oracle.gemm_fp8_w8a8_f64(qx.view(np.int8), sx, qw.view(np.int8), sw)
+    table = oracle.e4m3_decode_table()
+    for m in range(M):
+        for n in range(N):
+            acc = sum(float(table[qx[m, k]]) * float(table[qw[n, k]]) for k in range(K))
+            assert y[m, n] == pytest.approx(float(sx[m]) * float(sw[n]) * acc, rel=1e-13, abs=1e-300)
+    qx = rng.integers(0, 256, (40, 96), dtype=np.uint8)
+    qw = rng.integers(0, 256, (24, 96), dtype=np.uint8)
+    qx[(qx & 0x7F) == 0x7F] = 0
+    qw[(qw & 0x7F) == 0x7F] = 0
+    sx = rng.uniform(0.1, 2, 40).astype(np.float32)
+    sw = rng.uniform(0.1, 2, 24).astype(np.float32)
+    a = torch.from_numpy(qx).view(torch.float8_e4m3fn).double() * torch.from_numpy(sx).double()[:, None]
+    b = torch.from_numpy(qw).view(torch.float8_e4m3fn).double() * torch.from_numpy(sw).double()[:, None]
+    np.testing.assert_allclose(oracle.gemm_fp8_w8a8_f64(qx.view(np.int8), sx, qw.view(np.int8), sw),
+                               (a @ b.T).numpy(), rtol=1e-12, atol=1e-12)
+
+
 def _boundary_dense_patterns():
     """Every fp32 magnitude <= 448 whose low 14 mantissa bits are one of a few
     values on either side of the E4M3 rounding points (which sit at bit 19 for
