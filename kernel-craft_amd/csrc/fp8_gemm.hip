@@ -15,16 +15,32 @@
 // v_mfma_scale_f32_16x16x128_f8f6f4 accumulates them in fp32 (block scales
 // fixed at 2^0).  The scales are applied once per output: (acc * sx) * sw.
 //
-// Tiling.  A 256-thread workgroup computes a 128 x 128 tile of Y; wave w
-// owns the 64 x 64 quarter (w / 2, w % 2) as 4 x 4 MFMA tiles of 16 x 16.
-// K advances 128 at a time: the workgroup's 128 rows of qx and of qw for the
-// step (16 KB each) are staged in LDS, double-buffered, and each wave reads
-// its operands from there: lane (i, kb) of an A or B operand holds bytes
-// 32 kb .. 32 kb + 31 of row i of the 16-row block -- the same byte slots
-// for both operands, so each product pairs equal k.  LDS rows are padded to
-// 144 bytes, which spreads a 16-lane phase of 16-byte reads over all banks.
-// Workgroups are ordered so that the eight XCDs each sweep a band of
-// row tiles, sharing the qx rows in their L2.
+// Tiling.  A 512-thread workgroup (8 waves) computes a 256 x 256 tile of Y;
+// wave w owns the 128 x 64 block (w / 4, w % 4) as 8 x 4 MFMA tiles of
+// 16 x 16 (128 fp32 accumulators per lane).  K advances 128 at a time: the
+// workgroup's 256 rows of qx and 256 rows of qw for a step (32 KB each) go
+// from global memory straight into LDS (global_load_lds_dwordx4, no
+// registers in between), double-buffered, the loads for step s + 2 issued
+// as soon as step s's buffer has been read.  Each wave reads its operands
+// from LDS: lane (i, kb) of an A or B operand holds bytes 32 kb .. 32 kb + 31
+// of row i of a 16-row block -- the same byte slots for both operands, so
+// each product pairs equal k.
+//
+// LDS rows are 128 bytes with the 16-byte chunks XOR-swizzled by the row
+// (chunk c of row r at slot c ^ (r % 8)): a wave's load instruction fills 1
+// KB = 8 whole rows, and the 8 rows x 8 slots that a ds_read_b128 phase of
+// an operand read touches are all distinct banks.
+//
+// Tails.  Rows past M (N) load row M - 1 (N - 1): they only feed outputs
+// that are not stored.  In a last step with K % 128 != 0, the chunks past K
+// load the last valid chunk and the operand registers holding them are
+// zeroed before the MFMA, in both operands (so that a NaN code there cannot
+// reach a stored output).
+//
+// Order.  Workgroup b runs on XCD b % 8; each XCD takes a contiguous share
+// of the tile list, which is ordered in groups of kGroupM row tiles walked
+// column by column, so that the 32 tiles an XCD holds at once form a 4 x 8
+// block whose qx and qw rows its L2 shares.
 #include <algorithm>
 
 #include "kc_common.hpp"
@@ -34,102 +50,130 @@ namespace {
 typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void global_void;
 
-constexpr int kThreads = 256;
-constexpr int kBM = 128, kBN = 128, kBK = 128;
-constexpr int kRowPad = 144;                      // LDS bytes per staged row
-constexpr int kStage = (kBM + kBN) * kRowPad;     // one buffer: A rows then B rows
-constexpr int kE8M0One = 127;                     // block scale 2^0
+constexpr int kThreads = 512;
+constexpr int kBM = 256, kBN = 256, kBK = 128;
+constexpr int kTileBytes = kBM * kBK;            // one operand, one step
+constexpr int kStageBytes = 2 * kTileBytes;      // qx rows then qw rows
+constexpr int kLdsBytes = 2 * kStageBytes;       // double buffer: 128 KB
+constexpr int kGroupM = 4;
+constexpr int kE8M0One = 127;                    // block scale 2^0
 
-// 128 rows x 128 bytes of a [rows, K] code matrix into registers: thread t
-// loads 16 bytes of row t/8 + 32 q at byte 16 (t % 8), so that 8 lanes read
-// one row's 128 contiguous bytes.  Rows or k past the end read as zeros.
-__device__ __forceinline__ void load_tile(const int8_t* __restrict__ src, int64_t rows, int64_t K,
-                                          int64_t r0, int64_t k0, u32x4 (&v)[4]) {
-    const int t = threadIdx.x;
+// Issue the loads of one operand's 256 x 128-byte step tile into LDS.  Wave
+// w fills rows 32 w .. 32 w + 31 with four 1-KB instructions; lane l of
+// instruction i carries row 32 w + 8 i + l / 8, chunk (l % 8) ^ (l / 8).
+__device__ __forceinline__ void load_tile_lds(const int8_t* src, int64_t rows, int64_t K, int64_t r0,
+                                              int64_t k0, uint8_t* tile, int wave, int lane) {
+    const int chunk = (lane & 7) ^ (lane >> 3);
+    const int64_t k = min(k0 + 16 * chunk, K - 16);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int64_t r = r0 + t / 8 + 32 * q;
-        const int64_t k = k0 + 16 * (t % 8);
-        v[q] = u32x4{0u, 0u, 0u, 0u};
-        if (r < rows && k < K)  // K % 16 == 0: a 16-byte piece is all in or all out
-            v[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + r * K + k));
+    for (int i = 0; i < 4; ++i) {
+        const int row = 32 * wave + 8 * i + (lane >> 3);
+        const int64_t r = min(r0 + row, rows - 1);
+        __builtin_amdgcn_global_load_lds((global_void*)(src + r * K + k),
+                                         (lds_void*)(tile + (32 * wave + 8 * i) * kBK), 16, 0, 0);
     }
 }
 
-__device__ __forceinline__ void store_tile(uint8_t* lds, const u32x4 (&v)[4]) {
-    const int t = threadIdx.x;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<u32x4*>(lds + (t / 8 + 32 * q) * kRowPad + 16 * (t % 8)) = v[q];
+__device__ __forceinline__ void load_stage(const int8_t* qx, const int8_t* qw, int64_t M, int64_t N,
+                                           int64_t K, int64_t m0, int64_t n0, int64_t k0,
+                                           uint8_t* stage, int wave, int lane) {
+    load_tile_lds(qx, M, K, m0, k0, stage, wave, lane);
+    load_tile_lds(qw, N, K, n0, k0, stage + kTileBytes, wave, lane);
 }
 
-// Operand of a 16-row block starting at LDS row r0: lane (i, kb) reads
-// bytes 32 kb .. 32 kb + 31 of row r0 + i.
-__device__ __forceinline__ i32x8 read_operand(const uint8_t* lds, int r0, int lane) {
-    const uint8_t* p = lds + (r0 + (lane & 15)) * kRowPad + 32 * (lane >> 4);
-    const u32x4 lo = *reinterpret_cast<const u32x4*>(p);
-    const u32x4 hi = *reinterpret_cast<const u32x4*>(p + 16);
+// Operand of the 16-row block at tile row r0: lane (i, kb) gets bytes
+// 32 kb .. 32 kb + 31 of row r0 + i; with kvalid < 128 the 16-byte halves at
+// or past kvalid read as zeros.
+template <bool TAIL>
+__device__ __forceinline__ i32x8 read_operand(const uint8_t* tile, int r0, int lane, int kvalid) {
+    const int row = r0 + (lane & 15), kb = lane >> 4, sw = row & 7;
+    const uint8_t* p = tile + row * kBK;
+    u32x4 lo = *reinterpret_cast<const u32x4*>(p + 16 * ((2 * kb) ^ sw));
+    u32x4 hi = *reinterpret_cast<const u32x4*>(p + 16 * ((2 * kb + 1) ^ sw));
+    if constexpr (TAIL) {
+        if (32 * kb >= kvalid) lo = u32x4{0u, 0u, 0u, 0u};
+        if (32 * kb + 16 >= kvalid) hi = u32x4{0u, 0u, 0u, 0u};
+    }
     return i32x8{static_cast<int32_t>(lo.x), static_cast<int32_t>(lo.y), static_cast<int32_t>(lo.z),
                  static_cast<int32_t>(lo.w), static_cast<int32_t>(hi.x), static_cast<int32_t>(hi.y),
                  static_cast<int32_t>(hi.z), static_cast<int32_t>(hi.w)};
+}
+
+template <bool TAIL>
+__device__ __forceinline__ void mfma_step(const uint8_t* stage, int wm, int wn, int lane, int kvalid,
+                                          f32x4 (&acc)[8][4]) {
+    const uint8_t* at = stage;
+    const uint8_t* bt = stage + kTileBytes;
+    // One A operand is read ahead of the four MFMAs that use the previous
+    // one; the scheduling fences keep the compiler from hoisting all eight
+    // reads (which would not fit beside the accumulators).
+    i32x8 b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[j] = read_operand<TAIL>(bt, 64 * wn + 16 * j, lane, kvalid);
+    i32x8 a = read_operand<TAIL>(at, 128 * wm, lane, kvalid);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        i32x8 a_next = a;
+        if (i + 1 < 8) a_next = read_operand<TAIL>(at, 128 * wm + 16 * (i + 1), lane, kvalid);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b[j], acc[i][j], 0, 0, 0,
+                                                                         kE8M0One, 0, kE8M0One);
+        __builtin_amdgcn_sched_barrier(0);
+        a = a_next;
+    }
 }
 
 template <bool YBF16>
 __global__ __launch_bounds__(kThreads) void gemm_fp8_kernel(
     const int8_t* __restrict__ qx, const float* __restrict__ sx, const int8_t* __restrict__ qw,
     const float* __restrict__ sw, void* __restrict__ y, int64_t M, int64_t N, int64_t K,
-    int tiles_n, int tiles_m) {
-    extern __shared__ __align__(16) uint8_t lds[];  // [2][kBM + kBN][kRowPad]
+    int tiles_m, int tiles_n) {
+    extern __shared__ __align__(16) uint8_t lds[];  // [2 steps][qx tile, qw tile]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    // XCD-aware order: workgroup b runs on XCD b % 8; XCD x takes the
-    // (b / 8)-th tile of its contiguous share of the row-major tile list
-    // (a bijection for any grid size: XCDs x < nb % 8 get one tile more).
+    const int wm = wave >> 2, wn = wave & 3;
+
     const int b = blockIdx.x, nb = gridDim.x;
     const int x = b % 8, q = nb / 8, r = nb % 8;
-    const int lin = x * q + min(x, r) + b / 8;
-    const int tm = lin / tiles_n, tn = lin % tiles_n;
-    (void)tiles_m;
+    const int lin = x * q + min(x, r) + b / 8;      // a bijection of [0, nb)
+    const int per_group = kGroupM * tiles_n;
+    const int first_m = (lin / per_group) * kGroupM;
+    const int group_m = min(tiles_m - first_m, kGroupM);
+    const int tm = first_m + (lin % per_group) % group_m;
+    const int tn = (lin % per_group) / group_m;
     const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
 
-    f32x4 acc[4][4];
+    f32x4 acc[8][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+    // Full steps in the loop; a partial last step (K % 128 != 0) after it,
+    // so that the loop body has one code path for the accumulators.
+    const int full = static_cast<int>(K / kBK);
     const int steps = static_cast<int>((K + kBK - 1) / kBK);
-    u32x4 ra[4], rb[4];
-    load_tile(qx, M, K, m0, 0, ra);
-    load_tile(qw, N, K, n0, 0, rb);
-    store_tile(lds, ra);
-    store_tile(lds + kBM * kRowPad, rb);
-    __syncthreads();
-    for (int s = 0; s < steps; ++s) {
-        uint8_t* cur = lds + (s & 1) * kStage;
-        uint8_t* nxt = lds + ((s + 1) & 1) * kStage;
-        const bool more = s + 1 < steps;
-        if (more) {
-            load_tile(qx, M, K, m0, static_cast<int64_t>(s + 1) * kBK, ra);
-            load_tile(qw, N, K, n0, static_cast<int64_t>(s + 1) * kBK, rb);
-        }
-        i32x8 a[4], bop[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] = read_operand(cur, 64 * wm + 16 * i, lane);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) bop[j] = read_operand(cur + kBM * kRowPad, 64 * wn + 16 * j, lane);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                    a[i], bop[j], acc[i][j], 0, 0, 0, kE8M0One, 0, kE8M0One);
-        if (more) {
-            store_tile(nxt, ra);
-            store_tile(nxt + kBM * kRowPad, rb);
-        }
+    load_stage(qx, qw, M, N, K, m0, n0, 0, lds, wave, lane);
+    if (steps > 1) load_stage(qx, qw, M, N, K, m0, n0, kBK, lds + kStageBytes, wave, lane);
+    for (int s = 0; s < full; ++s) {
+        uint8_t* stage = lds + (s & 1) * kStageBytes;
+        // each stage is 8 load instructions per lane: leave the next stage's in flight
+        if (s + 1 < steps) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+        mfma_step<false>(stage, wm, wn, lane, kBK, acc);
+        __syncthreads();
+        if (s + 2 < steps)
+            load_stage(qx, qw, M, N, K, m0, n0, static_cast<int64_t>(s + 2) * kBK, stage, wave, lane);
+    }
+    if (full < steps) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        mfma_step<true>(lds + (full & 1) * kStageBytes, wm, wn, lane,
+                        static_cast<int>(K - static_cast<int64_t>(full) * kBK), acc);
     }
 
     // D layout of a 16 x 16 tile: lane (j, g) holds rows 4g + v, column j.
@@ -140,14 +184,14 @@ __global__ __launch_bounds__(kThreads) void gemm_fp8_kernel(
         if (n >= N) continue;
         const float swn = sw[n];
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
+        for (int mi = 0; mi < 8; ++mi) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int64_t m = m0 + 64 * wm + 16 * mi + 4 * g + v;
+                const int64_t m = m0 + 128 * wm + 16 * mi + 4 * g + v;
                 if (m >= M) continue;
-                const float r = (acc[mi][ni][v] * sx[m]) * swn;
-                if constexpr (YBF16) static_cast<uint16_t*>(y)[m * N + n] = kc::f32_to_bf16(r);
-                else static_cast<float*>(y)[m * N + n] = r;
+                const float rv = (acc[mi][ni][v] * sx[m]) * swn;
+                if constexpr (YBF16) static_cast<uint16_t*>(y)[m * N + n] = kc::f32_to_bf16(rv);
+                else static_cast<float*>(y)[m * N + n] = rv;
             }
         }
     }
@@ -169,15 +213,13 @@ int gemm_fp8(const char* fn, const int8_t* qx, const float* sx, const int8_t* qw
     const int64_t tm = (M + kBM - 1) / kBM, tn = (N + kBN - 1) / kBN;
     if (tm * tn > INT32_MAX)
         return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: too many tiles", fn);
-    const size_t lds = 2 * static_cast<size_t>(kStage);
     static bool attr_set = [] {
         return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_fp8_kernel<YBF16>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   static_cast<int>(2 * kStage)) == hipSuccess;
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes) == hipSuccess;
     }();
     if (!attr_set) return kc::set_error(KC_ERR_HIP, "%s: cannot raise the LDS limit", fn);
-    gemm_fp8_kernel<YBF16><<<static_cast<unsigned>(tm * tn), kThreads, lds, stream>>>(
-        qx, sx, qw, sw, y, M, N, K, static_cast<int>(tn), static_cast<int>(tm));
+    gemm_fp8_kernel<YBF16><<<static_cast<unsigned>(tm * tn), kThreads, kLdsBytes, stream>>>(
+        qx, sx, qw, sw, y, M, N, K, static_cast<int>(tm), static_cast<int>(tn));
     return kc::check_launch(fn);
 }
 
