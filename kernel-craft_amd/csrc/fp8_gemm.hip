@@ -20,16 +20,17 @@
 // 16 x 16 (128 fp32 accumulators per lane).  K advances 128 at a time: the
 // workgroup's 256 rows of qx and 256 rows of qw for a step (32 KB each) go
 // from global memory straight into LDS (global_load_lds_dwordx4, no
-// registers in between), double-buffered, the loads for step s + 2 issued
-// as soon as step s's buffer has been read.  Each wave reads its operands
+// registers in between), double-buffered: step s + 1's loads are issued
+// just before step s is multiplied.  Each wave reads its operands
 // from LDS: lane (i, kb) of an A or B operand holds bytes 32 kb .. 32 kb + 31
 // of row i of a 16-row block -- the same byte slots for both operands, so
 // each product pairs equal k.
 //
 // LDS rows are 128 bytes with the 16-byte chunks XOR-swizzled by the row
-// (chunk c of row r at slot c ^ (r % 8)): a wave's load instruction fills 1
-// KB = 8 whole rows, and the 8 rows x 8 slots that a ds_read_b128 phase of
-// an operand read touches are all distinct banks.
+// (chunk c of row r at slot c ^ ((r / 2) % 8)): a wave's load instruction
+// fills 1 KB = 8 whole rows, and the 16 lanes of a ds_read_b128 phase of an
+// operand read (16 consecutive rows, one chunk) land on 16 distinct 16-byte
+// bank groups of the 64-bank LDS.
 //
 // Tails.  Rows past M (N) load row M - 1 (N - 1): they only feed outputs
 // that are not stored.  In a last step with K % 128 != 0, the chunks past K
@@ -61,16 +62,19 @@ constexpr int kLdsBytes = 2 * kStageBytes;       // double buffer: 128 KB
 constexpr int kGroupM = 4;
 constexpr int kE8M0One = 127;                    // block scale 2^0
 
+__device__ __forceinline__ int swizzle(int row) { return (row >> 1) & 7; }
+
 // Issue the loads of one operand's 256 x 128-byte step tile into LDS.  Wave
 // w fills rows 32 w .. 32 w + 31 with four 1-KB instructions; lane l of
-// instruction i carries row 32 w + 8 i + l / 8, chunk (l % 8) ^ (l / 8).
+// instruction i carries row 32 w + 8 i + l / 8 into slot l % 8, i.e. chunk
+// (l % 8) ^ swizzle(row).
 __device__ __forceinline__ void load_tile_lds(const int8_t* src, int64_t rows, int64_t K, int64_t r0,
                                               int64_t k0, uint8_t* tile, int wave, int lane) {
-    const int chunk = (lane & 7) ^ (lane >> 3);
-    const int64_t k = min(k0 + 16 * chunk, K - 16);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int row = 32 * wave + 8 * i + (lane >> 3);
+        const int chunk = (lane & 7) ^ swizzle(row);
+        const int64_t k = min(k0 + 16 * chunk, K - 16);
         const int64_t r = min(r0 + row, rows - 1);
         __builtin_amdgcn_global_load_lds((global_void*)(src + r * K + k),
                                          (lds_void*)(tile + (32 * wave + 8 * i) * kBK), 16, 0, 0);
@@ -89,7 +93,7 @@ __device__ __forceinline__ void load_stage(const int8_t* qx, const int8_t* qw, i
 // or past kvalid read as zeros.
 template <bool TAIL>
 __device__ __forceinline__ i32x8 read_operand(const uint8_t* tile, int r0, int lane, int kvalid) {
-    const int row = r0 + (lane & 15), kb = lane >> 4, sw = row & 7;
+    const int row = r0 + (lane & 15), kb = lane >> 4, sw = swizzle(row);
     const uint8_t* p = tile + row * kBK;
     u32x4 lo = *reinterpret_cast<const u32x4*>(p + 16 * ((2 * kb) ^ sw));
     u32x4 hi = *reinterpret_cast<const u32x4*>(p + 16 * ((2 * kb + 1) ^ sw));
@@ -152,22 +156,21 @@ __global__ __launch_bounds__(kThreads) void gemm_fp8_kernel(
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Full steps in the loop; a partial last step (K % 128 != 0) after it,
-    // so that the loop body has one code path for the accumulators.
+    // One barrier per step: after it, every wave's loads of step s are in
+    // LDS and every wave has finished reading step s - 1's buffer, which then
+    // receives step s + 1 while step s is multiplied.  Full steps run in the
+    // loop, a partial last step (K % 128 != 0) after it, so that the loop
+    // body has one code path for the accumulators and ends in the MFMAs.
     const int full = static_cast<int>(K / kBK);
     const int steps = static_cast<int>((K + kBK - 1) / kBK);
     load_stage(qx, qw, M, N, K, m0, n0, 0, lds, wave, lane);
-    if (steps > 1) load_stage(qx, qw, M, N, K, m0, n0, kBK, lds + kStageBytes, wave, lane);
     for (int s = 0; s < full; ++s) {
-        uint8_t* stage = lds + (s & 1) * kStageBytes;
-        // each stage is 8 load instructions per lane: leave the next stage's in flight
-        if (s + 1 < steps) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        mfma_step<false>(stage, wm, wn, lane, kBK, acc);
-        __syncthreads();
-        if (s + 2 < steps)
-            load_stage(qx, qw, M, N, K, m0, n0, static_cast<int64_t>(s + 2) * kBK, stage, wave, lane);
+        if (s + 1 < steps)
+            load_stage(qx, qw, M, N, K, m0, n0, static_cast<int64_t>(s + 1) * kBK,
+                       lds + ((s + 1) & 1) * kStageBytes, wave, lane);
+        mfma_step<false>(lds + (s & 1) * kStageBytes, wm, wn, lane, kBK, acc);
     }
     if (full < steps) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
