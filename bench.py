@@ -22,7 +22,9 @@ beside it, each as algorithmic bytes over the average launch duration:
 `gemv_cfg0` (fp32 reference-ABI GEMV, 4096 x 4096), `gemm_cfg3` (MFMA
 small-batch GEMM, M = 4/16/64, K 8192, N 28672), `fp8_quant` (cfg1 per-token X
 and per-channel W, fp32 [4096, 4096]) and `fp8_cfg4` (SmoothQuant statistics
-and the two fused quantizers on bf16 X [16384, 8192] and W [28672, 8192]), and
+and the two fused quantizers on bf16 X [16384, 8192] and W [28672, 8192]),
+`fp8_gemm_cfg4` (the W8A8 FP8 GEMM on those codes, TFLOP/s against the FP8
+matrix peak, with torch._scaled_mm on the same codes beside it) and
 `convert_int4` (GPTQ and AWQ checkpoints of the gate/up layer to the layout).
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20]
@@ -44,6 +46,7 @@ for _p in (ROOT / "kernel-craft_amd" / "python", ROOT / "oracle"):
 
 METRIC = "INT4 GEMV HBM GB/s (% of peak) at M=1 8B shapes; FP8 quant GB/s"
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, AMD published
+PEAK_FP8_TFLOPS = 5000.0       # MI355X dense FP8 matrix peak, AMD published
 GS = 128
 LLAMA = [("qkv", 6144, 4096), ("o_proj", 4096, 4096), ("gate_up", 28672, 4096),
          ("down", 4096, 14336)]                        # (name, N, K)
@@ -410,7 +413,38 @@ def main() -> int:
     log(f"# cfg4 smoothquant+fp8: stats {t_stats:.1f} us, X {t_qx:.1f} us "
         f"({fp8_cfg4['quantize_x']['GBps']} GB/s), W {t_qw:.1f} us "
         f"({fp8_cfg4['quantize_w']['GBps']} GB/s), total {fp8_cfg4['total']['GBps']} GB/s")
-    del X4, W4, qx, qw
+
+    # ---- the W8A8 FP8 GEMM consuming cfg4's codes: Y [16384, 28672] bf16 --
+    Y4 = torch.empty(T4, N4, dtype=torch.bfloat16, device=dev)
+
+    def gemm_fp8(j: int) -> None:
+        ck(lib.kc_gemm_fp8_w8a8_bf16(qx.data_ptr(), sx.data_ptr(), qw.data_ptr(), sw.data_ptr(),
+                                     Y4.data_ptr(), T4, N4, D4, stream_ptr()),
+           "kc_gemm_fp8_w8a8_bf16")
+    gemm_flop = 2.0 * T4 * N4 * D4
+    t_gemm = time_launches(torch, gemm_fp8, 10)
+    gemm_tf = gemm_flop / (t_gemm * 1e-6) / 1e12
+    fp8_gemm = {"value": round(gemm_tf, 1), "unit": "TFLOP/s", "avg_us": round(t_gemm, 2),
+                "roofline": {"bound": "mfma", "achieved": round(gemm_tf, 1),
+                             "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(gemm_tf / PEAK_FP8_TFLOPS, 4)},
+                "config": "cfg4 consumer: Y = sx sw (qx . qw^T), qx [16384, 8192], qw [28672, "
+                          "8192] E4M3 from the cfg4 quantizers, bf16 out"}
+    # the vendor library on the same codes and scales, for reference
+    try:
+        a8 = qx.view(torch.float8_e4m3fn)
+        b8 = qw.view(torch.float8_e4m3fn)
+        sa, sb = sx.view(-1, 1), sw.view(1, -1)
+
+        def lib_gemm(j: int) -> None:
+            torch._scaled_mm(a8, b8.t(), scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
+        t_lib = time_launches(torch, lib_gemm, 10)
+        fp8_gemm["torch_scaled_mm_TFLOPs"] = round(gemm_flop / (t_lib * 1e-6) / 1e12, 1)
+    except Exception as e:  # noqa: BLE001 - a reference point only
+        fp8_gemm["torch_scaled_mm_TFLOPs"] = f"unavailable: {type(e).__name__}"
+    log(f"# fp8 gemm cfg4 consumer: {t_gemm:.1f} us, {fp8_gemm['value']} TFLOP/s "
+        f"(torch._scaled_mm: {fp8_gemm['torch_scaled_mm_TFLOPs']})")
+    del X4, W4, qx, qw, Y4
 
     # ---- checkpoint conversion: GPTQ and AWQ gate/up layer to the layout ----
     kc_, nc_, gc_ = 4096, 28672, 4096 // GS
@@ -494,6 +528,7 @@ def main() -> int:
                       "frac": round(fp8_gbs / PEAK_HBM_GBS, 4),
                       "per_channel_w": fp8_w},
         "fp8_cfg4": fp8_cfg4,
+        "fp8_gemm_cfg4": fp8_gemm,
         "gemv_cfg0": cfg0,
         "gemm_cfg3": cfg3,
         "convert_int4": convert,

@@ -11,9 +11,15 @@
 // (examples/python/transformer/fp8_quant.py:55-60), which is what the tests'
 // oracle does in fp64.
 //
-// Products of two E4M3 values are exact in fp32 (4-bit significands), and
-// v_mfma_scale_f32_16x16x128_f8f6f4 accumulates them in fp32 (block scales
-// fixed at 2^0).  The scales are applied once per output: (acc * sx) * sw.
+// Products of two E4M3 values are exact in fp32 (4-bit significands).  The
+// matrix core (v_mfma_scale_f32_16x16x128_f8f6f4, block scales fixed at 2^0)
+// does not accumulate them as IEEE fp32 adds: measured on MI355X, the
+// products of each block of 8 consecutive k are aligned to the block's
+// largest and truncated toward zero 14 bits below its leading bit before the
+// block sum joins the fp32 accumulator; E4M3 subnormals are exact.  Integer
+// valued codes (|v| <= 16) therefore come out exact, and in general each
+// output is within 2^-10 sum_k |product| of the exact sum.  The scales are
+// applied once per output: (acc * sx) * sw.
 //
 // Tiling.  A 512-thread workgroup (8 waves) computes a 256 x 256 tile of Y;
 // wave w owns the 128 x 64 block (w / 4, w % 4) as 8 x 4 MFMA tiles of
@@ -21,16 +27,17 @@
 // workgroup's 256 rows of qx and 256 rows of qw for a step (32 KB each) go
 // from global memory straight into LDS (global_load_lds_dwordx4, no
 // registers in between), double-buffered: step s + 1's loads are issued
-// just before step s is multiplied.  Each wave reads its operands
-// from LDS: lane (i, kb) of an A or B operand holds bytes 32 kb .. 32 kb + 31
-// of row i of a 16-row block -- the same byte slots for both operands, so
-// each product pairs equal k.
+// right after the step's barrier, before step s is multiplied.  Each wave
+// reads its operands from LDS: lane (i, kb) of an A or B operand holds bytes
+// 32 kb .. 32 kb + 31 of row i of a 16-row block -- the same byte slots for
+// both operands, so each product pairs equal k.  Within a step the four B
+// blocks and the first two A blocks are read first, then each A block two
+// groups of four MFMAs ahead of its use, in a pinned order.
 //
 // LDS rows are 128 bytes with the 16-byte chunks XOR-swizzled by the row
 // (chunk c of row r at slot c ^ ((r / 2) % 8)): a wave's load instruction
-// fills 1 KB = 8 whole rows, and the 16 lanes of a ds_read_b128 phase of an
-// operand read (16 consecutive rows, one chunk) land on 16 distinct 16-byte
-// bank groups of the 64-bank LDS.
+// fills 1 KB = 8 whole rows, and the operand reads (16 consecutive rows, one
+// chunk pair per lane group) measure free of bank conflicts.
 //
 // Tails.  Rows past M (N) load row M - 1 (N - 1): they only feed outputs
 // that are not stored.  In a last step with K % 128 != 0, the chunks past K
@@ -61,23 +68,42 @@ constexpr int kStageBytes = 2 * kTileBytes;      // qx rows then qw rows
 constexpr int kLdsBytes = 2 * kStageBytes;       // double buffer: 128 KB
 constexpr int kGroupM = 4;
 constexpr int kE8M0One = 127;                    // block scale 2^0
+// instruction classes of __builtin_amdgcn_sched_group_barrier
+constexpr int kSchedMfma = 0x008, kSchedDsRead = 0x100;
 
 __device__ __forceinline__ int swizzle(int row) { return (row >> 1) & 7; }
+
+// One global_load_lds_dwordx4: 16 bytes per lane from `g` into LDS at
+// lds_base + 16 * lane.  Written as inline assembly so that the compiler's
+// LDS-wait bookkeeping does not see it: with such a load in flight the
+// compiler cannot count the ordinary LDS reads and drains them all before
+// every use.  The kernel waits for these loads itself (vmcnt(0) before the
+// barrier that publishes the buffer), and the "memory" clobber keeps LDS
+// reads and writes on their side of it.
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_address(const uint8_t* p) {
+    return static_cast<uint32_t>(reinterpret_cast<size_t>((lds_void*)p));
+}
 
 // Issue the loads of one operand's 256 x 128-byte step tile into LDS.  Wave
 // w fills rows 32 w .. 32 w + 31 with four 1-KB instructions; lane l of
 // instruction i carries row 32 w + 8 i + l / 8 into slot l % 8, i.e. chunk
-// (l % 8) ^ swizzle(row).
+// (l % 8) ^ swizzle(row).  Rows past the end load the last row, chunks past
+// K the last valid chunk (their operand bytes are masked before use).
 __device__ __forceinline__ void load_tile_lds(const int8_t* src, int64_t rows, int64_t K, int64_t r0,
                                               int64_t k0, uint8_t* tile, int wave, int lane) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_address(tile + 32 * wave * kBK));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int row = 32 * wave + 8 * i + (lane >> 3);
         const int chunk = (lane & 7) ^ swizzle(row);
         const int64_t k = min(k0 + 16 * chunk, K - 16);
         const int64_t r = min(r0 + row, rows - 1);
-        __builtin_amdgcn_global_load_lds((global_void*)(src + r * K + k),
-                                         (lds_void*)(tile + (32 * wave + 8 * i) * kBK), 16, 0, 0);
+        lds_dma16(src + r * K + k, base + 8 * i * kBK);
     }
 }
 
@@ -131,6 +157,34 @@ __device__ __forceinline__ void mfma_step(const uint8_t* stage, int wm, int wn, 
     }
 }
 
+// One full step (no tail masks) with the A blocks read two groups ahead of
+// their four MFMAs, in a pinned order: B blocks and A blocks 0, 1 first,
+// then (read A block i + 2, MFMAs of A block i) for i = 0 .. 7.
+__device__ __forceinline__ void mfma_step_full(const uint8_t* stage, int wm, int wn, int lane,
+                                               f32x4 (&acc)[8][4]) {
+    const uint8_t* at = stage;
+    const uint8_t* bt = stage + kTileBytes;
+    i32x8 b[4], a[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[j] = read_operand<false>(bt, 64 * wn + 16 * j, lane, kBK);
+    a[0] = read_operand<false>(at, 128 * wm, lane, kBK);
+    a[1] = read_operand<false>(at, 128 * wm + 16, lane, kBK);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if (i + 2 < 8) a[i + 2] = read_operand<false>(at, 128 * wm + 16 * (i + 2), lane, kBK);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[i], b[j], acc[i][j], 0, 0, 0,
+                                                                         kE8M0One, 0, kE8M0One);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 12, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if (i + 2 < 8) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
+    }
+}
+
 template <bool YBF16>
 __global__ __launch_bounds__(kThreads) void gemm_fp8_kernel(
     const int8_t* __restrict__ qx, const float* __restrict__ sx, const int8_t* __restrict__ qw,
@@ -161,6 +215,10 @@ __global__ __launch_bounds__(kThreads) void gemm_fp8_kernel(
     // receives step s + 1 while step s is multiplied.  Full steps run in the
     // loop, a partial last step (K % 128 != 0) after it, so that the loop
     // body has one code path for the accumulators and ends in the MFMAs.
+    // Settle the scalar loads of the epilogue's pointers here: a scalar load
+    // still in flight in the loop would make every LDS wait a full drain
+    // (scalar loads return out of order on the same counter).
+    asm volatile("" ::"s"(y), "s"(sx), "s"(sw));
     const int full = static_cast<int>(K / kBK);
     const int steps = static_cast<int>((K + kBK - 1) / kBK);
     load_stage(qx, qw, M, N, K, m0, n0, 0, lds, wave, lane);
@@ -170,7 +228,7 @@ __global__ __launch_bounds__(kThreads) void gemm_fp8_kernel(
         if (s + 1 < steps)
             load_stage(qx, qw, M, N, K, m0, n0, static_cast<int64_t>(s + 1) * kBK,
                        lds + ((s + 1) & 1) * kStageBytes, wave, lane);
-        mfma_step<false>(lds + (s & 1) * kStageBytes, wm, wn, lane, kBK, acc);
+        mfma_step_full(lds + (s & 1) * kStageBytes, wm, wn, lane, acc);
     }
     if (full < steps) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
