@@ -301,7 +301,8 @@ __global__ __launch_bounds__(kWave) void quant_rows_wave_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// SmoothQuant quantizer, persistent: one 256-thread workgroup per row, the
+// Row quantizer, persistent (SmoothQuant, and plain per-token rows of 1024
+// 16-byte slots): one 256-thread workgroup per row, the
 // grid sized to what the device holds at once; workgroup b takes rows b,
 // b + G, b + 2G, ...  Thread t owns the 16-byte column slots t, t + 256, ...
 // (NV of them).  Its smoothing factors (and, for the division, their
@@ -388,11 +389,11 @@ template <int NV, bool BF16, Smooth S, int P, bool FULL>
 __global__ __launch_bounds__(kThreads) void quant_rows_smooth_kernel(
     const void* __restrict__ in, const float* __restrict__ smooth, int8_t* __restrict__ out,
     float* __restrict__ scales, int64_t rows, int64_t cols) {
-    static_assert(S != Smooth::kNone, "smoothing variants only");
     constexpr int kVals = BF16 ? 8 : 4;  // values per 16-byte slot
     constexpr int kF4 = kVals / 4;       // float4 per slot
     constexpr int kWaves = kThreads / kWave;
     constexpr bool kDivide = S == Smooth::kDiv;
+    constexpr bool kSmooth = S != Smooth::kNone;
     __shared__ uint32_t red[2][kWaves];  // row maxima, alternating rows
     __shared__ uint32_t red_exact[kWaves];
     __shared__ float red_min[kWaves];
@@ -405,11 +406,11 @@ __global__ __launch_bounds__(kThreads) void quant_rows_smooth_kernel(
     auto valid = [&](int j) { return FULL || tid + j * kThreads < nslots; };
 
     // Factors (quieted, as apply_smooth does) and their reciprocals.
-    f32x4 f[NV * kF4];
+    f32x4 f[kSmooth ? NV * kF4 : 1];
     f32x4 rf[kDivide ? NV * kF4 : 1];
     float smin = __builtin_inff();  // -1 once a factor is outside [2^-120, 2^120]
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
+    for (int j = 0; j < (kSmooth ? NV : 0); ++j) {
 #pragma unroll
         for (int h = 0; h < kF4; ++h) {
             f32x4 v = f32x4{1.0f, 1.0f, 1.0f, 1.0f};
@@ -473,17 +474,21 @@ __global__ __launch_bounds__(kThreads) void quant_rows_smooth_kernel(
 #pragma unroll
             for (int h = 0; h < kF4; ++h) {
                 const f32x4 x = values(b[j], h);
-                const f32x4 s = f[j * kF4 + h];
                 f32x4 v;
                 if constexpr (kDivide) {
+                    const f32x4 s = f[j * kF4 + h];
                     const f32x4 rr = rf[j * kF4 + h];
                     v = f32x4{markstein(x.x, s.x, rr.x), markstein(x.y, s.y, rr.y),
                               markstein(x.z, s.z, rr.z), markstein(x.w, s.w, rr.w)};
                     if (valid(j))
                         um = max(max(um, max(abs_bits(v.x), abs_bits(v.y))),
                                  max(abs_bits(v.z), abs_bits(v.w)));
-                } else {
+                } else if constexpr (kSmooth) {
+                    const f32x4 s = f[j * kF4 + h];
                     v = f32x4{x.x * s.x, x.y * s.y, x.z * s.z, x.w * s.w};  // fp8_quant.cu:183
+                    if (valid(j)) m = absmax4(m, v);
+                } else {
+                    v = quiet4(x);
                     if (valid(j)) m = absmax4(m, v);
                 }
                 q[j * kF4 + h] = v;
@@ -814,16 +819,18 @@ int launch_smooth(const char* fn, const void* in, const float* smooth, int8_t* o
     return kc::check_launch(fn);
 }
 
-// Persistent route for smoothing: rows of 256..1024 16-byte slots.  Returns
-// false when the shape takes another route.
+// Persistent route: rows of 256..1024 16-byte slots with smoothing, and
+// rows of exactly 1024 slots (4096 fp32 / 8192 bf16 values) without.  Plain
+// per-token rows of 1024 slots measured 7-9 % faster on this route than one
+// wave per row (cold inputs, 4096 rows); shorter plain rows were slower.
+// Returns false when the shape takes another route.
 template <bool BF16, Smooth S>
 bool try_smooth_persistent(const char* fn, const void* in, const float* smooth, int8_t* out,
                            float* scales, int64_t rows, int64_t cols, hipStream_t stream, int* st) {
-    if constexpr (S == Smooth::kNone) {
-        return false;
-    } else {
+    {
         const int64_t nslots = cols / (BF16 ? 8 : 4);
         if (nslots < kThreads || nslots > 4 * kThreads) return false;
+        if (S == Smooth::kNone && nslots != 4 * kThreads) return false;
         const bool full = nslots % kThreads == 0;
         const int64_t nv = (nslots + kThreads - 1) / kThreads;
         if (nv == 1) *st = launch_smooth<1, BF16, S, true>(fn, in, smooth, out, scales, rows, cols, stream);

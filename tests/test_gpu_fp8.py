@@ -225,22 +225,24 @@ def test_smooth_special_values(gpu, oracle, mode, dtype, cols, factors):
     _assert_codes_equal(q, eq)
 
 
-def test_per_token_bf16_special_values(gpu, oracle):
+@pytest.mark.parametrize("cols", [512, 8192])
+def test_per_token_bf16_special_values(gpu, oracle, cols):
     """bf16 rows with zeros, -0, NaN, inf, denormals and tiny absmax values
-    (the scale routes that divide exactly) through the one-wave kernel."""
+    (the scale routes that divide exactly) through the one-wave kernel (512)
+    and the persistent one (8192)."""
     rng = np.random.default_rng(11)
-    x = rng.standard_normal((10, 512)).astype(np.float32)
+    x = rng.standard_normal((10, cols)).astype(np.float32)
     x[0] = 0.0
     x[1] = -0.0
     x[2, ::5] = np.nan
     x[3, 7] = np.inf
-    x[4] = np.float32(2.0 ** -130) * np.sign(rng.standard_normal(512)).astype(np.float32)  # denormal bf16
-    x[5] = np.float32(2.0 ** -70) * rng.standard_normal(512).astype(np.float32)          # absmax < 2^-60
-    x[6] = np.float32(3e38) * rng.uniform(-1, 1, 512).astype(np.float32)
+    x[4] = np.float32(2.0 ** -130) * np.sign(rng.standard_normal(cols)).astype(np.float32)  # denormal bf16
+    x[5] = np.float32(2.0 ** -70) * rng.standard_normal(cols).astype(np.float32)          # absmax < 2^-60
+    x[6] = np.float32(3e38) * rng.uniform(-1, 1, cols).astype(np.float32)
     x[7, :] = np.nan
-    x[8] = np.float32(2.0 ** -100) * rng.standard_normal(512).astype(np.float32)
+    x[8] = np.float32(2.0 ** -100) * rng.standard_normal(cols).astype(np.float32)
     x[8, 3] = 1.0                                # tiny elements under a normal absmax
-    x[9] = np.float32(2.0) ** rng.integers(-40, 40, 512).astype(np.float32)
+    x[9] = np.float32(2.0) ** rng.integers(-40, 40, cols).astype(np.float32)
     xb = f32_to_bf16_bits(x)
     q, s = _per_token_bf16(gpu, xb)
     eq, es = oracle.quantize_fp8_per_token_bf16(xb)
@@ -248,9 +250,11 @@ def test_per_token_bf16_special_values(gpu, oracle):
     _assert_codes_equal(q, eq)
 
 
-def test_per_token_special_values(gpu, oracle):
+@pytest.mark.parametrize("cols", [256, 4096])
+def test_per_token_special_values(gpu, oracle, cols):
+    """One-wave kernel (256) and persistent kernel (4096 columns)."""
     rng = np.random.default_rng(7)
-    x = rng.standard_normal((15, 256)).astype(np.float32)
+    x = rng.standard_normal((15, cols)).astype(np.float32)
     x[0] = 0.0                                   # all zero -> scale 1
     x[1] = -0.0                                  # -0 -> code 0x80
     x[2, ::7] = np.nan                           # NaN ignored by absmax, -> +448
@@ -258,13 +262,13 @@ def test_per_token_special_values(gpu, oracle):
     x[4, 9] = -np.inf
     x[5] = np.float32(1e-42)                     # denormal absmax -> denormal scale
     x[5, ::2] = np.float32(-1e-42)
-    x[6] = rng.uniform(-1, 1, 256).astype(np.float32) * np.float32(3e38)   # huge, finite
-    x[7] = np.float32(2.0 ** -126) * rng.standard_normal(256).astype(np.float32)
+    x[6] = rng.uniform(-1, 1, cols).astype(np.float32) * np.float32(3e38)   # huge, finite
+    x[7] = np.float32(2.0 ** -126) * rng.standard_normal(cols).astype(np.float32)
     x[8, :] = np.nan                             # all NaN -> scale 1, codes +448
-    x[9] = rng.standard_normal(256).astype(np.float32) * np.float32(1e-30)
+    x[9] = rng.standard_normal(cols).astype(np.float32) * np.float32(1e-30)
     x[10, 0] = np.float32(448.0)                 # exact max
-    x[11] = np.float32(2.0) ** rng.integers(-20, 20, 256).astype(np.float32)
-    x[12] = np.float32(1e-44) * np.sign(rng.standard_normal(256)).astype(np.float32)  # scale 0
+    x[11] = np.float32(2.0) ** rng.integers(-20, 20, cols).astype(np.float32)
+    x[12] = np.float32(1e-44) * np.sign(rng.standard_normal(cols)).astype(np.float32)  # scale 0
     x[12, 3] = 0.0
     snan = np.array([0x7F800001, 0x7FA00000, 0xFF800001, 0xFFBFFFFF], np.uint32).view(np.float32)
     x[13, :4] = snan                             # signaling NaNs: ignored, -> +448
@@ -275,9 +279,11 @@ def test_per_token_special_values(gpu, oracle):
     _assert_codes_equal(q, eq)
 
 
-def test_per_token_rounding_boundaries(gpu, oracle):
+@pytest.mark.parametrize("cols", [512, 4096])
+def test_per_token_rounding_boundaries(gpu, oracle, cols):
     """Inputs whose quotient x/scale lands on E4M3 rounding midpoints and on
-    their fp32 neighbours: the divide must be correctly rounded."""
+    their fp32 neighbours: the divide must be correctly rounded (one-wave
+    kernel at 512 columns, persistent kernel at 4096)."""
     rng = np.random.default_rng(11)
     table = oracle.e4m3_decode_table()
     pos = np.sort(table[:0x7F])                       # finite non-negative values
@@ -289,8 +295,8 @@ def test_per_token_rounding_boundaries(gpu, oracle):
         vals = (mids.astype(np.float64) * np.float64(scale)).astype(np.float32)
         vals = np.concatenate([vals, np.nextafter(vals, np.float32(np.inf)),
                                np.nextafter(vals, np.float32(0))])
-        row = np.resize(vals, 512).astype(np.float32)
-        row *= np.where(rng.random(512) < 0.5, -1, 1).astype(np.float32)
+        row = np.resize(vals, cols).astype(np.float32)
+        row *= np.where(rng.random(cols) < 0.5, -1, 1).astype(np.float32)
         row[0] = amax
         rows.append(row)
     x = np.stack(rows)
