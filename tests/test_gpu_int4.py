@@ -264,7 +264,15 @@ def test_gemm_cfg3(gpu, oracle, m):
 
 @pytest.mark.parametrize("m,rows,cols,gs", [(1, 100, 1024, 128), (3, 64, 256, 128),
                                             (17, 130, 2048, 256), (33, 48, 640, 128),
-                                            (64, 16, 128, 128), (5, 40, 512, 64)])
+                                            (64, 16, 128, 128), (5, 40, 512, 64),
+                                            # M <= 4, X resident in LDS: ragged row
+                                            # tiles, spare waves, odd T-block counts,
+                                            # larger groups
+                                            (2, 250, 384, 128), (1, 17, 128, 128),
+                                            (4, 1000, 1280, 256), (3, 4096, 4096, 128),
+                                            (4, 7 * 16 * 3 + 5, 2048, 512),
+                                            # M <= 4 whose X does not fit in LDS
+                                            (4, 33, 32768, 128)])
 def test_gemm_shapes(gpu, oracle, m, rows, cols, gs):
     packed, scales, zeros = make_int4(rows, cols, gs, seed=m * 1000 + rows)
     xb = normal_bf16((m, cols), seed=m + rows)
