@@ -441,20 +441,22 @@ int launch_mfma(const char* fn, const uint8_t* packed, const float* scales, cons
 }
 
 // ---------------------------------------------------------------------------
-// Small M (1..4): X resident in LDS.  Each wave streams one 16-row weight
-// tile over the whole of K with no barrier in its loop: X (all M rows, all
-// K) is staged once per workgroup in the B-operand pair layout with its
-// T-block sums, and each wave stages the fold coefficients (s and
-// c2 = -s * (136 + z)) of its 16 rows for every group.  The wave keeps
-// D T-blocks of its weights in flight in a register ring (16 bytes per lane
-// per T-block, issued D T-blocks ahead of their use).  A workgroup of W
-// waves owns W consecutive row tiles; the launcher picks W so that the
-// grid matches the CUs where it can.
+// Small M (2..16): X resident in LDS.  Each wave streams one 16-row weight
+// tile over the whole of K with no barrier in its loop: X (all M rows) is
+// staged in the B-operand pair layout with its T-block sums -- all of K at
+// once when it fits, else in P phases of K / P (one restaging, between two
+// barriers, per phase) -- and each wave stages the fold coefficients
+// (s and c2 = -s * (136 + z)) of its 16 rows for every group once.  The wave
+// keeps D T-blocks of its weights in flight in a register ring (16 bytes per
+// lane per T-block, issued D T-blocks ahead of their use), across phases.
+// A workgroup of W waves owns W consecutive row tiles; W = 7 gives one
+// workgroup per CU at N = 28672.
 //
-// LDS: X slots [T][step w4][m][kb] (16 bytes each), X sums [T][m] (padded
-// to 16 bytes), then per wave cs[16 rows][g], cz[16 rows][g].
+// LDS: X slots [T of the phase][step w4][m][kb] (16 bytes each), X sums
+// [T of the phase][m] (padded to 16 bytes), then per wave cs[16 rows][g],
+// cz[16 rows][g].
 // ---------------------------------------------------------------------------
-constexpr int kXresMaxM = 4;
+constexpr int kXresMaxM = 16;
 
 // Sum over each 16-lane row of the wave with DPP rotations (VALU only).
 template <int CTRL>
@@ -470,25 +472,26 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-__host__ __device__ constexpr size_t xres_lds_bytes(int M, int K, int G, int W) {
-    return static_cast<size_t>(K / kTBlock) * 4 * M * 4 * 16 +   // X slots
-           static_cast<size_t>((K / kTBlock * M + 3) & ~3) * 4 +  // X sums, padded to 16 bytes
-           static_cast<size_t>(W) * 2 * G * 16 * 4;              // cs, cz per wave
+__host__ __device__ constexpr size_t xres_lds_bytes(int M, int K, int G, int W, int P) {
+    return static_cast<size_t>(K / kTBlock / P) * 4 * M * 4 * 16 +   // X slots of a phase
+           static_cast<size_t>((K / kTBlock / P * M + 3) & ~3) * 4 +  // X sums, padded to 16 bytes
+           static_cast<size_t>(W) * 2 * G * 16 * 4;                  // cs, cz per wave
 }
 
 template <int W, int D>
 __global__ __launch_bounds__(W * kWave) void gemm_int4_xres_kernel(
     const uint8_t* __restrict__ packed, const float* __restrict__ scales,
     const uint8_t* __restrict__ zeros, const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
-    int M, int N, int K, int gshift) {
+    int M, int N, int K, int gshift, int P) {
     extern __shared__ __align__(16) char lds[];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x >> 6;
     const int nT = K / kTBlock;
+    const int nTp = nT / P;                         // T-blocks per phase (the launcher: D divides it)
     const int G = nT >> gshift;
     u32x4* xslot = reinterpret_cast<u32x4*>(lds);
-    float* xsum = reinterpret_cast<float*>(xslot + static_cast<size_t>(nT) * 16 * M);
-    float* cs = xsum + ((nT * M + 3) & ~3) + wave * 2 * G * 16;  // 16-byte aligned
+    float* xsum = reinterpret_cast<float*>(xslot + static_cast<size_t>(nTp) * 16 * M);
+    float* cs = xsum + ((nTp * M + 3) & ~3) + wave * 2 * G * 16;  // 16-byte aligned
     float* cz = cs + G * 16;
     const int ntiles = (N + 15) / 16;
     const int tile = min(static_cast<int>(blockIdx.x) * W + wave, ntiles - 1);  // spare waves redo the last tile's math, store nothing
@@ -501,123 +504,131 @@ __global__ __launch_bounds__(W * kWave) void gemm_int4_xres_kernel(
     const u32x4* wrow = reinterpret_cast<const u32x4*>(packed + static_cast<int64_t>(min(row0 + i, N - 1)) * (K >> 1));
     u32x4 w[D];
 
-    // 2-3. Staging: X into the pair layout, and this wave's fold
-    // coefficients.  Every load of a batch (kXBatch X pieces per thread,
-    // 16 rows of coefficients per lane) is issued before the first is used,
-    // so that staging costs one memory round trip, not one per item; index
-    // arithmetic avoids divisions by run-time values, and the T-block sums
-    // reduce with DPP (no LDS round trips).
-    //   X: piece p of row m is X[m][8p .. 8p+7]: the B operand of T-block
-    //   p / 16, step p % 4, lane kb = (p / 4) % 4; 16 consecutive pieces (one
-    //   T-block of one row) sit in 16 consecutive lanes, which sum them.
-    //   Coefficients: cs[row][g] = s, cz[row][g] = -s * (136 + z).
-    constexpr int kXBatch = 16;
-    const int ppr = K >> 3;  // X pieces per row
+    // Staging of a phase's X: piece p of row m is X[m][8 p .. 8 p + 7] of the
+    // phase: the B operand of T-block p / 16, step p % 4, lane kb = (p / 4) %
+    // 4; 16 consecutive pieces (one T-block of one row) sit in 16 consecutive
+    // lanes, which sum them with DPP.  Every load of a batch (kXBatch pieces
+    // per thread) is issued before the first is used, so that a batch costs
+    // one memory round trip; (idx + 0.5) / ppr in fp32 gives the row exactly
+    // (idx < 2^24, and the quotient is never within 0.5 / ppr of an integer).
+    // With the first phase the wave also stages its coefficients,
+    // cs[row][g] = s, cz[row][g] = -s * (136 + z) (16 rows per lane, lane
+    // g + 64 j of each row), and fills its weight ring.
+    constexpr int kXBatch = 10;  // 4480 pieces per pass: M 16 x 2048 k, or M 4 x 8192 k
+    const int ppr = nTp * 16;                       // X pieces per row and phase
     const int npieces = M * ppr;
-    auto piece = [&](int idx, int& m, int& p) {  // idx -> (row m, piece p); M <= 4
-        m = (idx >= ppr) + (idx >= 2 * ppr) + (idx >= 3 * ppr);
-        p = idx - m * ppr;
-    };
-    // the coefficients: 16 rows x G groups, lane g + 64 j of each row;
-    // issued with the first X batch
+    const float inv_ppr = 1.0f / static_cast<float>(ppr);
     const int cpasses = (G + kWave - 1) / kWave;
-    for (int xbase = 0; xbase < npieces; xbase += kXBatch * W * kWave) {
-        u32x4 dv[kXBatch];
+    auto stage = [&](int phase) {
+        for (int xbase = 0; xbase < npieces; xbase += kXBatch * W * kWave) {
+            u32x4 dv[kXBatch];
 #pragma unroll
-        for (int b = 0; b < kXBatch; ++b) {
-            int m, p;
-            piece(min(xbase + b * W * kWave + static_cast<int>(threadIdx.x), npieces - 1), m, p);
-            dv[b] = *reinterpret_cast<const u32x4*>(X + static_cast<int64_t>(m) * K + 8 * p);
-        }
-        if (xbase == 0) {
-            for (int j = 0; j < cpasses; ++j) {
-                const int g = min(lane + kWave * j, G - 1);
-                float sv[16];
-                uint32_t zb[16];
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int64_t row = min(row0 + r, N - 1);
-                    sv[r] = scales[row * G + g];
-                    zb[r] = zeros[row * (G >> 1) + (g >> 1)];
-                }
-                if (lane + kWave * j < G) {
+            for (int b = 0; b < kXBatch; ++b) {
+                const int idx = min(xbase + b * W * kWave + static_cast<int>(threadIdx.x), npieces - 1);
+                const int m = static_cast<int>((static_cast<float>(idx) + 0.5f) * inv_ppr);
+                const int p = idx - m * ppr;
+                dv[b] = *reinterpret_cast<const u32x4*>(X + static_cast<int64_t>(m) * K +
+                                                        8 * (static_cast<int64_t>(phase) * ppr + p));
+            }
+            if (phase == 0 && xbase == 0) {
+                for (int j = 0; j < cpasses; ++j) {
+                    const int g = min(lane + kWave * j, G - 1);
+                    float sv[16];
+                    uint32_t zb[16];
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        const uint32_t z = (g & 1) ? (zb[r] >> 4) : (zb[r] & 0xFu);
-                        cs[r * G + g] = sv[r];  // [row][g]: consecutive lanes, consecutive words
-                        cz[r * G + g] = -sv[r] * static_cast<float>(136u + z);
+                        const int64_t row = min(row0 + r, N - 1);
+                        sv[r] = scales[row * G + g];
+                        zb[r] = zeros[row * (G >> 1) + (g >> 1)];
+                    }
+                    if (lane + kWave * j < G) {
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const uint32_t z = (g & 1) ? (zb[r] >> 4) : (zb[r] & 0xFu);
+                            cs[r * G + g] = sv[r];  // [row][g]: consecutive lanes, consecutive words
+                            cz[r * G + g] = -sv[r] * static_cast<float>(136u + z);
+                        }
                     }
                 }
-            }
 #pragma unroll
-            for (int u = 0; u < D; ++u) w[u] = wrow[min(u, nT - 1) * 4 + kb];
-        }
-        uint32_t sel_lo, sel_hi;  // v_perm_b32 selectors, in VGPRs
-        asm volatile("v_mov_b32 %0, 0x05040100" : "=v"(sel_lo));
-        asm volatile("v_mov_b32 %0, 0x07060302" : "=v"(sel_hi));
-        const uint32_t ones = 0x3F803F80u;
+                for (int u = 0; u < D; ++u) w[u] = wrow[min(u, nT - 1) * 4 + kb];
+            }
+            uint32_t sel_lo, sel_hi;  // v_perm_b32 selectors, in VGPRs
+            asm volatile("v_mov_b32 %0, 0x05040100" : "=v"(sel_lo));
+            asm volatile("v_mov_b32 %0, 0x07060302" : "=v"(sel_hi));
+            const uint32_t ones = 0x3F803F80u;
 #pragma unroll
-        for (int b = 0; b < kXBatch; ++b) {
-            const int idx = xbase + b * W * kWave + static_cast<int>(threadIdx.x);
-            const bool valid = idx < npieces;
-            int m, p;
-            piece(valid ? idx : 0, m, p);
-            const u32x4 d = valid ? dv[b] : u32x4{0u, 0u, 0u, 0u};
-            u32x4 q;
-            q.x = __builtin_amdgcn_perm(d.z, d.x, sel_lo);  // (x0, x4)
-            q.y = __builtin_amdgcn_perm(d.z, d.x, sel_hi);  // (x1, x5)
-            q.z = __builtin_amdgcn_perm(d.w, d.y, sel_lo);  // (x2, x6)
-            q.w = __builtin_amdgcn_perm(d.w, d.y, sel_hi);  // (x3, x7)
-            float sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.x), as_bf16x2(ones), 0.0f, false);
-            sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.y), as_bf16x2(ones), sm, false);
-            sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.z), as_bf16x2(ones), sm, false);
-            sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.w), as_bf16x2(ones), sm, false);
-            sm = row16_sum(sm);  // the T-block's 16 pieces, in one 16-lane row
-            if (valid) {
-                const int T = p >> 4, w4 = p & 3, pkb = (p >> 2) & 3;
-                xslot[((T * 4 + w4) * M + m) * 4 + pkb] = q;
-                if ((p & 15) == 0) xsum[T * M + m] = sm;
+            for (int b = 0; b < kXBatch; ++b) {
+                const int idx0 = xbase + b * W * kWave + static_cast<int>(threadIdx.x);
+                const bool valid = idx0 < npieces;
+                const int idx = valid ? idx0 : 0;
+                const int m = static_cast<int>((static_cast<float>(idx) + 0.5f) * inv_ppr);
+                const int p = idx - m * ppr;
+                const u32x4 d = valid ? dv[b] : u32x4{0u, 0u, 0u, 0u};
+                u32x4 q;
+                q.x = __builtin_amdgcn_perm(d.z, d.x, sel_lo);  // (x0, x4)
+                q.y = __builtin_amdgcn_perm(d.z, d.x, sel_hi);  // (x1, x5)
+                q.z = __builtin_amdgcn_perm(d.w, d.y, sel_lo);  // (x2, x6)
+                q.w = __builtin_amdgcn_perm(d.w, d.y, sel_hi);  // (x3, x7)
+                float sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.x), as_bf16x2(ones), 0.0f, false);
+                sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.y), as_bf16x2(ones), sm, false);
+                sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.z), as_bf16x2(ones), sm, false);
+                sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.w), as_bf16x2(ones), sm, false);
+                sm = row16_sum(sm);  // the T-block's 16 pieces, in one 16-lane row
+                if (valid) {
+                    const int T = p >> 4, w4 = p & 3, pkb = (p >> 2) & 3;
+                    xslot[((T * 4 + w4) * M + m) * 4 + pkb] = q;
+                    if ((p & 15) == 0) xsum[T * M + m] = sm;
+                }
             }
         }
-    }
+    };
+    stage(0);
     __syncthreads();
 
-    // 4. stream the weights: T-block T's four MFMA steps with X from LDS,
-    //    folded into acc (rows 4 kb + v of the tile, activation row i)
+    // Stream the weights: T-block T's four MFMA steps with X from LDS,
+    // folded into acc (rows 4 kb + v of the tile, activation row i).
     const NibConsts nk = nib_consts();
     const bool xlane = i < M;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int T0 = 0; T0 < nT; T0 += D) {
+    for (int ph = 0; ph < P; ++ph) {
+        for (int T0 = ph * nTp; T0 < (ph + 1) * nTp; T0 += D) {
 #pragma unroll
-        for (int u = 0; u < D; ++u) {
-            const int T = T0 + u;
-            if (T >= nT) continue;  // uniform; a guard, not a break, keeps the ring's indices static
-            bf16x8_t b[4];
-            float xs = 0.0f;
+            for (int u = 0; u < D; ++u) {
+                const int T = T0 + u;
+                const int Tl = T - ph * nTp;
+                bf16x8_t b[4];
+                float xs = 0.0f;
 #pragma unroll
-            for (int w4 = 0; w4 < 4; ++w4) b[w4] = bf16x8_t{};
-            if (xlane) {
+                for (int w4 = 0; w4 < 4; ++w4) b[w4] = bf16x8_t{};
+                if (xlane) {
 #pragma unroll
-                for (int w4 = 0; w4 < 4; ++w4)
-                    b[w4] = __builtin_bit_cast(bf16x8_t, xslot[((T * 4 + w4) * M + i) * 4 + kb]);
-                xs = xsum[T * M + i];
+                    for (int w4 = 0; w4 < 4; ++w4)
+                        b[w4] = __builtin_bit_cast(bf16x8_t, xslot[((Tl * 4 + w4) * M + i) * 4 + kb]);
+                    xs = xsum[Tl * M + i];
+                }
+                const int g = T >> gshift;
+                const float* cr = cs + 4 * kb * G + g;  // rows 4 kb .. 4 kb + 3
+                const float* zr = cz + 4 * kb * G + g;
+                const f32x4 s4 = {cr[0], cr[G], cr[2 * G], cr[3 * G]};
+                const f32x4 z4 = {zr[0], zr[G], zr[2 * G], zr[3 * G]};
+                const u32x4 wv = w[u];
+                f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_operand(wv.x, nk), b[0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_operand(wv.y, nk), b[1], d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_operand(wv.z, nk), b[2], d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_operand(wv.w, nk), b[3], d, 0, 0, 0);
+                acc.x = fmaf(s4.x, d.x, fmaf(z4.x, xs, acc.x));
+                acc.y = fmaf(s4.y, d.y, fmaf(z4.y, xs, acc.y));
+                acc.z = fmaf(s4.z, d.z, fmaf(z4.z, xs, acc.z));
+                acc.w = fmaf(s4.w, d.w, fmaf(z4.w, xs, acc.w));
+                // refill the ring slot: T-block T + D (past the end: the last one again)
+                w[u] = wrow[min(T + D, nT - 1) * 4 + kb];
             }
-            const int g = T >> gshift;
-            const float* cr = cs + 4 * kb * G + g;  // rows 4 kb .. 4 kb + 3
-            const float* zr = cz + 4 * kb * G + g;
-            const f32x4 s4 = {cr[0], cr[G], cr[2 * G], cr[3 * G]};
-            const f32x4 z4 = {zr[0], zr[G], zr[2 * G], zr[3 * G]};
-            const u32x4 wv = w[u];
-            f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_operand(wv.x, nk), b[0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_operand(wv.y, nk), b[1], d, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_operand(wv.z, nk), b[2], d, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_operand(wv.w, nk), b[3], d, 0, 0, 0);
-            acc.x = fmaf(s4.x, d.x, fmaf(z4.x, xs, acc.x));
-            acc.y = fmaf(s4.y, d.y, fmaf(z4.y, xs, acc.y));
-            acc.z = fmaf(s4.z, d.z, fmaf(z4.z, xs, acc.z));
-            acc.w = fmaf(s4.w, d.w, fmaf(z4.w, xs, acc.w));
-            // refill the ring slot: T-block T + D (past the end: the last one again)
-            w[u] = wrow[min(T + D, nT - 1) * 4 + kb];
+        }
+        if (ph + 1 < P) {  // uniform: restage X for the next phase
+            __syncthreads();
+            stage(ph + 1);
+            __syncthreads();
         }
     }
 
@@ -632,11 +643,25 @@ __global__ __launch_bounds__(W * kWave) void gemm_int4_xres_kernel(
     }
 }
 
+// Phases of K for the X-resident kernel: the fewest (1, 2, 4, ...) whose LDS
+// fits, with D dividing the T-blocks of a phase; 0 when none does.
+constexpr int kXresW = 7, kXresD = 8;
+
+inline int xres_phases(int M, int K, int G) {
+    const int nT = K / kTBlock;
+    for (int P = 1; P <= nT; P *= 2) {
+        if (nT % P != 0 || (nT / P) % kXresD != 0) break;
+        if (xres_lds_bytes(M, K, G, kXresW, P) <= 160 * 1024) return P;
+    }
+    return 0;
+}
+
 template <int W, int D>
 int launch_xres(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
-                const uint16_t* X, uint16_t* Y, int M, int N, int K, int gshift, hipStream_t stream) {
+                const uint16_t* X, uint16_t* Y, int M, int N, int K, int gshift, int P,
+                hipStream_t stream) {
     const int G = (K / kTBlock) >> gshift;
-    const size_t lds = xres_lds_bytes(M, K, G, W);
+    const size_t lds = xres_lds_bytes(M, K, G, W, P);
     static bool attr_set = [] {
         return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_int4_xres_kernel<W, D>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
@@ -644,7 +669,8 @@ int launch_xres(const char* fn, const uint8_t* packed, const float* scales, cons
     if (!attr_set) return kc::set_error(KC_ERR_HIP, "%s: cannot raise the LDS limit", fn);
     const int ntiles = (N + 15) / 16;
     const unsigned grid = static_cast<unsigned>((ntiles + W - 1) / W);
-    gemm_int4_xres_kernel<W, D><<<grid, W * kWave, lds, stream>>>(packed, scales, zeros, X, Y, M, N, K, gshift);
+    gemm_int4_xres_kernel<W, D><<<grid, W * kWave, lds, stream>>>(packed, scales, zeros, X, Y, M, N, K,
+                                                                   gshift, P);
     return kc::check_launch(fn);
 }
 
@@ -680,12 +706,13 @@ extern "C" int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
         return KC_SUCCESS;
     }
     const int gshift = kc::ilog2(group_size) - 7;
-    // M <= 4: the X-resident kernel when its LDS fits (7 waves per
-    // workgroup: N = 28672 gives one workgroup per CU).
+    // M <= 16: the X-resident kernel when its LDS fits in some number of
+    // phases of K.
     if (m <= kXresMaxM) {
-        const int G = (cols / kTBlock) >> gshift;
-        if (xres_lds_bytes(m, cols, G, 7) <= 160 * 1024)
-            return launch_xres<7, 8>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream);
+        const int P = xres_phases(m, cols, (cols / kTBlock) >> gshift);
+        if (P > 0)
+            return launch_xres<kXresW, kXresD>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols,
+                                               gshift, P, stream);
     }
     // m-tiles of 16 activation rows; with more of them each B operand read
     // from LDS is reused across two weight row tiles.

@@ -272,7 +272,12 @@ def test_gemm_cfg3(gpu, oracle, m):
                                             (4, 1000, 1280, 256), (3, 4096, 4096, 128),
                                             (4, 7 * 16 * 3 + 5, 2048, 512),
                                             # M <= 4 whose X does not fit in LDS
-                                            (4, 33, 32768, 128)])
+                                            (4, 33, 32768, 128),
+                                            # M 5..16: X in LDS in one, two and four
+                                            # phases of K
+                                            (16, 48, 1024, 128), (8, 300, 4096, 128),
+                                            (12, 257, 2048, 256), (16, 100, 8192, 128),
+                                            (6, 7 * 16 + 1, 8192, 512)])
 def test_gemm_shapes(gpu, oracle, m, rows, cols, gs):
     packed, scales, zeros = make_int4(rows, cols, gs, seed=m * 1000 + rows)
     xb = normal_bf16((m, cols), seed=m + rows)
