@@ -674,6 +674,242 @@ int launch_xres(const char* fn, const uint8_t* packed, const float* scales, cons
     return kc::check_launch(fn);
 }
 
+// ---------------------------------------------------------------------------
+// M 33..64: X resident in LDS, four activation tiles.  Each wave owns RT
+// 16-row weight tiles (consecutive) over the whole of K and every
+// activation row: per T-block it decodes each tile's A operands once and
+// runs them against the MT = 4 activation tiles' B operands from LDS (each
+// B read serves the RT weight tiles).  X is too large to hold whole (64 x
+// 8192 bf16 = 1 MB), so it passes through LDS in phases of NTP T-blocks,
+// double-buffered: the next phase's X is loaded into registers at the start
+// of a phase and written to the other buffer after the phase's math, with
+// one barrier per phase.  Weights stream through a D-deep register ring
+// (D a multiple of NTP, so phase switches sit at fixed places of the ring).
+// Coefficients per wave: scales [row][g] and zero nibbles [row][g] bytes.
+// ---------------------------------------------------------------------------
+constexpr int kXbigMT = 4;
+
+__host__ __device__ constexpr size_t xbig_lds_bytes(int M, int G, int W, int RT, int NTP) {
+    return 2 * static_cast<size_t>(NTP) * 4 * M * 4 * 16 +          // X slots, two phases
+           2 * static_cast<size_t>((NTP * M + 3) & ~3) * 4 +         // X sums, two phases
+           static_cast<size_t>(W) * RT * 16 * G * 5 +                // scales + zero bytes per wave
+           16;                                                        // alignment slack
+}
+
+template <int W, int RT, int NTP, int D>
+__global__ __launch_bounds__(W * kWave) void gemm_int4_xbig_kernel(
+    const uint8_t* __restrict__ packed, const float* __restrict__ scales,
+    const uint8_t* __restrict__ zeros, const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
+    int M, int N, int K, int gshift) {
+    static_assert(D % NTP == 0, "phase switches at fixed ring positions");
+    constexpr int MT = kXbigMT;
+    extern __shared__ __align__(16) char lds[];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x >> 6;
+    const int nT = K / kTBlock;
+    const int G = nT >> gshift;
+    const int slots = NTP * 16 * M;                 // u32x4 per phase buffer
+    const int sums = (NTP * M + 3) & ~3;
+    u32x4* xslot0 = reinterpret_cast<u32x4*>(lds);
+    float* xsum0 = reinterpret_cast<float*>(xslot0 + 2 * static_cast<size_t>(slots));
+    float* csw = xsum0 + 2 * sums + wave * RT * 16 * G;                // [RT*16 rows][G]
+    uint8_t* zsw = reinterpret_cast<uint8_t*>(xsum0 + 2 * sums + W * RT * 16 * G) + wave * RT * 16 * G;
+    const int ntiles = (N + 15) / 16;
+    const int tile0 = min((static_cast<int>(blockIdx.x) * W + wave) * RT, ntiles - 1);
+    const int i = lane & 15, kb = lane >> 4;
+    const int64_t rbytes = K >> 1;
+
+    // weight rows of this lane: row 16 (tile0 + rt) + i
+    const u32x4* wrow[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+        wrow[rt] = reinterpret_cast<const u32x4*>(packed + static_cast<int64_t>(min(16 * (tile0 + rt) + i, N - 1)) * rbytes);
+    u32x4 w[D][RT];
+
+    // X staging (see gemm_int4_xres_kernel): piece p of row m within a phase
+    constexpr int kXB = (NTP * 16 * 64 + W * kWave - 1) / (W * kWave);  // pieces per thread, M <= 64
+    const int ppr = NTP * 16;
+    const int npieces = M * ppr;
+    const float inv_ppr = 1.0f / static_cast<float>(ppr);
+    auto load_x = [&](int phase, u32x4 (&dv)[kXB]) {
+#pragma unroll
+        for (int b = 0; b < kXB; ++b) {
+            const int idx = min(b * W * kWave + static_cast<int>(threadIdx.x), npieces - 1);
+            const int m = static_cast<int>((static_cast<float>(idx) + 0.5f) * inv_ppr);
+            const int p = idx - m * ppr;
+            dv[b] = *reinterpret_cast<const u32x4*>(X + static_cast<int64_t>(m) * K +
+                                                    8 * (static_cast<int64_t>(phase) * ppr + p));
+        }
+    };
+    auto write_x = [&](int buf, const u32x4 (&dv)[kXB]) {
+        u32x4* xs = xslot0 + buf * slots;
+        float* xm = xsum0 + buf * sums;
+        uint32_t sel_lo, sel_hi;
+        asm volatile("v_mov_b32 %0, 0x05040100" : "=v"(sel_lo));
+        asm volatile("v_mov_b32 %0, 0x07060302" : "=v"(sel_hi));
+        const uint32_t ones = 0x3F803F80u;
+#pragma unroll
+        for (int b = 0; b < kXB; ++b) {
+            const int idx0 = b * W * kWave + static_cast<int>(threadIdx.x);
+            const bool valid = idx0 < npieces;
+            const int idx = valid ? idx0 : 0;
+            const int m = static_cast<int>((static_cast<float>(idx) + 0.5f) * inv_ppr);
+            const int p = idx - m * ppr;
+            const u32x4 d = valid ? dv[b] : u32x4{0u, 0u, 0u, 0u};
+            u32x4 q;
+            q.x = __builtin_amdgcn_perm(d.z, d.x, sel_lo);
+            q.y = __builtin_amdgcn_perm(d.z, d.x, sel_hi);
+            q.z = __builtin_amdgcn_perm(d.w, d.y, sel_lo);
+            q.w = __builtin_amdgcn_perm(d.w, d.y, sel_hi);
+            float sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.x), as_bf16x2(ones), 0.0f, false);
+            sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.y), as_bf16x2(ones), sm, false);
+            sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.z), as_bf16x2(ones), sm, false);
+            sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.w), as_bf16x2(ones), sm, false);
+            sm = row16_sum(sm);
+            if (valid) {
+                const int T = p >> 4, w4 = p & 3, pkb = (p >> 2) & 3;
+                xs[((T * 4 + w4) * M + m) * 4 + pkb] = q;
+                if ((p & 15) == 0) xm[T * M + m] = sm;
+            }
+        }
+    };
+
+    // prologue: phase 0's X, this wave's coefficients, the weight ring
+    {
+        u32x4 dv[kXB];
+        load_x(0, dv);
+        const int cpasses = (G + kWave - 1) / kWave;
+        for (int j = 0; j < cpasses; ++j) {
+            const int g = min(lane + kWave * j, G - 1);
+#pragma unroll
+            for (int r = 0; r < 16 * RT; ++r) {
+                const int64_t row = min(16 * tile0 + r, N - 1);
+                const float sv = scales[row * G + g];
+                const uint32_t zb = zeros[row * (G >> 1) + (g >> 1)];
+                if (lane + kWave * j < G) {
+                    csw[r * G + g] = sv;
+                    zsw[r * G + g] = static_cast<uint8_t>((g & 1) ? (zb >> 4) : (zb & 0xFu));
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < D; ++u)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) w[u][rt] = wrow[rt][min(u, nT - 1) * 4 + kb];
+        write_x(0, dv);
+    }
+    __syncthreads();
+
+    const NibConsts nk = nib_consts();
+    f32x4 acc[RT][MT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[rt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    u32x4 nx[kXB];
+    for (int T0 = 0; T0 < nT; T0 += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            const int T = T0 + u;
+            if (T >= nT) continue;                    // uniform
+            const int ph = T / NTP, Tl = T - ph * NTP;
+            const int buf = ph & 1;
+            if (Tl == 0 && ph + 1 < nT / NTP) load_x(ph + 1, nx);   // next phase's X in flight
+            const u32x4* xs = xslot0 + buf * slots;
+            const float* xm = xsum0 + buf * sums;
+            const int g = T >> gshift;
+            bf16x8_t a[RT][4];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const u32x4 wv = w[u][rt];
+                a[rt][0] = a_operand(wv.x, nk);
+                a[rt][1] = a_operand(wv.y, nk);
+                a[rt][2] = a_operand(wv.z, nk);
+                a[rt][3] = a_operand(wv.w, nk);
+                w[u][rt] = wrow[rt][min(T + D, nT - 1) * 4 + kb];   // refill the ring slot
+            }
+            f32x4 s4[RT], z4[RT];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const float* cr = csw + (16 * rt + 4 * kb) * G + g;
+                const uint8_t* zr = zsw + (16 * rt + 4 * kb) * G + g;
+                s4[rt] = f32x4{cr[0], cr[G], cr[2 * G], cr[3 * G]};
+                z4[rt] = f32x4{-s4[rt].x * static_cast<float>(136u + zr[0]),
+                               -s4[rt].y * static_cast<float>(136u + zr[G]),
+                               -s4[rt].z * static_cast<float>(136u + zr[2 * G]),
+                               -s4[rt].w * static_cast<float>(136u + zr[3 * G])};
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int m = 16 * mt + i;
+                bf16x8_t b[4];
+                float xsv = 0.0f;
+#pragma unroll
+                for (int w4 = 0; w4 < 4; ++w4) b[w4] = bf16x8_t{};
+                if (m < M) {
+#pragma unroll
+                    for (int w4 = 0; w4 < 4; ++w4)
+                        b[w4] = __builtin_bit_cast(bf16x8_t, xs[((Tl * 4 + w4) * M + m) * 4 + kb]);
+                    xsv = xm[Tl * M + m];
+                }
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rt][0], b[0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rt][1], b[1], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rt][2], b[2], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rt][3], b[3], d, 0, 0, 0);
+                    f32x4 ac = acc[rt][mt];
+                    ac.x = fmaf(s4[rt].x, d.x, fmaf(z4[rt].x, xsv, ac.x));
+                    ac.y = fmaf(s4[rt].y, d.y, fmaf(z4[rt].y, xsv, ac.y));
+                    ac.z = fmaf(s4[rt].z, d.z, fmaf(z4[rt].z, xsv, ac.z));
+                    ac.w = fmaf(s4[rt].w, d.w, fmaf(z4[rt].w, xsv, ac.w));
+                    acc[rt][mt] = ac;
+                }
+            }
+            if (Tl == NTP - 1 && ph + 1 < nT / NTP) {  // uniform: publish the next phase
+                write_x(buf ^ 1, nx);
+                __syncthreads();
+            }
+        }
+    }
+
+    // lane (i, kb) holds Y[m = 16 mt + i][n = 16 (tile0 + rt) + 4 kb + v]
+    const int first = (static_cast<int>(blockIdx.x) * W + wave) * RT;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        if (first + rt >= ntiles) continue;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int m = 16 * mt + i;
+            if (m >= M) continue;
+            const float vals[4] = {acc[rt][mt].x, acc[rt][mt].y, acc[rt][mt].z, acc[rt][mt].w};
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int n = 16 * (first + rt) + 4 * kb + v;
+                if (n < N) Y[static_cast<int64_t>(m) * N + n] = kc::f32_to_bf16(vals[v]);
+            }
+        }
+    }
+}
+
+template <int W, int RT, int NTP, int D>
+int launch_xbig(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
+                const uint16_t* X, uint16_t* Y, int M, int N, int K, int gshift, hipStream_t stream) {
+    const int G = (K / kTBlock) >> gshift;
+    const size_t lds = xbig_lds_bytes(M, G, W, RT, NTP);
+    if (lds > 160 * 1024) return -1;
+    static bool attr_set = [] {
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_int4_xbig_kernel<W, RT, NTP, D>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+    }();
+    if (!attr_set) return kc::set_error(KC_ERR_HIP, "%s: cannot raise the LDS limit", fn);
+    const int ntiles = (N + 15) / 16;
+    const int per_wg = W * RT;
+    const unsigned grid = static_cast<unsigned>((ntiles + per_wg - 1) / per_wg);
+    gemm_int4_xbig_kernel<W, RT, NTP, D><<<grid, W * kWave, lds, stream>>>(packed, scales, zeros, X, Y, M, N, K, gshift);
+    return kc::check_launch(fn);
+}
+
 }  // namespace
 
 extern "C" int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
@@ -713,6 +949,14 @@ extern "C" int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
         if (P > 0)
             return launch_xres<kXresW, kXresD>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols,
                                                gshift, P, stream);
+    }
+    // M 33..64: the four-tile X-resident kernel when its LDS fits (K 8192,
+    // N 28672: M 33 / 48 / 64 in 86 / 90 / 94 us against 105 / 119 / 125 us
+    // below; at M 17..32 the kernel below is faster, 65-77 us against 80-85)
+    if (m > 32 && (cols / kTBlock) % 8 == 0) {
+        const int st = launch_xbig<7, 1, 2, 8>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols,
+                                               gshift, stream);
+        if (st >= 0) return st;
     }
     // m-tiles of 16 activation rows; with more of them each B operand read
     // from LDS is reused across two weight row tiles.

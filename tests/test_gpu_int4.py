@@ -277,7 +277,11 @@ def test_gemm_cfg3(gpu, oracle, m):
                                             # phases of K
                                             (16, 48, 1024, 128), (8, 300, 4096, 128),
                                             (12, 257, 2048, 256), (16, 100, 8192, 128),
-                                            (6, 7 * 16 + 1, 8192, 512)])
+                                            (6, 7 * 16 + 1, 8192, 512),
+                                            # M 33..64: four activation tiles, X in
+                                            # double-buffered phases
+                                            (33, 70, 1024, 128), (64, 7 * 16 * 2 + 9, 2048, 256),
+                                            (48, 200, 8192, 128)])
 def test_gemm_shapes(gpu, oracle, m, rows, cols, gs):
     packed, scales, zeros = make_int4(rows, cols, gs, seed=m * 1000 + rows)
     xb = normal_bf16((m, cols), seed=m + rows)
