@@ -123,6 +123,68 @@ def hbm(nbytes: int, us: float) -> dict:
             "frac": round(gbs / PEAK_HBM_GBS, 4)}
 
 
+def counter_probe(args, torch, lib, dev) -> int:
+    """Launch sequences for the rocprofv3 --pmc passes in profiles/ (one kind
+    of kernel at a time, so that per-dispatch counters are easy to read)."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(77)
+    stream = torch.cuda.current_stream().cuda_stream
+    if args.quant_probe:
+        n = 4096
+        xs = [torch.randn(n, n, device=dev, generator=gen) for _ in range(18)]   # 1.2 GB
+        q = torch.empty(n, n, dtype=torch.int8, device=dev)
+        s = torch.empty(n, device=dev)
+        for j in range(20):
+            st = lib.kc_quantize_fp8_per_token_f32(xs[j % len(xs)].data_ptr(), q.data_ptr(),
+                                                   s.data_ptr(), n, n, stream)
+            if st:
+                raise RuntimeError(lib.kc_last_error_string().decode())
+        torch.cuda.synchronize()
+        src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print("quant probe done: 20 x cfg1 per-token quantizer, 20 x copy of 67108864 B", flush=True)
+        return 0
+    # cfg3 GEMMs
+    n, k = 28672, 8192
+    g = k // GS
+    w = [(torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=dev, generator=gen),
+          torch.empty(n, g, device=dev).uniform_(0.005, 0.02, generator=gen),
+          torch.randint(0, 256, (n, g // 2), dtype=torch.uint8, device=dev, generator=gen))
+         for _ in range(8)]                                                      # 1 GB
+    for m in (4, 16, 64):
+        x = torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16)
+        y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        for j in range(10):
+            p, sc, z = w[j % len(w)]
+            st = lib.kc_gemm_int4_bf16(p.data_ptr(), sc.data_ptr(), z.data_ptr(), x.data_ptr(),
+                                       y.data_ptr(), m, n, k, GS, stream)
+            if st:
+                raise RuntimeError(lib.kc_last_error_string().decode())
+        torch.cuda.synchronize()
+    del w
+    # the FP8 W8A8 GEMM at the cfg4 consumer shape
+    t4, d4, n4 = 16384, 8192, 28672
+    qx = torch.randint(-128, 128, (t4, d4), dtype=torch.int8, device=dev, generator=gen)
+    qw = torch.randint(-128, 128, (n4, d4), dtype=torch.int8, device=dev, generator=gen)
+    qx[(qx & 0x7F) == 0x7F] = 0                    # no NaN codes
+    qw[(qw & 0x7F) == 0x7F] = 0
+    sx = torch.rand(t4, device=dev, generator=gen)
+    sw = torch.rand(n4, device=dev, generator=gen)
+    y4 = torch.empty(t4, n4, dtype=torch.bfloat16, device=dev)
+    for _ in range(3):
+        st = lib.kc_gemm_fp8_w8a8_bf16(qx.data_ptr(), sx.data_ptr(), qw.data_ptr(), sw.data_ptr(),
+                                       y4.data_ptr(), t4, n4, d4, stream)
+        if st:
+            raise RuntimeError(lib.kc_last_error_string().decode())
+    torch.cuda.synchronize()
+    print("mfma probe done: 10 x cfg3 GEMM at M 4, 16, 64; 3 x FP8 GEMM 16384 x 28672 x 8192",
+          flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -134,6 +196,12 @@ def main() -> int:
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc: launch the gate/up GEMV and a plain 64 MiB "
                          "device copy (the counter calibration) 20 times each, then exit")
+    ap.add_argument("--quant-probe", action="store_true",
+                    help="for rocprofv3 --pmc: launch the cfg1 FP8 per-token quantizer 20 "
+                         "times over rotating inputs and the 64 MiB copy 20 times, then exit")
+    ap.add_argument("--mfma-probe", action="store_true",
+                    help="for rocprofv3 --pmc: launch the cfg3 GEMMs (M 4, 16, 64) 10 times "
+                         "each and the FP8 W8A8 GEMM (cfg4 shape) 3 times, then exit")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -152,6 +220,9 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     log(f"# {lib.kc_version().decode()} on {torch.cuda.get_device_name(dev)}")
+
+    if args.quant_probe or args.mfma_probe:
+        return counter_probe(args, torch, lib, dev)
 
     # ---- inputs (BASELINE cfg2 distributions), rotated over > 1 GiB --------
     layer_bytes = sum(gemv_bytes(n, k) for _, n, k in LLAMA)
