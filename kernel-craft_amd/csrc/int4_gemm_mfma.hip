@@ -910,6 +910,272 @@ int launch_xbig(const char* fn, const uint8_t* packed, const float* scales, cons
     return kc::check_launch(fn);
 }
 
+
+// ---------------------------------------------------------------------------
+// M 17..64: K split across the waves of a workgroup, X straight from the
+// cache into registers.
+//
+// A workgroup of four waves (one per SIMD) owns RT = 7 consecutive 16-row
+// weight tiles (112 rows: N = 28672 gives 256 workgroups, one per CU); wave
+// w owns the T-blocks [w nT / 4, (w + 1) nT / 4) of K for all seven tiles
+// and all MT activation tiles.  Per T-block a wave loads the MT B operands
+// of its K range from X (every wave reads a different quarter of X, so no
+// activation byte passes through LDS or is read twice by a CU), decodes each
+// weight tile's A operands once and runs them against the MT activation
+// tiles, and folds the T-block into its accumulators with the coefficients
+// (s, c2) staged in LDS at the start.  The weights stream through a D-deep
+// ring of T-blocks in registers, X one T-block ahead.  At the end the four
+// K parts of each output tile are summed through LDS in a fixed order.
+//
+// Against the X-resident kernels, where every wave runs over all of K and
+// all waves of a CU share X through LDS, the B-operand LDS traffic (each
+// wave re-reading all of X) and the restaging of X by phases are gone; the
+// cost is 4 x RT x MT accumulators per wave and a final cross-wave sum.
+// ---------------------------------------------------------------------------
+constexpr int kKsWaves = 4;
+constexpr int kKsRT = 7, kKsD = 2;
+
+__device__ __forceinline__ float swap32_sum(float a) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, a),
+                                                    __builtin_bit_cast(unsigned, a), false, false);
+    const unsigned r0 = r[0], r1 = r[1];
+    return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+}
+
+__device__ __forceinline__ float swap16_sum(float a) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, a),
+                                                    __builtin_bit_cast(unsigned, a), false, false);
+    const unsigned r0 = r[0], r1 = r[1];
+    return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+}
+
+// LDS: the coefficients cs[t][row], cz[t][row] of every wave's K range, later
+// reused for the cross-wave sum (one f32x4 per lane, tile and wave).
+__host__ __device__ constexpr size_t kslice_lds_bytes(int MT, int RT, int nT) {
+    const size_t coef = static_cast<size_t>(kKsWaves) * ((nT + kKsWaves - 1) / kKsWaves) * 16 * RT * 8;
+    const size_t red = static_cast<size_t>(kKsWaves) * RT * MT * kWave * 16;
+    return coef > red ? coef : red;
+}
+
+template <int MT, int RT, int D>
+__global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslice_kernel(
+    const uint8_t* __restrict__ packed, const float* __restrict__ scales,
+    const uint8_t* __restrict__ zeros, const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
+    int M, int N, int K, int gshift) {
+    extern __shared__ __align__(16) char lds[];
+    constexpr int kRows = 16 * RT;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x >> 6;
+    const int i = lane & 15, kb = lane >> 4;
+    const int nT = K / kTBlock;
+    const int G = nT >> gshift;
+    const int ntmax = (nT + kKsWaves - 1) / kKsWaves;
+    const int t0 = (wave * nT) / kKsWaves, t1 = ((wave + 1) * nT) / kKsWaves;
+    const int nt = t1 - t0;  // 0 for some waves when nT < 4
+    const int tl = max(t1 - 1, 0);
+    const int row_base = blockIdx.x * kRows;
+    float* cs = reinterpret_cast<float*>(lds) + static_cast<size_t>(wave) * ntmax * kRows * 2;
+    float* cz = cs + ntmax * kRows;
+
+    // Byte offsets of this lane's weight rows (row_base + 16 rt + i, bytes
+    // 16 kb .. 16 kb + 15 of each T-block) and X rows (16 c + i, bytes
+    // 64 kb .. 64 kb + 63 of each T-block): 32 bits, the launcher checks that
+    // both operands are smaller than 4 GiB.  Rows past the end are clamped.
+    uint32_t woff[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+        woff[rt] = static_cast<uint32_t>(min(row_base + 16 * rt + i, N - 1)) * static_cast<uint32_t>(K >> 1) + 16u * kb;
+    uint32_t xoff[MT];
+#pragma unroll
+    for (int c = 0; c < MT; ++c)
+        xoff[c] = static_cast<uint32_t>(min(16 * c + i, M - 1)) * static_cast<uint32_t>(2 * K) + 64u * kb;
+    const uint8_t* xbytes = reinterpret_cast<const uint8_t*>(X);
+    auto wload = [&](int rt, int T) {
+        return *reinterpret_cast<const u32x4*>(packed + (static_cast<uint32_t>(64 * min(T, tl)) + woff[rt]));
+    };
+    auto xload = [&](int c, int T, int s) {
+        return *reinterpret_cast<const u32x4*>(xbytes + (static_cast<uint32_t>(256 * min(T, tl) + 16 * s) + xoff[c]));
+    };
+
+    u32x4 wr[D][RT];  // weight ring: T-blocks T .. T + D - 1
+    u32x4 xb[MT][4];  // X of the next T-block
+#pragma unroll
+    for (int u = 0; u < D; ++u)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) wr[u][rt] = wload(rt, t0 + u);
+#pragma unroll
+    for (int c = 0; c < MT; ++c)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) xb[c][s] = xload(c, t0, s);
+
+    // Fold coefficients of this wave's K range, cs[t][row] = s and
+    // cz[t][row] = -s (136 + z): every load of a pass is issued before the
+    // first is used (one memory round trip per pass); item idx = (row, t)
+    // with t fastest, row = (idx + 0.5) / nt in fp32 (exact: idx < 2^24 and
+    // the quotient is never within 0.5 / nt of an integer).
+    {
+        constexpr int kBatch = 28;  // 16 T-blocks x 112 rows in one pass
+        const int items = nt * kRows;
+        const float inv_nt = 1.0f / static_cast<float>(max(nt, 1));
+        for (int base = 0; base < items; base += kBatch * kWave) {
+            float sv[kBatch];
+            uint32_t zb[kBatch];
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {
+                const int idx = min(base + b * kWave + lane, items - 1);
+                const int r = static_cast<int>((static_cast<float>(idx) + 0.5f) * inv_nt);
+                const int g = (t0 + idx - r * nt) >> gshift;
+                const int64_t row = min(row_base + r, N - 1);
+                sv[b] = scales[row * G + g];
+                zb[b] = zeros[row * (G >> 1) + (g >> 1)];
+            }
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {
+                const int idx = base + b * kWave + lane;
+                if (idx < items) {
+                    const int r = static_cast<int>((static_cast<float>(idx) + 0.5f) * inv_nt);
+                    const int t = idx - r * nt;
+                    const int g = (t0 + t) >> gshift;
+                    const uint32_t z = (g & 1) ? (zb[b] >> 4) : (zb[b] & 0xFu);
+                    cs[t * kRows + r] = sv[b];
+                    cz[t * kRows + r] = -sv[b] * static_cast<float>(136u + z);
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    const NibConsts nk = nib_consts();
+    uint32_t sel_lo, sel_hi;  // v_perm_b32 selectors, in VGPRs
+    asm volatile("v_mov_b32 %0, 0x05040100" : "=v"(sel_lo));
+    asm volatile("v_mov_b32 %0, 0x07060302" : "=v"(sel_hi));
+    const uint32_t ones = 0x3F803F80u;
+    f32x4 acc[RT][MT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int c = 0; c < MT; ++c) acc[rt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // A whole number of ring turns, so the body has no branch (a guarded
+    // iteration would make the compiler's load-count waits conservative):
+    // padding T-blocks past the range reload the last one and fold with 0.
+    const int tend = t0 + ((nt + D - 1) / D) * D;
+    for (int T0 = t0; T0 < tend; T0 += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            const int T = T0 + u;
+            const bool live = T < t1;
+            // B operands in pair order, and the T-block sums of X: lane
+            // (i, kb) sums its 32 values, the four kb lanes are added with
+            // permlane swaps.
+            bf16x8_t b[MT][4];
+            float xs[MT];
+#pragma unroll
+            for (int c = 0; c < MT; ++c) {
+                float sm = 0.0f;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const u32x4 d = xb[c][s];
+                    u32x4 q;
+                    q.x = __builtin_amdgcn_perm(d.z, d.x, sel_lo);  // (x0, x4)
+                    q.y = __builtin_amdgcn_perm(d.z, d.x, sel_hi);  // (x1, x5)
+                    q.z = __builtin_amdgcn_perm(d.w, d.y, sel_lo);  // (x2, x6)
+                    q.w = __builtin_amdgcn_perm(d.w, d.y, sel_hi);  // (x3, x7)
+                    b[c][s] = __builtin_bit_cast(bf16x8_t, q);
+                    sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.x), as_bf16x2(ones), sm, false);
+                    sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.y), as_bf16x2(ones), sm, false);
+                    sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.z), as_bf16x2(ones), sm, false);
+                    sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.w), as_bf16x2(ones), sm, false);
+                }
+                xs[c] = swap16_sum(swap32_sum(sm));
+            }
+#pragma unroll
+            for (int c = 0; c < MT; ++c)
+#pragma unroll
+                for (int s = 0; s < 4; ++s) xb[c][s] = xload(c, T + 1, s);
+            const int tt = min(T, tl) - t0;
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const u32x4 wv = wr[u][rt];
+                const bf16x8_t a0 = a_operand(wv.x, nk), a1 = a_operand(wv.y, nk);
+                const bf16x8_t a2 = a_operand(wv.z, nk), a3 = a_operand(wv.w, nk);
+                wr[u][rt] = wload(rt, T + D);
+                f32x4 s4 = *reinterpret_cast<const f32x4*>(cs + tt * kRows + 16 * rt + 4 * kb);
+                f32x4 z4 = *reinterpret_cast<const f32x4*>(cz + tt * kRows + 16 * rt + 4 * kb);
+                if (!live) {
+                    s4 = f32x4{0.f, 0.f, 0.f, 0.f};
+                    z4 = s4;
+                }
+#pragma unroll
+                for (int c = 0; c < MT; ++c) {
+                    f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[c][0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[c][1], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[c][2], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b[c][3], d, 0, 0, 0);
+                    f32x4& a = acc[rt][c];
+                    a.x = fmaf(s4.x, d.x, fmaf(z4.x, xs[c], a.x));
+                    a.y = fmaf(s4.y, d.y, fmaf(z4.y, xs[c], a.y));
+                    a.z = fmaf(s4.z, d.z, fmaf(z4.z, xs[c], a.z));
+                    a.w = fmaf(s4.w, d.w, fmaf(z4.w, xs[c], a.w));
+                }
+                // one weight tile at a time: without this fence the scheduler
+                // interleaves the tiles and the register demand spills
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+
+    // Sum the four K parts of every output tile through LDS (waves in a
+    // fixed order), wave w finishing tiles w, w + 4, ...; lane (i, kb) of
+    // tile (rt, c) holds Y[m = 16 c + i][n = row_base + 16 rt + 4 kb + v].
+    __syncthreads();  // every wave is done with the coefficients
+    f32x4* red = reinterpret_cast<f32x4*>(lds);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int c = 0; c < MT; ++c) red[((wave * RT + rt) * MT + c) * kWave + lane] = acc[rt][c];
+    __syncthreads();
+    for (int tile = wave; tile < RT * MT; tile += kKsWaves) {
+        const int rt = tile / MT, c = tile - rt * MT;
+        f32x4 v = red[(rt * MT + c) * kWave + lane];
+#pragma unroll
+        for (int w = 1; w < kKsWaves; ++w) {
+            const f32x4 o = red[((w * RT + rt) * MT + c) * kWave + lane];
+            v.x += o.x;
+            v.y += o.y;
+            v.z += o.z;
+            v.w += o.w;
+        }
+        const int m = 16 * c + i;
+        const int n0 = row_base + 16 * rt + 4 * kb;
+        if (m < M) {
+            const float vals[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (n0 + e < N) Y[static_cast<int64_t>(m) * N + n0 + e] = kc::f32_to_bf16(vals[e]);
+        }
+    }
+}
+
+// Returns -1 when the kernel does not apply (LDS or 32-bit offsets).
+template <int MT>
+int launch_kslice(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
+                  const uint16_t* X, uint16_t* Y, int M, int N, int K, int gshift, hipStream_t stream) {
+    const size_t lds = kslice_lds_bytes(MT, kKsRT, K / kTBlock);
+    if (lds > 160 * 1024 || static_cast<uint64_t>(N) * (K / 2) >= (uint64_t{1} << 32) ||
+        static_cast<uint64_t>(M) * K * 2 >= (uint64_t{1} << 32))
+        return -1;
+    static bool attr_set = [] {
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_int4_kslice_kernel<MT, kKsRT, kKsD>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+    }();
+    if (!attr_set) return kc::set_error(KC_ERR_HIP, "%s: cannot raise the LDS limit", fn);
+    const unsigned grid = static_cast<unsigned>((N + 16 * kKsRT - 1) / (16 * kKsRT));
+    gemm_int4_kslice_kernel<MT, kKsRT, kKsD><<<grid, kKsWaves * kWave, lds, stream>>>(
+        packed, scales, zeros, X, Y, M, N, K, gshift);
+    return kc::check_launch(fn);
+}
+
 }  // namespace
 
 extern "C" int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
@@ -949,6 +1215,19 @@ extern "C" int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
         if (P > 0)
             return launch_xres<kXresW, kXresD>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols,
                                                gshift, P, stream);
+    }
+    // M 17..64: the K-split kernel (K 8192, N 28672, MI355X: M 32 / 48 / 64
+    // in 47 / 57 / 68 us, against 77 / 95 / 101 us for the kernels below,
+    // which remain for shapes it does not take: K above about 20000, where
+    // its coefficient stage does not fit in LDS, or operands of 4 GiB).
+    if (m > kXresMaxM) {
+        int st = -1;
+        switch ((m + 15) / 16) {
+            case 2: st = launch_kslice<2>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+            case 3: st = launch_kslice<3>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+            default: st = launch_kslice<4>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+        }
+        if (st >= 0) return st;
     }
     // M 33..64: the four-tile X-resident kernel when its LDS fits (K 8192,
     // N 28672: M 33 / 48 / 64 in 86 / 90 / 94 us against 105 / 119 / 125 us

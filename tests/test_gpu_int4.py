@@ -240,7 +240,7 @@ def _gemm(torch, packed, scales, zeros, xb, m, rows, cols, gs):
     return bf16_bits_to_f32(_host_bf16_bits(dy)).reshape(m, rows), (dp, ds, dz, dx)
 
 
-@pytest.mark.parametrize("m", [4, 16, 64])
+@pytest.mark.parametrize("m", [4, 16, 32, 64])
 def test_gemm_cfg3(gpu, oracle, m):
     """M in {4, 16, 64}, K = 8192, N = 28672, gs 128.  Sampled rows against the
     fp64 oracle (reference GEMV per activation row); every row against an fp32
@@ -278,10 +278,18 @@ def test_gemm_cfg3(gpu, oracle, m):
                                             (16, 48, 1024, 128), (8, 300, 4096, 128),
                                             (12, 257, 2048, 256), (16, 100, 8192, 128),
                                             (6, 7 * 16 + 1, 8192, 512),
-                                            # M 33..64: four activation tiles, X in
-                                            # double-buffered phases
+                                            # M 17..64, K split over four waves:
+                                            # ragged rows and activation tiles,
+                                            # waves with no T-block (K < 512),
+                                            # ranges of unequal length
                                             (33, 70, 1024, 128), (64, 7 * 16 * 2 + 9, 2048, 256),
-                                            (48, 200, 8192, 128)])
+                                            (48, 200, 8192, 128), (20, 224, 4096, 128),
+                                            (32, 1000, 4096, 128), (40, 113, 16384, 128),
+                                            (17, 7, 256, 256), (63, 1, 512, 128),
+                                            (26, 130, 1152, 128),
+                                            # M 33..64 whose coefficients do not fit
+                                            # in LDS: the X-resident fallback
+                                            (64, 50, 24576, 128)])
 def test_gemm_shapes(gpu, oracle, m, rows, cols, gs):
     packed, scales, zeros = make_int4(rows, cols, gs, seed=m * 1000 + rows)
     xb = normal_bf16((m, cols), seed=m + rows)
