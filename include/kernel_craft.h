@@ -75,6 +75,12 @@ void launch_smoothquant_scale(const float* d_input,
                               const float* d_smooth_scales, float* d_output,
                               int rows, int cols, kc_stream_t stream);
 
+/* y[r,i] = (g[i] * x[r,i]) / sqrt(sum_j x[r,j]^2 / D + eps), fp32 [rows, D].
+ * Replaces rmsnorm.cu:83-88; like that launcher (and unlike the others
+ * here) it does not synchronize its stream. */
+void launch_rmsnorm(const float* d_x, const float* d_g, float* d_y, int rows,
+                    int D, float eps, kc_stream_t stream);
+
 /* ======================================================================
  * Part 2 -- error channel (no reference counterpart: the reference's
  * launchers report nothing, quant_int4.cu:205,233, fp8_quant.cu:225)
@@ -129,6 +135,25 @@ typedef struct kc_gemv_op {
     int rows, cols, group_size, reserved;
 } kc_gemv_op;
 int kc_gemv_int4_bf16_chain(const kc_gemv_op* ops, int n_ops, kc_stream_t stream);
+
+/* RMSNorm with bf16 input, weight and output (fp32 arithmetic, output
+ * rounded to nearest even): the bf16 counterpart of launch_rmsnorm,
+ * rmsnorm.cu:40-70.  x, y [rows, D]; g [D]. */
+int kc_rmsnorm_bf16(const uint16_t* d_x, const uint16_t* d_g, uint16_t* d_y,
+                    int rows, int D, float eps, kc_stream_t stream);
+
+/* The RMSNorm in front of a decoder GEMV, fused into it (no counterpart in
+ * the reference, where rmsnorm.cu:83-88 and quant_int4.cu:221-234 are two
+ * launches with the normalized vector in memory between them):
+ *   y = W x,  x[k] = bf16((gamma[k] * h[k]) / sqrt(sum h^2 / cols + eps))
+ * h, gamma [cols] bf16; y [rows] bf16; W as in kc_gemv_int4_bf16.  x is
+ * what kc_rmsnorm_bf16 would write, to within the order of the fp32 sum of
+ * squares. */
+int kc_rmsnorm_gemv_int4_bf16(const uint16_t* d_h, const uint16_t* d_gamma,
+                              float eps, const uint8_t* d_packed,
+                              const float* d_scales, const uint8_t* d_zeros,
+                              uint16_t* d_y, int rows, int cols,
+                              int group_size, kc_stream_t stream);
 
 /* GPTQ / AWQ INT4 checkpoints to the layout above (no counterpart in the
  * reference, which only describes its format as GPTQ/AWQ-style,
@@ -250,7 +275,7 @@ void launch_col_parallel_linear(const float* d_x, const float* d_W, float* d_y,
 void launch_row_parallel_linear(const float* d_x_rank, const float* d_W,
                                 float* d_out, int M, int N, int K_rank,
                                 kc_stream_t stream);
-/* selective_scan.cu:104-109, depthwise_conv1d.cu:84-87, rmsnorm.cu:83-85 */
+/* selective_scan.cu:104-109, depthwise_conv1d.cu:84-87 */
 void launch_selective_scan(const float* d_u, const float* d_A_log,
                            const float* d_B, const float* d_C,
                            const float* d_delta, float* d_y, int B_, int L,
@@ -258,8 +283,6 @@ void launch_selective_scan(const float* d_u, const float* d_A_log,
 void launch_depthwise_conv1d(const float* d_x, const float* d_w,
                              const float* d_bias, float* d_y, int B_, int D,
                              int L, int d_conv, kc_stream_t stream);
-void launch_rmsnorm(const float* d_x, const float* d_g, float* d_y, int rows,
-                    int D, float eps, kc_stream_t stream);
 /* tensor_parallel_nccl.cu:171-198 (the reference's own no-NCCL stubs) */
 void nccl_comm_init_all(void** comms, int num_comms, const int* devs);
 void nccl_comm_destroy(void* comm);

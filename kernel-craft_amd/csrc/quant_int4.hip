@@ -56,23 +56,45 @@ __device__ __forceinline__ void store_y(void* y, int64_t n, float v) {
     else static_cast<float*>(y)[n] = v;
 }
 
+// 1 / sqrt(sum h^2 / K + eps) of a bf16 vector, summed by one wave (the
+// RMSNorm in front of a fused GEMV; the arithmetic of rmsnorm.hip).
+__device__ __forceinline__ float rms_inverse(const uint16_t* h, int64_t K, float eps, int lane) {
+    float ss = 0.0f;
+    for (int64_t k = lane; k < K; k += kWave) {
+        const float v = kc::bf16_to_f32(h[k]);
+        ss = fmaf(v, v, ss);
+    }
+    ss = kc::wave_sum(ss);
+    return 1.0f / sqrtf(ss / static_cast<float>(K) + eps);
+}
+
 // ---------------------------------------------------------------------------
 // Generic GEMV: any even K and any group size dividing K.  One wave per row,
 // lanes stride over bytes with the reference's own index arithmetic
 // (quant_int4.cu:143-164), dequantizing each weight to fp32 as the reference
 // does before the FMA.
 // ---------------------------------------------------------------------------
-template <bool XBF16, bool YBF16>
+template <bool XBF16, bool YBF16, bool NORM>
 __global__ __launch_bounds__(kThreads) void gemv_int4_generic_kernel(
     const uint8_t* __restrict__ packed, const float* __restrict__ scales,
     const uint8_t* __restrict__ zeros, const void* __restrict__ x, void* __restrict__ y,
-    int64_t rows, int64_t cols, int64_t gs) {
+    int64_t rows, int64_t cols, int64_t gs, const uint16_t* __restrict__ gamma, float eps) {
+    static_assert(!NORM || XBF16, "the fused RMSNorm takes bf16 x");
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t row = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
     if (row >= rows) return;
     const int64_t nbytes = cols >> 1;
     const int64_t G = cols / gs;
     const uint8_t* prow = packed + row * nbytes;
+    float rms_inv = 1.0f;
+    if constexpr (NORM) rms_inv = rms_inverse(static_cast<const uint16_t*>(x), cols, eps, lane);
+    // x[k] as the GEMV sees it: bf16((gamma[k] * h[k]) * rms_inv) when fused
+    auto xin = [&](int64_t k) {
+        if constexpr (NORM)
+            return kc::bf16_to_f32(kc::f32_to_bf16((kc::bf16_to_f32(gamma[k]) * load_x<true>(x, k)) * rms_inv));
+        else
+            return load_x<XBF16>(x, k);
+    };
     float acc = 0.0f;
     for (int64_t b = lane; b < nbytes; b += kWave) {
         const int64_t c0 = 2 * b;
@@ -82,8 +104,8 @@ __global__ __launch_bounds__(kThreads) void gemv_int4_generic_kernel(
             static_cast<float>(sext4(p) - zero_nibble(zeros, row, G, g0)) * scales[row * G + g0];
         const float w1 =
             static_cast<float>(sext4(p >> 4) - zero_nibble(zeros, row, G, g1)) * scales[row * G + g1];
-        acc = fmaf(w0, load_x<XBF16>(x, c0), acc);
-        acc = fmaf(w1, load_x<XBF16>(x, c0 + 1), acc);
+        acc = fmaf(w0, xin(c0), acc);
+        acc = fmaf(w1, xin(c0 + 1), acc);
     }
     acc = kc::wave_sum(acc);
     if (lane == 0) store_y<YBF16>(y, row, acc);
@@ -114,11 +136,12 @@ __global__ __launch_bounds__(kThreads) void gemv_int4_generic_kernel(
 // The fold of one chunk's dot product into the row sum:
 //     acc += c1 * dot + c2 * sum(x),   c1 = s,  c2 = -s * (off + z)
 // off = 136 for the bf16 encoding 128 + (q ^ 8), 8 for fp32.
-template <int R, int CPL, int SLOT, int WPB, bool XBF16, bool YBF16>
+template <int R, int CPL, int SLOT, int WPB, bool XBF16, bool YBF16, bool NORM>
 __global__ __launch_bounds__(WPB * kWave) void gemv_int4_fast_kernel(
     const uint8_t* __restrict__ packed, const float* __restrict__ scales,
     const uint8_t* __restrict__ zeros, const void* __restrict__ x, void* __restrict__ y,
-    int rows, int cols, int gshift) {
+    int rows, int cols, int gshift, const uint16_t* __restrict__ gamma, float eps) {
+    static_assert(!NORM || XBF16, "the fused RMSNorm takes bf16 x");
     using SM = SlotMap<SLOT>;
     constexpr int kSlots = R * CPL;
     constexpr int kRegs = (kSlots + SM::kPerReg - 1) / SM::kPerReg;
@@ -140,11 +163,18 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_int4_fast_kernel(
 
     // 1a. x, raw
     u32x4 xr[kQPT];
+    u32x4 gr[NORM ? kQPT : 1];
     {
         const u32x4* src = static_cast<const u32x4*>(x);
 #pragma unroll
         for (int u = 0; u < kQPT; ++u)
             xr[u] = src[min(static_cast<int>(threadIdx.x) + u * kThreadsWG, nquads - 1)];
+        if constexpr (NORM) {
+            const u32x4* gsrc = reinterpret_cast<const u32x4*>(gamma);
+#pragma unroll
+            for (int u = 0; u < kQPT; ++u)
+                gr[u] = gsrc[min(static_cast<int>(threadIdx.x) + u * kThreadsWG, nquads - 1)];
+        }
     }
     // 1b. scale and zero byte of every item this lane holds
     float s_it[kRegs];
@@ -174,6 +204,46 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_int4_fast_kernel(
     // keep every load above this point: the compiler otherwise sinks weight
     // loads towards their uses, leaving one row in flight at a time
     __builtin_amdgcn_sched_barrier(0);
+
+    // 1d. fused RMSNorm: sum of squares of h over the workgroup (each quad
+    // once; the clamped duplicates past the end are skipped), partial sums
+    // of the waves added in a fixed order, then x = bf16((gamma h) rms_inv)
+    if constexpr (NORM) {
+        float* part = xsum + cpr;  // WPB partial sums after the chunk sums
+        float ss = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kQPT; ++u) {
+            if (static_cast<int>(threadIdx.x) + u * kThreadsWG < nquads) {
+                const uint32_t w4[4] = {xr[u].x, xr[u].y, xr[u].z, xr[u].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float lo = __uint_as_float(w4[j] << 16), hi = __uint_as_float(w4[j] & 0xFFFF0000u);
+                    ss = fmaf(lo, lo, ss);
+                    ss = fmaf(hi, hi, ss);
+                }
+            }
+        }
+        ss = kc::wave_sum(ss);
+        if (lane == 0) part[wave] = ss;
+        __syncthreads();
+        float tot = part[0];
+#pragma unroll
+        for (int w = 1; w < WPB; ++w) tot += part[w];
+        const float rms_inv = 1.0f / sqrtf(tot / static_cast<float>(cols) + eps);
+#pragma unroll
+        for (int u = 0; u < kQPT; ++u) {
+            const uint32_t w4[4] = {xr[u].x, xr[u].y, xr[u].z, xr[u].w};
+            const uint32_t g4[4] = {gr[u].x, gr[u].y, gr[u].z, gr[u].w};
+            uint32_t o4[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float lo = (__uint_as_float(g4[j] << 16) * __uint_as_float(w4[j] << 16)) * rms_inv;
+                const float hi = (__uint_as_float(g4[j] & 0xFFFF0000u) * __uint_as_float(w4[j] & 0xFFFF0000u)) * rms_inv;
+                o4[j] = static_cast<uint32_t>(kc::f32_to_bf16(lo)) | (static_cast<uint32_t>(kc::f32_to_bf16(hi)) << 16);
+            }
+            xr[u] = u32x4{o4[0], o4[1], o4[2], o4[3]};
+        }
+    }
 
     // 2. stage x in LDS
     {
@@ -351,50 +421,65 @@ int device_max_lds() {
     return v;
 }
 
-template <int R, int CPL, int SLOT, int WPB, bool XB, bool YB>
-void launch_fast(const uint8_t* packed, const float* scales, const uint8_t* zeros, const void* x,
-                 void* y, int rows, int cols, int gshift, size_t lds, hipStream_t stream) {
+// Launch arguments shared by every GEMV variant; gamma and eps are used by
+// the fused RMSNorm only.
+struct GemvArgs {
+    const uint8_t* packed;
+    const float* scales;
+    const uint8_t* zeros;
+    const void* x;
+    void* y;
+    const uint16_t* gamma;
+    float eps;
+};
+
+template <int R, int CPL, int SLOT, int WPB, bool XB, bool YB, bool NORM>
+void launch_fast(const GemvArgs& a, int rows, int cols, int gshift, size_t lds, hipStream_t stream) {
     const int wave_blocks = (rows + R - 1) / R;
     const unsigned grid = static_cast<unsigned>((wave_blocks + WPB - 1) / WPB);
-    gemv_int4_fast_kernel<R, CPL, SLOT, WPB, XB, YB><<<grid, WPB * kWave, lds, stream>>>(
-        packed, scales, zeros, x, y, rows, cols, gshift);
+    gemv_int4_fast_kernel<R, CPL, SLOT, WPB, XB, YB, NORM><<<grid, WPB * kWave, lds, stream>>>(
+        a.packed, a.scales, a.zeros, a.x, a.y, rows, cols, gshift, a.gamma, a.eps);
 }
 
 // Rows per wave and waves per workgroup: 2 rows and 4 waves up to K = 16384
 // (at most 8 weight chunks per row and lane); 1 row and 8 waves beyond.
-template <int CPL, bool XB, bool YB>
-void launch_fast_cpl(int slot, const uint8_t* packed, const float* scales, const uint8_t* zeros,
-                     const void* x, void* y, int rows, int cols, int gshift, size_t lds,
+template <int CPL, bool XB, bool YB, bool NORM>
+void launch_fast_cpl(int slot, const GemvArgs& a, int rows, int cols, int gshift, size_t lds,
                      hipStream_t stream) {
     constexpr int R = CPL <= 8 ? 2 : 1;
     constexpr int WPB = CPL <= 8 ? 4 : 8;
     if (slot == 16)
-        launch_fast<R, CPL, 16, WPB, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, lds, stream);
+        launch_fast<R, CPL, 16, WPB, XB, YB, NORM>(a, rows, cols, gshift, lds, stream);
     else
-        launch_fast<R, CPL, 64, WPB, XB, YB>(packed, scales, zeros, x, y, rows, cols, gshift, lds, stream);
+        launch_fast<R, CPL, 64, WPB, XB, YB, NORM>(a, rows, cols, gshift, lds, stream);
 }
 
-template <bool XB, bool YB>
+template <bool XB, bool YB, bool NORM = false>
 int gemv_int4(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
               const void* x, void* y, int64_t rows, int64_t cols, int64_t gs,
-              hipStream_t stream) {
+              hipStream_t stream, const uint16_t* gamma = nullptr, float eps = 0.0f) {
     int st = check_int4_args(fn, packed, scales, zeros, x, y, rows, cols, gs);
     if (st != KC_SUCCESS) return st;
+    if (NORM && rows > 0 && cols > 0 && !gamma)
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: null device pointer", fn);
     if (rows == 0) return KC_SUCCESS;
     const int64_t cpr = cols >> 5;
     const int64_t cpl = (cpr + 63) / 64;
-    // x and its chunk sums in LDS
-    const size_t lds = static_cast<size_t>(cpr) * (XB ? 64 : 128) + static_cast<size_t>(cpr) * 4;
+    // x and its chunk sums in LDS (and the waves' partial sums of squares)
+    const size_t lds = static_cast<size_t>(cpr) * (XB ? 64 : 128) + static_cast<size_t>(cpr) * 4 +
+                       (NORM ? 8 * sizeof(float) : 0);
     const bool fast = cols > 0 && gs >= 32 && kc::is_pow2(gs) && cpl <= 16 &&
                       rows <= INT32_MAX && kc::aligned(packed, 16) && kc::aligned(x, 16) &&
+                      (!NORM || kc::aligned(gamma, 16)) &&
                       lds <= static_cast<size_t>(device_max_lds());
+    const GemvArgs a{packed, scales, zeros, x, y, gamma, eps};
     if (fast) {
         const int gshift = kc::ilog2(gs) - 5;
         const int slot = gshift >= 2 ? 16 : 64;
         const int r = static_cast<int>(rows), c = static_cast<int>(cols);
-#define KC_FAST_CASE(N)                                                                         \
-    case N:                                                                                     \
-        launch_fast_cpl<N, XB, YB>(slot, packed, scales, zeros, x, y, r, c, gshift, lds, stream); \
+#define KC_FAST_CASE(N)                                                            \
+    case N:                                                                        \
+        launch_fast_cpl<N, XB, YB, NORM>(slot, a, r, c, gshift, lds, stream);      \
         break;
         switch (cpl) {
             KC_FAST_CASE(1) KC_FAST_CASE(2) KC_FAST_CASE(3) KC_FAST_CASE(4)
@@ -409,8 +494,8 @@ int gemv_int4(const char* fn, const uint8_t* packed, const float* scales, const 
         if (grid > INT32_MAX)
             return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: rows=%lld too large", fn,
                                  (long long)rows);
-        gemv_int4_generic_kernel<XB, YB><<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(
-            packed, scales, zeros, x, y, rows, cols, gs);
+        gemv_int4_generic_kernel<XB, YB, NORM><<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(
+            packed, scales, zeros, x, y, rows, cols, gs, gamma, eps);
     }
     return kc::check_launch(fn);
 }
@@ -467,4 +552,16 @@ extern "C" int kc_gemv_int4_bf16(const uint8_t* d_packed, const float* d_scales,
                                  int rows, int cols, int group_size, kc_stream_t stream) {
     return gemv_int4<true, true>("kc_gemv_int4_bf16", d_packed, d_scales, d_zeros, d_x, d_y,
                                  rows, cols, group_size, stream);
+}
+
+// y = W bf16(RMSNorm(h) * gamma): the RMSNorm in front of a decoder GEMV
+// (rmsnorm.cu:40-70 followed by quant_int4.cu:126-175), folded into the
+// GEMV's staging of x.  Every workgroup sums the squares of h itself (K
+// bf16 values from the cache), so the normalized vector is never written.
+extern "C" int kc_rmsnorm_gemv_int4_bf16(const uint16_t* d_h, const uint16_t* d_gamma, float eps,
+                                         const uint8_t* d_packed, const float* d_scales,
+                                         const uint8_t* d_zeros, uint16_t* d_y, int rows, int cols,
+                                         int group_size, kc_stream_t stream) {
+    return gemv_int4<true, true, true>("kc_rmsnorm_gemv_int4_bf16", d_packed, d_scales, d_zeros, d_h,
+                                       d_y, rows, cols, group_size, stream, d_gamma, eps);
 }

@@ -59,10 +59,6 @@ void launch_depthwise_conv1d(const float*, const float*, const float*, float*, i
     stub("launch_depthwise_conv1d");
 }
 
-void launch_rmsnorm(const float*, const float*, float*, int, int, float, kc_stream_t) {
-    stub("launch_rmsnorm");
-}
-
 void nccl_comm_init_all(void**, int, const int*) { stub("nccl_comm_init_all"); }
 void nccl_comm_destroy(void*) {}
 void nccl_group_start(void) {}

@@ -125,6 +125,9 @@ PROTOTYPES = {
     "kc_quantize_fp8_smooth_div_f32": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp], _i),
     "kc_quantize_fp8_smooth_div_bf16": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp], _i),
     "kc_quantize_fp8_smooth_mul_bf16": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp], _i),
+    "launch_rmsnorm": ([_vp, _vp, _vp, _i, _i, ctypes.c_float, _vp], None),
+    "kc_rmsnorm_bf16": ([_vp, _vp, _vp, _i, _i, ctypes.c_float, _vp], _i),
+    "kc_rmsnorm_gemv_int4_bf16": ([_vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
 }
 
 
@@ -454,6 +457,46 @@ def fp8_gemm_w8a8(qx, sx, qw, sw, out_dtype=None):
     with kernel_span("fp8_gemm_w8a8", m=M, n=N, k=K):
         st = fn(_ptr(qx), _ptr(sx), _ptr(qw), _ptr(sw), _ptr(y), M, N, K, _stream())
     _check("fp8_gemm_w8a8", st)
+    return y
+
+
+def rmsnorm(x, g, eps: float = 1e-6):
+    """y = g * x / sqrt(mean(x^2, -1) + eps) per row (rmsnorm.cu:40-70):
+    fp32 x and g through launch_rmsnorm, bf16 through kc_rmsnorm_bf16."""
+    import torch
+    x, g = x.contiguous(), g.contiguous()
+    _on_gpu(x, g)
+    D = x.shape[-1]
+    rows = x.numel() // max(D, 1)
+    if g.numel() != D or g.dtype != x.dtype:
+        raise ValueError("rmsnorm: g must hold D values of x's dtype")
+    y = torch.empty_like(x)
+    with kernel_span("rmsnorm", rows=rows, d=D):
+        if x.dtype == torch.float32:
+            _get_lib().launch_rmsnorm(_ptr(x), _ptr(g), _ptr(y), rows, D, eps, _stream())
+            st = None
+        elif x.dtype == torch.bfloat16:
+            st = _get_lib().kc_rmsnorm_bf16(_ptr(x), _ptr(g), _ptr(y), rows, D, eps, _stream())
+        else:
+            raise TypeError("rmsnorm: float32 or bfloat16 tensors")
+    _check("rmsnorm", st)
+    return y
+
+
+def rmsnorm_int4_gemv_bf16(h, gamma, packed, scales, zeros, rows: int, cols: int,
+                           group_size: int = 128, eps: float = 1e-6):
+    """y = W_int4 * bf16(rmsnorm(h) * gamma) in one launch: bf16 h, gamma
+    [cols], bf16 y [rows] (kc_rmsnorm_gemv_int4_bf16)."""
+    import torch
+    h, gamma, packed, scales, zeros = (h.contiguous(), gamma.contiguous(), packed.contiguous(),
+                                       scales.contiguous(), zeros.contiguous())
+    _on_gpu(h, gamma, packed, scales, zeros)
+    y = torch.empty(rows, dtype=torch.bfloat16, device=packed.device)
+    with kernel_span("rmsnorm_int4_gemv_bf16", rows=rows, cols=cols, group_size=group_size):
+        st = _get_lib().kc_rmsnorm_gemv_int4_bf16(_ptr(h), _ptr(gamma), eps, _ptr(packed),
+                                                  _ptr(scales), _ptr(zeros), _ptr(y), rows, cols,
+                                                  group_size, _stream())
+    _check("rmsnorm_int4_gemv_bf16", st)
     return y
 
 

@@ -176,6 +176,21 @@ py::array_t<float> smoothquant_scale(const carray<float>& input, const carray<fl
     return download<float>(out, {rows, cols});
 }
 
+// pybind_transformer.cpp:759-800 of the reference: x fp32 [rows, D], g [D].
+py::array_t<float> rmsnorm(const carray<float>& x, const carray<float>& g, float eps) {
+    need(x.ndim() == 2, "rmsnorm: x must be 2-D [rows, D]");
+    need(g.ndim() == 1, "rmsnorm: g must be 1-D [D]");
+    const int rows = static_cast<int>(x.shape(0)), D = static_cast<int>(x.shape(1));
+    need(g.shape(0) == D, "rmsnorm: g.shape[0] must equal D");
+    DeviceBuffer dx = upload(x), dg = upload(g);
+    DeviceBuffer dy(static_cast<size_t>(rows) * D * sizeof(float));
+    kc_get_last_error();
+    launch_rmsnorm(dx.as<float>(), dg.as<float>(), dy.as<float>(), rows, D, eps, nullptr);
+    hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    check_library("rmsnorm");
+    return download<float>(dy, {rows, D});
+}
+
 void register_not_implemented(py::module_& m, const char* name, const char* doc) {
     const std::string msg = std::string(name) + " is outside the MI355X build's quantization path";
     m.def(
@@ -203,6 +218,8 @@ PYBIND11_MODULE(kernel_craft_transformer, m) {
           py::arg("cols"), py::arg("per_token") = true, "Dequantize FP8 E4M3 back to FP32");
     m.def("smoothquant_scale", &smoothquant_scale, py::arg("input"), py::arg("smooth_scales"),
           "SmoothQuant activation smoothing: input / smooth_scales (per column)");
+    m.def("rmsnorm", &rmsnorm, py::arg("x"), py::arg("g"), py::arg("eps") = 1e-6f,
+          "RMSNorm: y = g * x / sqrt(mean(x^2) + eps) per row (fp32)");
 
     register_not_implemented(m, "flash_attention", "Not implemented in this build");
     register_not_implemented(m, "paged_attention", "Not implemented in this build");
@@ -218,6 +235,5 @@ PYBIND11_MODULE(kernel_craft_transformer, m) {
     register_not_implemented(m, "nccl_group_end", "Not implemented in this build");
     register_not_implemented(m, "selective_scan", "Not implemented in this build");
     register_not_implemented(m, "depthwise_conv1d", "Not implemented in this build");
-    register_not_implemented(m, "rmsnorm", "Not implemented in this build");
     m.attr("HAVE_NCCL") = false;
 }

@@ -26,6 +26,10 @@
  *   kco_smoothquant_scale            KAT test_fp8_quant.cpp:99-135, numpy divide.
  *   extensions                       composition identities with the pinned
  *                                    functions above (fused == two-step).
+ *   kco_rmsnorm_*                    reference KATs test_mamba_ops.cpp:219-300 (glibc
+ *                                    srand/rand recipes) and test_mamba_bindings.py:
+ *                                    251-290 (golden fixtures); constant rows, scale
+ *                                    invariance, rms of the output.
  */
 #include "kc_oracle.h"
 
@@ -378,5 +382,37 @@ void kco_quantize_fp8_smooth_mul_bf16(const uint16_t* in, const float* s,
         for (int64_t c = 0; c < cols; ++c)
             out[r * cols + c] =
                 (int8_t)clamp_encode((kco_bf16_to_f32(w[c]) * s[c]) / sc);
+    }
+}
+
+/* RMSNorm, the reference's CPU check (tests/test_mamba_ops.cpp:89-101) of
+ * rmsnorm.cu:40-70: per row, ss = sum x^2 in index order (one fp32 multiply
+ * and one fp32 add per term), rms_inv = 1 / sqrt(ss / D + eps), and
+ * y = (g * x) * rms_inv. */
+void kco_rmsnorm_f32(const float* x, const float* g, float* y, int64_t rows,
+                     int64_t D, float eps) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * D;
+        float ss = 0.0f;
+        for (int64_t i = 0; i < D; ++i) ss += xr[i] * xr[i];
+        const float rms_inv = 1.0f / sqrtf(ss / (float)D + eps);
+        for (int64_t i = 0; i < D; ++i) y[r * D + i] = g[i] * xr[i] * rms_inv;
+    }
+}
+
+/* The same with bf16 x, g and y (fp32 arithmetic, y rounded to nearest
+ * even): the input the fused RMSNorm -> GEMV hands its GEMV. */
+void kco_rmsnorm_bf16(const uint16_t* x, const uint16_t* g, uint16_t* y,
+                      int64_t rows, int64_t D, float eps) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint16_t* xr = x + r * D;
+        float ss = 0.0f;
+        for (int64_t i = 0; i < D; ++i) {
+            const float v = kco_bf16_to_f32(xr[i]);
+            ss += v * v;
+        }
+        const float rms_inv = 1.0f / sqrtf(ss / (float)D + eps);
+        for (int64_t i = 0; i < D; ++i)
+            y[r * D + i] = kco_f32_to_bf16(kco_bf16_to_f32(g[i]) * kco_bf16_to_f32(xr[i]) * rms_inv);
     }
 }

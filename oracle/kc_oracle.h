@@ -83,6 +83,12 @@ void kco_quantize_fp8_smooth_mul_bf16(const uint16_t* in, const float* s,
                                       int8_t* out, float* scales,
                                       int64_t rows, int64_t cols);
 
+/* RMSNorm (tests/test_mamba_ops.cpp:89-101, rmsnorm.cu:40-70). */
+void kco_rmsnorm_f32(const float* x, const float* g, float* y, int64_t rows,
+                     int64_t D, float eps);
+void kco_rmsnorm_bf16(const uint16_t* x, const uint16_t* g, uint16_t* y,
+                      int64_t rows, int64_t D, float eps);
+
 #ifdef __cplusplus
 }
 #endif

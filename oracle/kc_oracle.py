@@ -45,6 +45,8 @@ _SIGS = {
     "kco_quantize_fp8_smooth_div_f32": ([_P, _P, _P, _P, _I64, _I64], None),
     "kco_quantize_fp8_smooth_div_bf16": ([_P, _P, _P, _P, _I64, _I64], None),
     "kco_quantize_fp8_smooth_mul_bf16": ([_P, _P, _P, _P, _I64, _I64], None),
+    "kco_rmsnorm_f32": ([_P, _P, _P, _I64, _I64, ctypes.c_float], None),
+    "kco_rmsnorm_bf16": ([_P, _P, _P, _I64, _I64, ctypes.c_float], None),
 }
 
 
@@ -181,6 +183,21 @@ def quantize_fp8_per_token_bf16(x_bf16):
     s = np.empty(rows, np.float32)
     lib().kco_quantize_fp8_per_token_bf16(_p(x_bf16), _p(q), _p(s), rows, cols)
     return q, s
+
+
+def rmsnorm(x, g, eps=1e-6):
+    """RMSNorm of every row of x (tests/test_mamba_ops.cpp:89-101): fp32 x, g
+    give fp32 y; bf16 bit patterns (uint16) give bf16 bits."""
+    if np.asarray(x).dtype == np.uint16:
+        x, g = _c(x, np.uint16), _c(g, np.uint16)
+        fn = lib().kco_rmsnorm_bf16
+    else:
+        x, g = _c(x, np.float32), _c(g, np.float32)
+        fn = lib().kco_rmsnorm_f32
+    x2 = x.reshape(-1, x.shape[-1])
+    y = np.empty_like(x2)
+    fn(_p(x2), _p(g), _p(y), x2.shape[0], x2.shape[1], float(eps))
+    return y.reshape(x.shape)
 
 
 def col_absmax(x):

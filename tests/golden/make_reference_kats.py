@@ -27,6 +27,25 @@ def c_rand_unit_f32() -> np.float32:
     return np.float32(np.float32(_libc.rand()) / np.float32(RAND_MAX))
 
 
+def c_fill_rand(n: int, lo: float, hi: float) -> np.ndarray:
+    """tests/test_mamba_ops.cpp:31-33: lo + (hi - lo) * (float)rand() / RAND_MAX,
+    left to right in fp32."""
+    lo32, span = np.float32(lo), np.float32(np.float32(hi) - np.float32(lo))
+    return np.array([lo32 + (span * np.float32(_libc.rand())) / np.float32(RAND_MAX)
+                     for _ in range(n)], np.float32)
+
+
+def rmsnorm_cpu(x: np.ndarray, g: np.ndarray, eps: np.float32) -> np.ndarray:
+    """tests/test_mamba_ops.cpp:89-101: ss += x*x in index order (fp32),
+    rms_inv = 1 / sqrt(ss / D + eps), y = g * x * rms_inv."""
+    rows, D = x.shape
+    ss = np.zeros(rows, np.float32)
+    for i in range(D):
+        ss = (ss + x[:, i] * x[:, i]).astype(np.float32)
+    rms_inv = np.float32(1.0) / np.sqrt(ss / np.float32(D) + eps)
+    return (g[None, :] * x * rms_inv[:, None]).astype(np.float32)
+
+
 def pack_nibbles(w: np.ndarray) -> np.ndarray:
     """tests/test_quant_int4.cpp:31-33: low nibble = even column."""
     w = w.astype(np.int64)
@@ -147,6 +166,30 @@ def main() -> None:
     # test_transformer_bindings.py:212-220 and test_vllm_backend.py:214-223
     fx["fp8_tok_rng42_x"] = np.random.default_rng(42).uniform(-1, 1, (8, 64)).astype(np.float32)
     fx["fp8_tok_rng11_x"] = np.random.default_rng(11).uniform(-1, 1, (8, 64)).astype(np.float32)
+
+    # RMSNorm, tests/test_mamba_ops.cpp:219-300: fill_rand (:31-33) from
+    # glibc srand/rand, expected values by rmsnorm_cpu (:89-101), tolerances
+    # 1e-5 / 1e-4 / 1e-4 max abs.  Only the leading rows of the larger cases
+    # are kept (their rows come from the full recipe).
+    for name, seed, rows, D, xr, gr, keep in (("rms_basic", 3, 8, 8, (-1, 1), (0.5, 1.5), 8),
+                                              ("rms_d768", 77, 128, 768, (-2, 2), (0.8, 1.2), 4),
+                                              ("rms_d4096", 13, 16, 4096, (-1, 1), (0.9, 1.1), 2)):
+        _libc.srand(seed)
+        x = c_fill_rand(rows * D, *xr).reshape(rows, D)
+        g = c_fill_rand(D, *gr)
+        fx[f"{name}_x"] = x[:keep]
+        fx[f"{name}_g"] = g
+        fx[f"{name}_expected"] = rmsnorm_cpu(x[:keep], g, np.float32(1e-6))
+
+    # RMSNorm, src/python/tests/test_mamba_bindings.py:251-262 (default_rng(3),
+    # expected by rmsnorm_ref :100-113 in float32 numpy, tol 1e-5)
+    rng = np.random.default_rng(3)
+    x = rng.uniform(-1, 1, (8, 64)).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, 64).astype(np.float32)
+    ss = np.mean(x ** 2, axis=-1, keepdims=True)
+    fx["rms_py_rng3_x"] = x
+    fx["rms_py_rng3_g"] = g
+    fx["rms_py_rng3_expected"] = (g * x * (1.0 / np.sqrt(ss + 1e-6))).astype(np.float32)
 
     np.savez_compressed(OUT, **fx)
     print(f"wrote {OUT} ({len(fx)} arrays)")

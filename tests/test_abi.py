@@ -66,9 +66,9 @@ def test_stubs_report_not_implemented(lib, capfd):
     assert b"launch_flash_attention" in lib.kc_last_error_string()
     assert lib.kc_get_last_error() == 2
     assert lib.kc_get_last_error() == 0
-    lib.launch_rmsnorm.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int, ctypes.c_int,
-                                                           ctypes.c_float, ctypes.c_void_p]
-    lib.launch_rmsnorm(None, None, None, 1, 1, 1e-6, None)
+    lib.launch_depthwise_conv1d.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 4 + [
+        ctypes.c_void_p]
+    lib.launch_depthwise_conv1d(None, None, None, None, 1, 1, 1, 1, None)
     assert lib.kc_get_last_error() == 2
     lib.nccl_comm_count.restype = ctypes.c_int
     lib.nccl_comm_user_rank.restype = ctypes.c_int

@@ -1,0 +1,176 @@
+"""RMSNorm and the fused RMSNorm -> INT4 GEMV on the GPU vs the CPU oracle.
+
+Bars: launch_rmsnorm within the reference tests' own max-abs bars (1e-5 for
+rows of 8 and 64 values, 1e-4 beyond; tests/test_mamba_ops.cpp:219-300,
+test_mamba_bindings.py:251-300) of the oracle, which reproduces the
+reference's CPU check bit for bit.  The kernel sums the squares in another
+order (and with FMA, as nvcc contracts the reference kernel), so a bf16
+output may sit one unit in the last place from the oracle's.  The fused
+GEMV's bf16 output is held to relative L2 3e-3 of the fp64 GEMV of the
+oracle's normalized vector (the bf16 GEMV bar is 1e-2).
+"""
+import numpy as np
+import pytest
+
+import kc_abi
+from kc_abi import ptr, stream
+from kc_data import bf16_bits_to_f32, f32_to_bf16_bits, make_int4, normal_bf16, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _dev_bf16(torch, bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).cuda().view(torch.bfloat16)
+
+
+def _bits(t):
+    return t.view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+
+
+def _rmsnorm_f32(torch, x, g, eps=1e-6, offset=0):
+    """launch_rmsnorm; offset (in floats) moves every pointer off 16-byte
+    alignment to take the scalar path."""
+    L = kc_abi.lib()
+    rows, D = x.shape
+    bx = torch.zeros(x.size + offset, dtype=torch.float32, device="cuda")
+    bg = torch.zeros(D + offset, dtype=torch.float32, device="cuda")
+    by = torch.full((x.size + offset,), float("nan"), dtype=torch.float32, device="cuda")
+    bx[offset:] = _dev(torch, x.reshape(-1))
+    bg[offset:] = _dev(torch, g)
+    print(f"launch_rmsnorm rows={rows} D={D} offset={offset}", flush=True)
+    L.launch_rmsnorm(ptr(bx[offset:]), ptr(bg[offset:]), ptr(by[offset:]), rows, D, eps, stream())
+    torch.cuda.synchronize()
+    kc_abi.check("launch_rmsnorm")
+    return by[offset:].cpu().numpy().reshape(rows, D)
+
+
+@pytest.mark.parametrize("name,tol", [("rms_basic", 1e-5), ("rms_d768", 1e-4), ("rms_d4096", 1e-4),
+                                      ("rms_py_rng3", 1e-5)])
+def test_rmsnorm_reference_kats(gpu, golden, name, tol):
+    x, g = golden[f"{name}_x"], golden[f"{name}_g"]
+    y = _rmsnorm_f32(gpu, x, g)
+    assert np.max(np.abs(y - golden[f"{name}_expected"])) < tol
+
+
+@pytest.mark.parametrize("rows,D,offset", [(1, 4096, 0), (37, 4096, 0), (5, 256, 0), (3, 64, 0),
+                                           (9, 8192, 0), (2, 12, 0), (4, 777, 0), (6, 1024, 1),
+                                           (3, 20000, 0), (0, 64, 0)])
+def test_rmsnorm_f32_shapes(gpu, oracle, rows, D, offset):
+    rng = np.random.default_rng(rows * 31 + D)
+    x = rng.uniform(-2, 2, (rows, D)).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    y = _rmsnorm_f32(gpu, x, g, 1e-6, offset)
+    if rows:
+        exp = oracle.rmsnorm(x, g, 1e-6)
+        assert np.max(np.abs(y - exp)) <= 2e-5 * np.max(np.abs(exp))
+
+
+def test_rmsnorm_unit_and_constant_rows(gpu):
+    """test_mamba_bindings.py:288-310: a constant row gives g; with g = 1 the
+    output's rms is 1."""
+    y = _rmsnorm_f32(gpu, np.full((4, 64), 2.0, np.float32), np.ones(64, np.float32))
+    assert np.max(np.abs(y - 1.0)) < 1e-5
+    x = np.random.default_rng(22).uniform(-1, 1, (32, 256)).astype(np.float32)
+    y = _rmsnorm_f32(gpu, x, np.ones(256, np.float32))
+    assert np.max(np.abs(np.sqrt(np.mean(y.astype(np.float64) ** 2, axis=1)) - 1.0)) < 1e-4
+
+
+@pytest.mark.parametrize("rows,D", [(1, 4096), (16, 4096), (7, 8192), (3, 14336), (5, 100)])
+def test_rmsnorm_bf16(gpu, oracle, rows, D):
+    L = kc_abi.lib()
+    rng = np.random.default_rng(D + rows)
+    xb = f32_to_bf16_bits(rng.standard_normal((rows, D)).astype(np.float32) * 3)
+    gb = f32_to_bf16_bits(rng.uniform(0.5, 1.5, D).astype(np.float32))
+    dx, dg = _dev_bf16(gpu, xb), _dev_bf16(gpu, gb)
+    dy = gpu.empty(rows, D, dtype=gpu.bfloat16, device="cuda")
+    print(f"kc_rmsnorm_bf16 rows={rows} D={D}", flush=True)
+    st = L.kc_rmsnorm_bf16(ptr(dx), ptr(dg), ptr(dy), rows, D, 1e-5, stream())
+    kc_abi.check("kc_rmsnorm_bf16", st)
+    gpu.cuda.synchronize()
+    got = bf16_bits_to_f32(_bits(dy))
+    exp = bf16_bits_to_f32(oracle.rmsnorm(xb, gb, 1e-5))
+    ulp = np.abs(exp) * 2.0 ** -7 + 1e-30
+    assert np.all(np.abs(got - exp) <= ulp)
+    assert np.mean(got == exp) > 0.99
+
+
+def _fused(torch, packed, scales, zeros, hb, gb, rows, cols, gs, eps=1e-5, gamma_offset=0):
+    L = kc_abi.lib()
+    dp, ds, dz = _dev(torch, packed), _dev(torch, scales), _dev(torch, zeros)
+    dh = _dev_bf16(torch, hb)
+    gbuf = torch.zeros(cols + gamma_offset, dtype=torch.bfloat16, device="cuda")
+    gbuf[gamma_offset:] = _dev_bf16(torch, gb)
+    dy = torch.full((rows,), float("nan"), dtype=torch.bfloat16, device="cuda")
+    print(f"kc_rmsnorm_gemv_int4_bf16 rows={rows} cols={cols} gs={gs} goff={gamma_offset}",
+          flush=True)
+    st = L.kc_rmsnorm_gemv_int4_bf16(ptr(dh), ptr(gbuf[gamma_offset:]), eps, ptr(dp), ptr(ds),
+                                     ptr(dz), ptr(dy), rows, cols, gs, stream())
+    kc_abi.check("kc_rmsnorm_gemv_int4_bf16", st)
+    torch.cuda.synchronize()
+    return bf16_bits_to_f32(_bits(dy)), (dp, ds, dz, dh)
+
+
+@pytest.mark.parametrize("rows,cols,gs,goff", [(6144, 4096, 128, 0), (512, 14336, 128, 0),
+                                               (300, 20480, 128, 0), (77, 1024, 64, 0),
+                                               (33, 2080, 32, 0), (40, 384, 128, 1),
+                                               (16, 96, 24, 0)])
+def test_rmsnorm_gemv_fused(gpu, oracle, rows, cols, gs, goff):
+    """Fast path (K up to 16384 and beyond, groups of 32..128), and the
+    generic path (unaligned gamma, groups that are not a power of two)."""
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=rows + cols)
+    rng = np.random.default_rng(cols)
+    hb = f32_to_bf16_bits(rng.standard_normal(cols).astype(np.float32) * 4)
+    gb = f32_to_bf16_bits(rng.uniform(0.5, 1.5, cols).astype(np.float32))
+    y, _ = _fused(gpu, packed, scales, zeros, hb, gb, rows, cols, gs, 1e-5, goff)
+    xb = oracle.rmsnorm(hb[None, :], gb, 1e-5)[0]
+    truth = oracle.gemv_int4_f64(packed, scales, zeros.reshape(-1), bf16_bits_to_f32(xb), rows,
+                                 cols, gs)
+    assert rel_l2(y, truth) < 3e-3
+
+
+def test_rmsnorm_gemv_fused_matches_two_launches(gpu):
+    """The fused launch against kc_rmsnorm_bf16 followed by kc_gemv_int4_bf16
+    (Llama gate/up shape): the same normalized vector up to the order of the
+    sum of squares, so the outputs agree to a few bf16 units."""
+    L = kc_abi.lib()
+    rows, cols, gs = 28672, 4096, 128
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=8)
+    rng = np.random.default_rng(9)
+    hb = f32_to_bf16_bits(rng.standard_normal(cols).astype(np.float32))
+    gb = f32_to_bf16_bits(rng.uniform(0.5, 1.5, cols).astype(np.float32))
+    y, (dp, ds, dz, dh) = _fused(gpu, packed, scales, zeros, hb, gb, rows, cols, gs)
+    dg = _dev_bf16(gpu, gb)
+    dx = gpu.empty(cols, dtype=gpu.bfloat16, device="cuda")
+    dy = gpu.empty(rows, dtype=gpu.bfloat16, device="cuda")
+    print("kc_rmsnorm_bf16 + kc_gemv_int4_bf16 gate/up", flush=True)
+    kc_abi.check("kc_rmsnorm_bf16", L.kc_rmsnorm_bf16(ptr(dh), ptr(dg), ptr(dx), 1, cols, 1e-5,
+                                                      stream()))
+    kc_abi.check("kc_gemv_int4_bf16", L.kc_gemv_int4_bf16(ptr(dp), ptr(ds), ptr(dz), ptr(dx),
+                                                          ptr(dy), rows, cols, gs, stream()))
+    gpu.cuda.synchronize()
+    y2 = bf16_bits_to_f32(_bits(dy))
+    assert rel_l2(y, y2) < 1e-3
+
+
+def test_rmsnorm_gemv_argument_errors(gpu):
+    L = kc_abi.lib()
+    rows, cols, gs = 64, 256, 128
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=1)
+    dp, ds, dz = _dev(gpu, packed), _dev(gpu, scales), _dev(gpu, zeros)
+    dh = _dev_bf16(gpu, normal_bf16((cols,), seed=2))
+    dy = gpu.empty(rows, dtype=gpu.bfloat16, device="cuda")
+    L.kc_get_last_error()
+    st = L.kc_rmsnorm_gemv_int4_bf16(ptr(dh), None, 1e-5, ptr(dp), ptr(ds), ptr(dz), ptr(dy),
+                                     rows, cols, gs, stream())
+    assert st == 1 and b"null" in L.kc_last_error_string()
+    st = L.kc_rmsnorm_gemv_int4_bf16(ptr(dh), ptr(dh), 1e-5, ptr(dp), ptr(ds), ptr(dz), ptr(dy),
+                                     rows, cols + 1, gs, stream())
+    assert st == 1
+    L.kc_get_last_error()
+    st = L.kc_rmsnorm_bf16(ptr(dh), ptr(dh), ptr(dy), -1, cols, 1e-5, stream())
+    assert st == 1
+    L.kc_get_last_error()

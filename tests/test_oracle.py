@@ -503,3 +503,61 @@ def test_bf16_rounding_helpers(oracle):
         assert oracle.lib().kco_f32_to_bf16(float(v)) == int(b)
     ref = torch.from_numpy(vals).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     np.testing.assert_array_equal(bits, ref)
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm (tests/test_mamba_ops.cpp:89-101, rmsnorm.cu:40-70)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["rms_basic", "rms_d768", "rms_d4096"])
+def test_rmsnorm_reference_kats(oracle, golden, name):
+    """The reference C++ tests' recipes (glibc rand) and CPU check: the
+    restatement reproduces rmsnorm_cpu's fp32 results bit for bit."""
+    y = oracle.rmsnorm(golden[f"{name}_x"], golden[f"{name}_g"], 1e-6)
+    np.testing.assert_array_equal(y, golden[f"{name}_expected"])
+
+
+def test_rmsnorm_reference_kat_python(oracle, golden):
+    """test_mamba_bindings.py:251-262 (numpy mean, so another summation
+    order): the reference test's own 1e-5 bar."""
+    y = oracle.rmsnorm(golden["rms_py_rng3_x"], golden["rms_py_rng3_g"], 1e-6)
+    assert np.max(np.abs(y - golden["rms_py_rng3_expected"])) < 1e-5
+
+
+def test_rmsnorm_closed_forms(oracle):
+    # a constant row c: y = g * c / sqrt(c^2 + eps)
+    D = 64
+    g = np.linspace(0.5, 1.5, D).astype(np.float32)
+    x = np.full((3, D), [[2.0], [-0.25], [3.0]], np.float32)
+    y = oracle.rmsnorm(x, g, 1e-6)
+    c = x[:, :1].astype(np.float64)
+    np.testing.assert_allclose(y, g[None, :] * c / np.sqrt(c * c + 1e-6), rtol=2e-7)
+    # with g = 1 the output's mean square is ms / (ms + eps): a divisor other
+    # than D, or a missing square, moves it
+    rng = np.random.default_rng(22)
+    x = rng.uniform(-1, 1, (32, 256)).astype(np.float32)
+    eps = 0.25
+    y = oracle.rmsnorm(x, np.ones(256, np.float32), eps).astype(np.float64)
+    ms = np.mean(x.astype(np.float64) ** 2, axis=1)
+    np.testing.assert_allclose(np.mean(y * y, axis=1), ms / (ms + eps), rtol=1e-5)
+
+
+def test_rmsnorm_scale_invariance_exact(oracle):
+    """With eps = 0 a power-of-two scale of x cancels exactly (every step
+    scales by a power of two), so y is bit-identical."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((4, 300)).astype(np.float32)
+    g = rng.uniform(0.5, 2.0, 300).astype(np.float32)
+    y = oracle.rmsnorm(x, g, 0.0)
+    for k in (-8, 3, 20):
+        np.testing.assert_array_equal(oracle.rmsnorm(x * np.float32(2.0 ** k), g, 0.0), y)
+
+
+def test_rmsnorm_bf16_is_rounded_f32(oracle):
+    """bf16 in, bf16 out: the fp32 RMSNorm of the bf16 values, rounded."""
+    rng = np.random.default_rng(6)
+    xb = f32_to_bf16_bits(rng.standard_normal((5, 4096)).astype(np.float32))
+    gb = f32_to_bf16_bits(rng.uniform(0.5, 1.5, 4096).astype(np.float32))
+    yb = oracle.rmsnorm(xb, gb, 1e-5)
+    ref = oracle.rmsnorm(bf16_bits_to_f32(xb), bf16_bits_to_f32(gb), 1e-5)
+    np.testing.assert_array_equal(yb, f32_to_bf16_bits(ref))

@@ -36,11 +36,12 @@ SIGNATURES = {
     "gemv_int4": [("packed", None), ("scales", None), ("zeros", None), ("x", None), ("rows", None),
                   ("cols", None), ("group_size", "128")],
     "smoothquant_scale": [("input", None), ("smooth_scales", None)],
+    "rmsnorm": [("x", None), ("g", None), ("eps", "9.999999974752427e-07")],  # 1e-6f
 }
 OUT_OF_SCOPE = ["flash_attention", "paged_attention", "speculative_decode", "ring_allreduce",
                 "allgather", "col_parallel_linear", "row_parallel_linear", "nccl_comm_init",
                 "nccl_comm_destroy", "nccl_allreduce", "nccl_group_start", "nccl_group_end",
-                "selective_scan", "depthwise_conv1d", "rmsnorm"]
+                "selective_scan", "depthwise_conv1d"]
 
 
 def _args(fn):
@@ -173,3 +174,18 @@ def test_module_matches_oracle(gpu, kct, oracle):
                                   oracle.dequantize_fp8(q, s, 37, 200, per_token=False))
     sm = rng.uniform(0.1, 10.0, 200).astype(np.float32)
     np.testing.assert_array_equal(kct.smoothquant_scale(a, sm), oracle.smoothquant_scale(a, sm))
+
+
+@pytest.mark.gpu
+def test_reference_rmsnorm_binding(gpu, kct, golden):
+    """test_mamba_bindings.py:251-320 re-expressed: the rng(3) case against its
+    expected values, a constant input, and the output shape."""
+    print("pybind rmsnorm", flush=True)
+    y = kct.rmsnorm(golden["rms_py_rng3_x"], golden["rms_py_rng3_g"])
+    assert np.max(np.abs(y - golden["rms_py_rng3_expected"])) < 1e-5
+    y = kct.rmsnorm(np.full((4, 64), 2.0, np.float32), np.ones(64, np.float32))
+    assert np.max(np.abs(y - 1.0)) < 1e-5
+    x = np.random.default_rng(0).uniform(-1, 1, (7, 128)).astype(np.float32)
+    assert kct.rmsnorm(x, np.ones(128, np.float32)).shape == (7, 128)
+    with pytest.raises(ValueError, match="g.shape"):
+        kct.rmsnorm(x, np.ones(127, np.float32))
