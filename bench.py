@@ -25,7 +25,9 @@ and per-channel W, fp32 [4096, 4096]) and `fp8_cfg4` (SmoothQuant statistics
 and the two fused quantizers on bf16 X [16384, 8192] and W [28672, 8192]),
 `fp8_gemm_cfg4` (the W8A8 FP8 GEMM on those codes, TFLOP/s against the FP8
 matrix peak, with torch._scaled_mm on the same codes beside it) and
-`convert_int4` (GPTQ and AWQ checkpoints of the gate/up layer to the layout).
+`convert_int4` (GPTQ and AWQ checkpoints of the gate/up layer to the layout) and
+`decode_fusion` (the RMSNorm in front of the QKV and gate/up GEMVs, fused into
+the GEMV, against two launches).
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20]
 """
@@ -517,6 +519,37 @@ def main() -> int:
         f"(torch._scaled_mm: {fp8_gemm['torch_scaled_mm_TFLOPs']})")
     del X4, W4, qx, qw, Y4
 
+    # ---- decode fusion: the RMSNorm in front of the QKV and gate/up GEMVs ----
+    # (kc_rmsnorm_bf16 then kc_gemv_int4_bf16, against the fused launch)
+    fusion = {"config": "RMSNorm (bf16 h, gamma [4096], eps 1e-5) + INT4 GEMV, two launches "
+                        "vs kc_rmsnorm_gemv_int4_bf16; GB/s of the GEMV's algorithmic bytes "
+                        "plus gamma"}
+    h_ = torch.randn(4096, device=dev, generator=gen).to(torch.bfloat16)
+    gam = torch.empty(4096, device=dev).uniform_(0.5, 1.5, generator=gen).to(torch.bfloat16)
+    xn = torch.empty(4096, dtype=torch.bfloat16, device=dev)
+    for i in (0, 2):
+        name, n, k = LLAMA[i]
+        yf = torch.empty(n, dtype=torch.bfloat16, device=dev)
+
+        def two(j: int, i=i, n=n, k=k, yf=yf) -> None:
+            p, sc, z = layers[j % copies][i]
+            ck(lib.kc_rmsnorm_bf16(h_.data_ptr(), gam.data_ptr(), xn.data_ptr(), 1, k, 1e-5,
+                                   stream_ptr()), "kc_rmsnorm_bf16")
+            ck(lib.kc_gemv_int4_bf16(p.data_ptr(), sc.data_ptr(), z.data_ptr(), xn.data_ptr(),
+                                     yf.data_ptr(), n, k, GS, stream_ptr()), "kc_gemv_int4_bf16")
+
+        def fused(j: int, i=i, n=n, k=k, yf=yf) -> None:
+            p, sc, z = layers[j % copies][i]
+            ck(lib.kc_rmsnorm_gemv_int4_bf16(h_.data_ptr(), gam.data_ptr(), 1e-5, p.data_ptr(),
+                                             sc.data_ptr(), z.data_ptr(), yf.data_ptr(), n, k, GS,
+                                             stream_ptr()), "kc_rmsnorm_gemv_int4_bf16")
+        nb = gemv_bytes(n, k) + 2 * k
+        r = hbm(nb, time_launches(torch, fused, reps))
+        r["two_launches_us"] = round(time_launches(torch, two, reps), 3)
+        fusion[name] = r
+        log(f"# fusion {name}: fused {r['avg_us']} us ({r['GBps']} GB/s), two launches "
+            f"{r['two_launches_us']} us")
+
     # ---- checkpoint conversion: GPTQ and AWQ gate/up layer to the layout ----
     kc_, nc_, gc_ = 4096, 28672, 4096 // GS
     conv_b = (kc_ * nc_ // 2 + gc_ * nc_ // 2 + gc_ * nc_ * 2      # qweight, qzeros, fp16 scales
@@ -603,6 +636,7 @@ def main() -> int:
         "gemv_cfg0": cfg0,
         "gemm_cfg3": cfg3,
         "convert_int4": convert,
+        "decode_fusion": fusion,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

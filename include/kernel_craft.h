@@ -145,10 +145,12 @@ int kc_rmsnorm_bf16(const uint16_t* d_x, const uint16_t* d_g, uint16_t* d_y,
 /* The RMSNorm in front of a decoder GEMV, fused into it (no counterpart in
  * the reference, where rmsnorm.cu:83-88 and quant_int4.cu:221-234 are two
  * launches with the normalized vector in memory between them):
- *   y = W x,  x[k] = bf16((gamma[k] * h[k]) / sqrt(sum h^2 / cols + eps))
- * h, gamma [cols] bf16; y [rows] bf16; W as in kc_gemv_int4_bf16.  x is
- * what kc_rmsnorm_bf16 would write, to within the order of the fp32 sum of
- * squares. */
+ *   y = rms_inv * (W x),  x[k] = bf16(gamma[k] * h[k]),
+ *   rms_inv = 1 / sqrt(sum_k h[k]^2 / cols + eps)
+ * h, gamma [cols] bf16; y [rows] bf16; W as in kc_gemv_int4_bf16.  The
+ * same as kc_rmsnorm_bf16 followed by kc_gemv_int4_bf16 except that the
+ * normalization is applied to the fp32 row sums instead of before x is
+ * rounded to bf16 (one rounding less). */
 int kc_rmsnorm_gemv_int4_bf16(const uint16_t* d_h, const uint16_t* d_gamma,
                               float eps, const uint8_t* d_packed,
                               const float* d_scales, const uint8_t* d_zeros,

@@ -46,6 +46,16 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
     return static_cast<uint16_t>(u >> 16);
 }
 
+// Two fp32 -> packed bf16 (lo in bits 0-15), round to nearest even: one
+// v_cvt_pk_bf16_f32 on gfx950.  Finite values and infinities convert as
+// f32_to_bf16 does; a NaN stays a NaN.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
 __host__ __device__ constexpr bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
 
 inline int ilog2(int64_t v) {

@@ -88,10 +88,11 @@ __global__ __launch_bounds__(kThreads) void gemv_int4_generic_kernel(
     const uint8_t* prow = packed + row * nbytes;
     float rms_inv = 1.0f;
     if constexpr (NORM) rms_inv = rms_inverse(static_cast<const uint16_t*>(x), cols, eps, lane);
-    // x[k] as the GEMV sees it: bf16((gamma[k] * h[k]) * rms_inv) when fused
+    // x[k] as the GEMV sees it: bf16(gamma[k] * h[k]) when fused (the row
+    // sum is scaled by rms_inv at the end)
     auto xin = [&](int64_t k) {
         if constexpr (NORM)
-            return kc::bf16_to_f32(kc::f32_to_bf16((kc::bf16_to_f32(gamma[k]) * load_x<true>(x, k)) * rms_inv));
+            return kc::bf16_to_f32(kc::f32_to_bf16(kc::bf16_to_f32(gamma[k]) * load_x<true>(x, k)));
         else
             return load_x<XBF16>(x, k);
     };
@@ -107,7 +108,7 @@ __global__ __launch_bounds__(kThreads) void gemv_int4_generic_kernel(
         acc = fmaf(w0, xin(c0), acc);
         acc = fmaf(w1, xin(c0 + 1), acc);
     }
-    acc = kc::wave_sum(acc);
+    acc = kc::wave_sum(acc) * rms_inv;
     if (lane == 0) store_y<YBF16>(y, row, acc);
 }
 
@@ -205,44 +206,32 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_int4_fast_kernel(
     // loads towards their uses, leaving one row in flight at a time
     __builtin_amdgcn_sched_barrier(0);
 
-    // 1d. fused RMSNorm: sum of squares of h over the workgroup (each quad
-    // once; the clamped duplicates past the end are skipped), partial sums
-    // of the waves added in a fixed order, then x = bf16((gamma h) rms_inv)
+    // 1d. fused RMSNorm: x = bf16(gamma h) is staged in place of h, and each
+    // wave's sum of h^2 (every quad once: the clamped duplicates past the
+    // end are skipped) goes to LDS; after the staging barrier every wave adds
+    // the partial sums in a fixed order and scales its row sums by
+    // rms_inv = 1 / sqrt(sum h^2 / K + eps).  No barrier of its own.
+    [[maybe_unused]] float* part = xsum + cpr;  // WPB partial sums after the chunk sums
     if constexpr (NORM) {
-        float* part = xsum + cpr;  // WPB partial sums after the chunk sums
         float ss = 0.0f;
 #pragma unroll
         for (int u = 0; u < kQPT; ++u) {
-            if (static_cast<int>(threadIdx.x) + u * kThreadsWG < nquads) {
-                const uint32_t w4[4] = {xr[u].x, xr[u].y, xr[u].z, xr[u].w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float lo = __uint_as_float(w4[j] << 16), hi = __uint_as_float(w4[j] & 0xFFFF0000u);
-                    ss = fmaf(lo, lo, ss);
-                    ss = fmaf(hi, hi, ss);
-                }
-            }
-        }
-        ss = kc::wave_sum(ss);
-        if (lane == 0) part[wave] = ss;
-        __syncthreads();
-        float tot = part[0];
-#pragma unroll
-        for (int w = 1; w < WPB; ++w) tot += part[w];
-        const float rms_inv = 1.0f / sqrtf(tot / static_cast<float>(cols) + eps);
-#pragma unroll
-        for (int u = 0; u < kQPT; ++u) {
+            const bool valid = static_cast<int>(threadIdx.x) + u * kThreadsWG < nquads;
             const uint32_t w4[4] = {xr[u].x, xr[u].y, xr[u].z, xr[u].w};
             const uint32_t g4[4] = {gr[u].x, gr[u].y, gr[u].z, gr[u].w};
             uint32_t o4[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float lo = (__uint_as_float(g4[j] << 16) * __uint_as_float(w4[j] << 16)) * rms_inv;
-                const float hi = (__uint_as_float(g4[j] & 0xFFFF0000u) * __uint_as_float(w4[j] & 0xFFFF0000u)) * rms_inv;
-                o4[j] = static_cast<uint32_t>(kc::f32_to_bf16(lo)) | (static_cast<uint32_t>(kc::f32_to_bf16(hi)) << 16);
+                const float lo = __uint_as_float(w4[j] << 16), hi = __uint_as_float(w4[j] & 0xFFFF0000u);
+                if (valid)  // lo^2 + hi^2 + ss, exact products
+                    ss = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(w4[j]), as_bf16x2(w4[j]), ss, false);
+                o4[j] = kc::pack_bf16x2(__uint_as_float(g4[j] << 16) * lo,
+                                        __uint_as_float(g4[j] & 0xFFFF0000u) * hi);
             }
             xr[u] = u32x4{o4[0], o4[1], o4[2], o4[3]};
         }
+        ss = kc::wave_sum(ss);
+        if (lane == 0) part[wave] = ss;
     }
 
     // 2. stage x in LDS
@@ -321,7 +310,13 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_int4_fast_kernel(
             acc[r] = fmaf(m1, chunk_dot<XBF16>(w[r][j], xc, nk), fmaf(m2, xs, acc[r]));
         }
     }
-    const float t = wave_reduce_rows<R>(acc);
+    float t = wave_reduce_rows<R>(acc);
+    if constexpr (NORM) {
+        float tot = part[0];
+#pragma unroll
+        for (int w = 1; w < WPB; ++w) tot += part[w];
+        t *= 1.0f / sqrtf(tot / static_cast<float>(cols) + eps);
+    }
     constexpr int kGroup = kWave / R;
     const int r = lane / kGroup;
     if ((lane & (kGroup - 1)) == 0 && row0 + r < rows) store_y<YBF16>(y, row0 + r, t);
@@ -554,10 +549,12 @@ extern "C" int kc_gemv_int4_bf16(const uint8_t* d_packed, const float* d_scales,
                                  rows, cols, group_size, stream);
 }
 
-// y = W bf16(RMSNorm(h) * gamma): the RMSNorm in front of a decoder GEMV
+// y = rms_inv * (W bf16(gamma h)): the RMSNorm in front of a decoder GEMV
 // (rmsnorm.cu:40-70 followed by quant_int4.cu:126-175), folded into the
-// GEMV's staging of x.  Every workgroup sums the squares of h itself (K
-// bf16 values from the cache), so the normalized vector is never written.
+// GEMV.  Every workgroup sums the squares of h itself (K bf16 values from
+// the cache) while it stages bf16(gamma h) as x, and scales its row sums by
+// rms_inv at the end, so the normalized vector is never written and the
+// staging needs no barrier of its own.
 extern "C" int kc_rmsnorm_gemv_int4_bf16(const uint16_t* d_h, const uint16_t* d_gamma, float eps,
                                          const uint8_t* d_packed, const float* d_scales,
                                          const uint8_t* d_zeros, uint16_t* d_y, int rows, int cols,

@@ -63,9 +63,7 @@ __device__ __forceinline__ u32x4 pack(const float (&v)[Elem<BF16>::kPerSlot]) {
     uint32_t w[4];
     if constexpr (BF16) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            w[j] = static_cast<uint32_t>(kc::f32_to_bf16(v[2 * j])) |
-                   (static_cast<uint32_t>(kc::f32_to_bf16(v[2 * j + 1])) << 16);
+        for (int j = 0; j < 4; ++j) w[j] = kc::pack_bf16x2(v[2 * j], v[2 * j + 1]);
     } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) w[j] = __float_as_uint(v[j]);
