@@ -322,6 +322,128 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_int4_fast_kernel(
     if ((lane & (kGroup - 1)) == 0 && row0 + r < rows) store_y<YBF16>(y, row0 + r, t);
 }
 
+
+// ---------------------------------------------------------------------------
+// GEMV with K split across waves and x per lane (bf16, K a multiple of 2048).
+//
+// A workgroup of KW x RGW waves computes RGW groups of R rows; wave (kw, rg)
+// takes chunk c = 64 kw + lane (32 k) of each of its R rows.  A lane loads
+// its own chunk of x (64 bytes), permutes it into the decode's pair order and
+// sums it once, and reuses both for all R rows: x is never staged in LDS and
+// no barrier stands between a wave's loads and its arithmetic.  Each wave
+// reduces its R row sums across its lanes; the KW partial sums of a row meet
+// in LDS after the only barrier, at the end.  Measured against the
+// LDS-staged kernel (K 14336 down projection: 8.8 -> 8.0 us; K 4096 with
+// N <= 6144 a few per cent; K 16384 / 8192 with N 4096: 9.8 -> 8.6, 5.6 ->
+// 5.4 us); the gate/up shape (K 4096, N 28672) keeps the staged kernel.
+// With NORM, x = bf16(gamma h) and each wave adds its lanes' sums of h^2 to
+// the partials, so the row sums are scaled by rms_inv at the end.
+// ---------------------------------------------------------------------------
+template <int R, int KW, int RGW, bool NORM>
+__global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
+    const uint8_t* __restrict__ packed, const float* __restrict__ scales,
+    const uint8_t* __restrict__ zeros, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+    int rows, int cols, int gshift, const uint16_t* __restrict__ gamma, float eps) {
+    static_assert(R % 4 == 0, "rows are reduced across the wave four at a time");
+    __shared__ float part[RGW][KW][R + 1];  // row sums, then the sum of h^2
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x >> 6;
+    const int kw = wave % KW, rg = wave / KW;
+    const int row0 = (blockIdx.x * RGW + rg) * R;
+    const int c = kw * kWave + lane;  // cols == KW * 2048: every lane has a chunk
+    const int G = cols >> (5 + gshift);
+    const int g = c >> gshift;
+    const int64_t rbytes = cols >> 1;
+
+    // loads: x chunk (and gamma), then scales and zero bytes, then weights
+    const u32x4* xs = reinterpret_cast<const u32x4*>(x) + c * 4;
+    u32x4 xq[4], gq[NORM ? 4 : 1];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xq[q] = xs[q];
+    if constexpr (NORM) {
+        const u32x4* gsrc = reinterpret_cast<const u32x4*>(gamma) + c * 4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) gq[q] = gsrc[q];
+    }
+    float sv[R];
+    uint32_t zb[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t rr = min(row0 + r, rows - 1);
+        sv[r] = scales[rr * G + g];
+        zb[r] = zeros[rr * (G >> 1) + (g >> 1)];
+    }
+    u32x4 w[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t rr = min(row0 + r, rows - 1);
+        w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(packed + rr * rbytes) + c);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load above issued before any use
+
+    uint32_t sel_lo, sel_hi;  // v_perm_b32 selectors, in VGPRs
+    asm volatile("v_mov_b32 %0, 0x05040100" : "=v"(sel_lo));
+    asm volatile("v_mov_b32 %0, 0x07060302" : "=v"(sel_hi));
+    const uint32_t ones = 0x3F803F80u;
+    float hss = 0.0f;  // this lane's sum of h^2 (NORM)
+    u32x4 xp[4];
+    float xsm = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        u32x4 d = xq[q];
+        if constexpr (NORM) {
+            const uint32_t h4[4] = {d.x, d.y, d.z, d.w};
+            const uint32_t g4[4] = {gq[q].x, gq[q].y, gq[q].z, gq[q].w};
+            uint32_t o4[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                hss = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(h4[j]), as_bf16x2(h4[j]), hss, false);
+                o4[j] = kc::pack_bf16x2(__uint_as_float(g4[j] << 16) * __uint_as_float(h4[j] << 16),
+                                        __uint_as_float(g4[j] & 0xFFFF0000u) * __uint_as_float(h4[j] & 0xFFFF0000u));
+            }
+            d = u32x4{o4[0], o4[1], o4[2], o4[3]};
+        }
+        xp[q].x = __builtin_amdgcn_perm(d.z, d.x, sel_lo);  // (x0, x4)
+        xp[q].y = __builtin_amdgcn_perm(d.z, d.x, sel_hi);  // (x1, x5)
+        xp[q].z = __builtin_amdgcn_perm(d.w, d.y, sel_lo);  // (x2, x6)
+        xp[q].w = __builtin_amdgcn_perm(d.w, d.y, sel_hi);  // (x3, x7)
+        xsm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.x), as_bf16x2(ones), xsm, false);
+        xsm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.y), as_bf16x2(ones), xsm, false);
+        xsm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.z), as_bf16x2(ones), xsm, false);
+        xsm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.w), as_bf16x2(ones), xsm, false);
+    }
+    const NibConsts nk = nib_consts();
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t z = (g & 1) ? (zb[r] >> 4) : (zb[r] & 0xFu);
+        acc[r] = fmaf(sv[r], chunk_dot<true>(w[r], xp, nk), -sv[r] * static_cast<float>(136u + z) * xsm);
+    }
+#pragma unroll
+    for (int r4 = 0; r4 < R; r4 += 4) {
+        const float v4[4] = {acc[r4], acc[r4 + 1], acc[r4 + 2], acc[r4 + 3]};
+        const float t = wave_reduce_rows<4>(v4);  // lane 16 j holds row r4 + j
+        if ((lane & 15) == 0) part[rg][kw][r4 + (lane >> 4)] = t;
+    }
+    if constexpr (NORM) {
+        hss = kc::wave_sum(hss);
+        if (lane == 0) part[rg][kw][R] = hss;
+    }
+    __syncthreads();
+    if (kw == 0 && lane < R) {
+        float t = part[rg][0][lane];
+#pragma unroll
+        for (int k = 1; k < KW; ++k) t += part[rg][k][lane];
+        if constexpr (NORM) {
+            float ss = part[rg][0][R];
+#pragma unroll
+            for (int k = 1; k < KW; ++k) ss += part[rg][k][R];
+            t *= 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+        }
+        if (row0 + lane < rows) y[row0 + lane] = kc::f32_to_bf16(t);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Dequantization to fp32 (quant_int4.cu:68-105): exactly one fp32 rounding,
 // (float)(sext4(q) - z) * s.
@@ -449,6 +571,39 @@ void launch_fast_cpl(int slot, const GemvArgs& a, int rows, int cols, int gshift
         launch_fast<R, CPL, 64, WPB, XB, YB, NORM>(a, rows, cols, gshift, lds, stream);
 }
 
+// The per-lane-x kernel for bf16 GEMVs whose K is 2048 x KW (KW 2..8):
+// R = 4 rows per wave (8 for KW >= 3 with N >= 16384), two row groups per
+// workgroup at KW = 2; at KW = 2 only up to N = 16384 (the staged kernel is
+// as fast or faster on the larger K = 4096 shapes).  False when it does not
+// apply.
+template <bool NORM>
+bool launch_xl(const GemvArgs& a, int64_t rows, int64_t cols, int gshift, hipStream_t stream) {
+    if (cols % 2048 != 0 || rows > INT32_MAX) return false;
+    const int kw = static_cast<int>(cols / 2048);
+    if (kw < 2 || kw > 8 || (kw == 2 && rows > 16384)) return false;
+    const int r = static_cast<int>(rows), c = static_cast<int>(cols);
+    const bool wide = kw >= 3 && rows >= 16384;
+    const auto* xp = static_cast<const uint16_t*>(a.x);
+    auto* yp = static_cast<uint16_t*>(a.y);
+#define KC_XL(KWV, RV, RGWV)                                                                     \
+    gemv_int4_xl_kernel<RV, KWV, RGWV, NORM><<<static_cast<unsigned>((r + RV * RGWV - 1) / (RV * RGWV)), \
+                                               KWV * RGWV * kWave, 0, stream>>>(                 \
+        a.packed, a.scales, a.zeros, xp, yp, r, c, gshift, a.gamma, a.eps)
+#define KC_XL_CASE(KWV)                  \
+    case KWV:                            \
+        if (wide) KC_XL(KWV, 8, 1);      \
+        else KC_XL(KWV, 4, 1);           \
+        break;
+    switch (kw) {
+        case 2: KC_XL(2, 4, 2); break;
+        KC_XL_CASE(3) KC_XL_CASE(4) KC_XL_CASE(5) KC_XL_CASE(6) KC_XL_CASE(7) KC_XL_CASE(8)
+        default: return false;
+    }
+#undef KC_XL_CASE
+#undef KC_XL
+    return true;
+}
+
 template <bool XB, bool YB, bool NORM = false>
 int gemv_int4(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
               const void* x, void* y, int64_t rows, int64_t cols, int64_t gs,
@@ -468,6 +623,9 @@ int gemv_int4(const char* fn, const uint8_t* packed, const float* scales, const 
                       (!NORM || kc::aligned(gamma, 16)) &&
                       lds <= static_cast<size_t>(device_max_lds());
     const GemvArgs a{packed, scales, zeros, x, y, gamma, eps};
+    if constexpr (XB && YB) {
+        if (fast && launch_xl<NORM>(a, rows, cols, kc::ilog2(gs) - 5, stream)) return kc::check_launch(fn);
+    }
     if (fast) {
         const int gshift = kc::ilog2(gs) - 5;
         const int slot = gshift >= 2 ? 16 : 64;

@@ -213,7 +213,12 @@ def test_gemv_bf16_llama_shapes(gpu, oracle, rows, cols):
     assert rel_l2(y, truth) < 3e-3
 
 
-@pytest.mark.parametrize("rows,cols,gs", [(5, 96, 32), (3, 100, 10), (70, 2048, 64)])
+@pytest.mark.parametrize("rows,cols,gs", [(5, 96, 32), (3, 100, 10), (70, 2048, 64),
+                                           # K = 2048 x KW, x per lane: 4 or 8 rows per
+                                           # wave, ragged row counts, groups 32..256
+                                           (1000, 8192, 128), (20000, 6144, 64),
+                                           (17, 16384, 256), (4099, 10240, 32),
+                                           (16384, 4096, 128), (16385, 4096, 128)])
 def test_gemv_bf16_other_shapes(gpu, oracle, rows, cols, gs):
     packed, scales, zeros = make_int4(rows, cols, gs, seed=rows + cols)
     xb = normal_bf16(cols, seed=cols)

@@ -116,12 +116,14 @@ def _fused(torch, packed, scales, zeros, hb, gb, rows, cols, gs, eps=1e-5, gamma
 
 
 @pytest.mark.parametrize("rows,cols,gs,goff", [(6144, 4096, 128, 0), (512, 14336, 128, 0),
+                                               (20000, 8192, 128, 0), (28672, 4096, 128, 0),
                                                (300, 20480, 128, 0), (77, 1024, 64, 0),
                                                (33, 2080, 32, 0), (40, 384, 128, 1),
                                                (16, 96, 24, 0)])
 def test_rmsnorm_gemv_fused(gpu, oracle, rows, cols, gs, goff):
-    """Fast path (K up to 16384 and beyond, groups of 32..128), and the
-    generic path (unaligned gamma, groups that are not a power of two)."""
+    """The per-lane-x kernel (K = 2048 x 2..8), the LDS-staged kernel (gate/up,
+    K 20480, small K), and the generic path (unaligned gamma, groups that are
+    not a power of two)."""
     packed, scales, zeros = make_int4(rows, cols, gs, seed=rows + cols)
     rng = np.random.default_rng(cols)
     hb = f32_to_bf16_bits(rng.standard_normal(cols).astype(np.float32) * 4)
