@@ -25,9 +25,19 @@
 // exactly as the GEMV does.  Groups smaller than 128 fall back to the GEMV
 // per activation row.
 //
-// Work split.  A workgroup of NW waves owns 16*RT*NW consecutive weight rows
-// and the whole K; wave w owns row tiles w*RT .. w*RT+RT-1.  K is walked in
-// chunks of TPC T-blocks, software pipelined:
+// Kernels, by M (kc_gemm_int4_bf16 at the bottom picks one):
+//   M 2..16   gemm_int4_xres_kernel: X resident in LDS, one wave per 16-row
+//             weight tile over all of K;
+//   M 17..64  gemm_int4_kslice_kernel: K split over the four waves of a CU,
+//             X from the cache into registers;
+//   fallbacks gemm_int4_xbig_kernel (M 33..64) and gemm_int4_mfma_kernel
+//             (below) when the K-split kernel's coefficients do not fit in
+//             LDS (K above about 20000).
+//
+// gemm_int4_mfma_kernel work split.  A workgroup of NW waves owns
+// 16*RT*NW consecutive weight rows and the whole K; wave w owns row tiles
+// w*RT .. w*RT+RT-1.  K is walked in chunks of TPC T-blocks, software
+// pipelined:
 //   * X of the next chunk is loaded, rearranged into the B-operand layout
 //     (with its T-block sums) and written to the other half of a
 //     double-buffered LDS area, together with that chunk's fold coefficients
@@ -675,7 +685,8 @@ int launch_xres(const char* fn, const uint8_t* packed, const float* scales, cons
 }
 
 // ---------------------------------------------------------------------------
-// M 33..64: X resident in LDS, four activation tiles.  Each wave owns RT
+// M 33..64 when the K-split kernel below does not apply (K above about
+// 20000): X resident in LDS, four activation tiles.  Each wave owns RT
 // 16-row weight tiles (consecutive) over the whole of K and every
 // activation row: per T-block it decodes each tile's A operands once and
 // runs them against the MT = 4 activation tiles' B operands from LDS (each

@@ -14,7 +14,8 @@
 // n' = q ^ 8 = sext4(q) + 8 in [0, 15]:
 //     sum_k W x = s * (sum_k n' x - (8 + z) * sum_k x)        per chunk
 // The per-chunk sum of x is computed once per workgroup while x is staged in
-// LDS.  With bf16 x each nibble becomes the exact bf16 (128 + n') by one
+// LDS (gemv_int4_fast_kernel), or once per lane for the one chunk it owns
+// (gemv_int4_xl_kernel, bf16 with K = 2048 x 2..8: no LDS staging).  With bf16 x each nibble becomes the exact bf16 (128 + n') by one
 // bitwise op, ((d ^ 0x00080008) & 0x000F000F) | 0x43004300 (v_bitop3_b32), and
 // pairs of them meet pairs of x in v_dot2_f32_bf16 (exact products, fp32
 // accumulation); the extra 128 * sum x is removed with the zero point.  With
