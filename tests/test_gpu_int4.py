@@ -218,7 +218,8 @@ def test_gemv_bf16_llama_shapes(gpu, oracle, rows, cols):
                                            # wave, ragged row counts, groups 32..256
                                            (1000, 8192, 128), (20000, 6144, 64),
                                            (17, 16384, 256), (4099, 10240, 32),
-                                           (16384, 4096, 128), (16385, 4096, 128)])
+                                           (16384, 4096, 128), (16385, 4096, 128),
+                                           (100, 8192, 512), (9, 4096, 2048)])
 def test_gemv_bf16_other_shapes(gpu, oracle, rows, cols, gs):
     packed, scales, zeros = make_int4(rows, cols, gs, seed=rows + cols)
     xb = normal_bf16(cols, seed=cols)
@@ -291,7 +292,7 @@ def test_gemm_cfg3(gpu, oracle, m):
                                             (48, 200, 8192, 128), (20, 224, 4096, 128),
                                             (32, 1000, 4096, 128), (40, 113, 16384, 128),
                                             (17, 7, 256, 256), (63, 1, 512, 128),
-                                            (26, 130, 1152, 128),
+                                            (26, 130, 1152, 128), (40, 200, 4096, 512),
                                             # M 33..64 whose coefficients do not fit
                                             # in LDS: the X-resident fallback
                                             (64, 50, 24576, 128)])
