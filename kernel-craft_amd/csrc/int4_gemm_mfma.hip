@@ -463,8 +463,8 @@ int launch_mfma(const char* fn, const uint8_t* packed, const float* scales, cons
 // workgroup per CU at N = 28672.
 //
 // LDS: X slots [T of the phase][step w4][m][kb] (16 bytes each), X sums
-// [T of the phase][m] (padded to 16 bytes), then per wave cs[16 rows][g],
-// cz[16 rows][g].
+// [T of the phase][m] (padded to 16 bytes), then per wave cs[g][16 rows],
+// cz[g][16 rows].
 // ---------------------------------------------------------------------------
 constexpr int kXresMaxM = 16;
 
@@ -522,7 +522,7 @@ __global__ __launch_bounds__(W * kWave) void gemm_int4_xres_kernel(
     // one memory round trip; (idx + 0.5) / ppr in fp32 gives the row exactly
     // (idx < 2^24, and the quotient is never within 0.5 / ppr of an integer).
     // With the first phase the wave also stages its coefficients,
-    // cs[row][g] = s, cz[row][g] = -s * (136 + z) (16 rows per lane, lane
+    // cs[g][row] = s, cz[g][row] = -s * (136 + z) (16 rows per lane, lane
     // g + 64 j of each row), and fills its weight ring.
     constexpr int kXBatch = 10;  // 4480 pieces per pass: M 16 x 2048 k, or M 4 x 8192 k
     const int ppr = nTp * 16;                       // X pieces per row and phase
@@ -555,8 +555,8 @@ __global__ __launch_bounds__(W * kWave) void gemm_int4_xres_kernel(
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
                             const uint32_t z = (g & 1) ? (zb[r] >> 4) : (zb[r] & 0xFu);
-                            cs[r * G + g] = sv[r];  // [row][g]: consecutive lanes, consecutive words
-                            cz[r * G + g] = -sv[r] * static_cast<float>(136u + z);
+                            cs[g * 16 + r] = sv[r];  // [g][row]: a lane's 4 rows are one 16-byte read
+                            cz[g * 16 + r] = -sv[r] * static_cast<float>(136u + z);
                         }
                     }
                 }
@@ -599,7 +599,9 @@ __global__ __launch_bounds__(W * kWave) void gemm_int4_xres_kernel(
     // Stream the weights: T-block T's four MFMA steps with X from LDS,
     // folded into acc (rows 4 kb + v of the tile, activation row i).
     const NibConsts nk = nib_consts();
-    const bool xlane = i < M;
+    // lanes of activation rows past M read row M - 1: their output columns
+    // are never stored, and no branch or zero fill is needed per T-block
+    const int ib = min(i, M - 1);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int ph = 0; ph < P; ++ph) {
         for (int T0 = ph * nTp; T0 < (ph + 1) * nTp; T0 += D) {
@@ -608,20 +610,13 @@ __global__ __launch_bounds__(W * kWave) void gemm_int4_xres_kernel(
                 const int T = T0 + u;
                 const int Tl = T - ph * nTp;
                 bf16x8_t b[4];
-                float xs = 0.0f;
 #pragma unroll
-                for (int w4 = 0; w4 < 4; ++w4) b[w4] = bf16x8_t{};
-                if (xlane) {
-#pragma unroll
-                    for (int w4 = 0; w4 < 4; ++w4)
-                        b[w4] = __builtin_bit_cast(bf16x8_t, xslot[((Tl * 4 + w4) * M + i) * 4 + kb]);
-                    xs = xsum[Tl * M + i];
-                }
+                for (int w4 = 0; w4 < 4; ++w4)
+                    b[w4] = __builtin_bit_cast(bf16x8_t, xslot[((Tl * 4 + w4) * M + ib) * 4 + kb]);
+                const float xs = xsum[Tl * M + ib];
                 const int g = T >> gshift;
-                const float* cr = cs + 4 * kb * G + g;  // rows 4 kb .. 4 kb + 3
-                const float* zr = cz + 4 * kb * G + g;
-                const f32x4 s4 = {cr[0], cr[G], cr[2 * G], cr[3 * G]};
-                const f32x4 z4 = {zr[0], zr[G], zr[2 * G], zr[3 * G]};
+                const f32x4 s4 = *reinterpret_cast<const f32x4*>(cs + g * 16 + 4 * kb);  // rows 4 kb .. 4 kb + 3
+                const f32x4 z4 = *reinterpret_cast<const f32x4*>(cz + g * 16 + 4 * kb);
                 const u32x4 wv = w[u];
                 f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_operand(wv.x, nk), b[0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_operand(wv.y, nk), b[1], d, 0, 0, 0);
@@ -643,7 +638,7 @@ __global__ __launch_bounds__(W * kWave) void gemm_int4_xres_kernel(
     }
 
     // lane (i, kb) holds Y[m = i][n = row0 + 4 kb + v]
-    if (owner && xlane) {
+    if (owner && i < M) {
         const float vals[4] = {acc.x, acc.y, acc.z, acc.w};
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
