@@ -26,13 +26,13 @@
 // per activation row.
 //
 // Kernels, by M (kc_gemm_int4_bf16 at the bottom picks one):
-//   M 2..16   gemm_int4_xres_kernel: X resident in LDS, one wave per 16-row
+//   M 2..8    gemm_int4_xres_kernel: X resident in LDS, one wave per 16-row
 //             weight tile over all of K;
-//   M 17..64  gemm_int4_kslice_kernel: K split over the four waves of a CU,
+//   M 9..64   gemm_int4_kslice_kernel: K split over the four waves of a CU,
 //             X from the cache into registers;
-//   fallbacks gemm_int4_xbig_kernel (M 33..64) and gemm_int4_mfma_kernel
-//             (below) when the K-split kernel's coefficients do not fit in
-//             LDS (K above about 20000).
+//   fallbacks gemm_int4_xres_kernel (M 9..16), gemm_int4_xbig_kernel
+//             (M 33..64) and gemm_int4_mfma_kernel (below) when the K-split
+//             kernel's coefficients do not fit in LDS (K above about 20000).
 //
 // gemm_int4_mfma_kernel work split.  A workgroup of NW waves owns
 // 16*RT*NW consecutive weight rows and the whole K; wave w owns row tiles
@@ -466,7 +466,8 @@ int launch_mfma(const char* fn, const uint8_t* packed, const float* scales, cons
 // [T of the phase][m] (padded to 16 bytes), then per wave cs[g][16 rows],
 // cz[g][16 rows].
 // ---------------------------------------------------------------------------
-constexpr int kXresMaxM = 16;
+constexpr int kXresMaxM = 16;  // the kernel's limit; kc_gemm_int4_bf16 uses it up to kXresBestM
+constexpr int kXresBestM = 8;  // M 9..16 are faster on the K-split kernel (K 8192, N 28672: M 12 35.9 against 37.6 us, M 16 37.4 against 41.0)
 
 // Sum over each 16-lane row of the wave with DPP rotations (VALU only).
 template <int CTRL>
@@ -1214,26 +1215,34 @@ extern "C" int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
         return KC_SUCCESS;
     }
     const int gshift = kc::ilog2(group_size) - 7;
-    // M <= 16: the X-resident kernel when its LDS fits in some number of
+    // M <= 8: the X-resident kernel when its LDS fits in some number of
     // phases of K.
-    if (m <= kXresMaxM) {
+    if (m <= kXresBestM) {
         const int P = xres_phases(m, cols, (cols / kTBlock) >> gshift);
         if (P > 0)
             return launch_xres<kXresW, kXresD>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols,
                                                gshift, P, stream);
     }
-    // M 17..64: the K-split kernel (K 8192, N 28672, MI355X: M 32 / 48 / 64
-    // in 47 / 57 / 68 us, against 77 / 95 / 101 us for the kernels below,
-    // which remain for shapes it does not take: K above about 20000, where
-    // its coefficient stage does not fit in LDS, or operands of 4 GiB).
-    if (m > kXresMaxM) {
+    // M 9..64: the K-split kernel (K 8192, N 28672, MI355X: M 16 / 32 / 48 /
+    // 64 in 37 / 47 / 57 / 68 us, against 41 / 77 / 95 / 101 us for the
+    // kernels below, which remain for shapes it does not take: K above about
+    // 20000, where its coefficient stage does not fit in LDS, or operands of
+    // 4 GiB).
+    if (m > kXresBestM) {
         int st = -1;
         switch ((m + 15) / 16) {
+            case 1: st = launch_kslice<1>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
             case 2: st = launch_kslice<2>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
             case 3: st = launch_kslice<3>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
             default: st = launch_kslice<4>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
         }
         if (st >= 0) return st;
+    }
+    if (m <= kXresMaxM) {
+        const int P = xres_phases(m, cols, (cols / kTBlock) >> gshift);
+        if (P > 0)
+            return launch_xres<kXresW, kXresD>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols,
+                                               gshift, P, stream);
     }
     // M 33..64: the four-tile X-resident kernel when its LDS fits (K 8192,
     // N 28672: M 33 / 48 / 64 in 86 / 90 / 94 us against 105 / 119 / 125 us

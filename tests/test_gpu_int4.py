@@ -279,11 +279,13 @@ def test_gemm_cfg3(gpu, oracle, m):
                                             (4, 7 * 16 * 3 + 5, 2048, 512),
                                             # M <= 4 whose X does not fit in LDS
                                             (4, 33, 32768, 128),
-                                            # M 5..16: X in LDS in one, two and four
-                                            # phases of K
+                                            # M 5..8: X in LDS in one, two and four
+                                            # phases of K; M 9..16 on the K-split
+                                            # kernel, or past its LDS on the chunked one
                                             (16, 48, 1024, 128), (8, 300, 4096, 128),
                                             (12, 257, 2048, 256), (16, 100, 8192, 128),
-                                            (6, 7 * 16 + 1, 8192, 512),
+                                            (6, 7 * 16 + 1, 8192, 512), (8, 500, 8192, 128),
+                                            (12, 100, 24576, 128), (9, 40, 2048, 256),
                                             # M 17..64, K split over four waves:
                                             # ragged rows and activation tiles,
                                             # waves with no T-block (K < 512),
