@@ -958,8 +958,9 @@ __device__ __forceinline__ float swap16_sum(float a) {
 
 // LDS: the coefficients cs[t][row], cz[t][row] of every wave's K range, later
 // reused for the cross-wave sum (one f32x4 per lane, tile and wave).
-__host__ __device__ constexpr size_t kslice_lds_bytes(int MT, int RT, int nT) {
-    const size_t coef = static_cast<size_t>(kKsWaves) * ((nT + kKsWaves - 1) / kKsWaves) * 16 * RT * 8;
+// (a wave's range rounded up to whole ring turns of D T-blocks)
+__host__ __device__ constexpr size_t kslice_lds_bytes(int MT, int RT, int D, int nT) {
+    const size_t coef = static_cast<size_t>(kKsWaves) * (((nT + kKsWaves - 1) / kKsWaves + D - 1) / D * D) * 16 * RT * 8;
     const size_t red = static_cast<size_t>(kKsWaves) * RT * MT * kWave * 16;
     return coef > red ? coef : red;
 }
@@ -976,9 +977,10 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslice_kernel(
     const int i = lane & 15, kb = lane >> 4;
     const int nT = K / kTBlock;
     const int G = nT >> gshift;
-    const int ntmax = (nT + kKsWaves - 1) / kKsWaves;
+    const int ntmax = ((nT + kKsWaves - 1) / kKsWaves + D - 1) / D * D;  // whole ring turns
     const int t0 = (wave * nT) / kKsWaves, t1 = ((wave + 1) * nT) / kKsWaves;
     const int nt = t1 - t0;  // 0 for some waves when nT < 4
+    const int ntp = (nt + D - 1) / D * D;  // the loop's T-blocks: nt, padded to whole ring turns
     const int tl = max(t1 - 1, 0);
     const int row_base = blockIdx.x * kRows;
     float* cs = reinterpret_cast<float*>(lds) + static_cast<size_t>(wave) * ntmax * kRows * 2;
@@ -1049,6 +1051,11 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslice_kernel(
                 }
             }
         }
+        // padding T-blocks fold with zero coefficients
+        for (int idx = nt * kRows + lane; idx < ntp * kRows; idx += kWave) {
+            cs[idx] = 0.0f;
+            cz[idx] = 0.0f;
+        }
     }
     __syncthreads();
 
@@ -1065,13 +1072,13 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslice_kernel(
 
     // A whole number of ring turns, so the body has no branch (a guarded
     // iteration would make the compiler's load-count waits conservative):
-    // padding T-blocks past the range reload the last one and fold with 0.
-    const int tend = t0 + ((nt + D - 1) / D) * D;
+    // padding T-blocks past the range reload the last one and fold with the
+    // zero coefficients staged for them.
+    const int tend = t0 + ntp;
     for (int T0 = t0; T0 < tend; T0 += D) {
 #pragma unroll
         for (int u = 0; u < D; ++u) {
             const int T = T0 + u;
-            const bool live = T < t1;
             // B operands in pair order, and the T-block sums of X: lane
             // (i, kb) sums its 32 values, the four kb lanes are added with
             // permlane swaps.
@@ -1100,19 +1107,15 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslice_kernel(
             for (int c = 0; c < MT; ++c)
 #pragma unroll
                 for (int s = 0; s < 4; ++s) xb[c][s] = xload(c, T + 1, s);
-            const int tt = min(T, tl) - t0;
+            const int tt = T - t0;
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
                 const u32x4 wv = wr[u][rt];
                 const bf16x8_t a0 = a_operand(wv.x, nk), a1 = a_operand(wv.y, nk);
                 const bf16x8_t a2 = a_operand(wv.z, nk), a3 = a_operand(wv.w, nk);
                 wr[u][rt] = wload(rt, T + D);
-                f32x4 s4 = *reinterpret_cast<const f32x4*>(cs + tt * kRows + 16 * rt + 4 * kb);
-                f32x4 z4 = *reinterpret_cast<const f32x4*>(cz + tt * kRows + 16 * rt + 4 * kb);
-                if (!live) {
-                    s4 = f32x4{0.f, 0.f, 0.f, 0.f};
-                    z4 = s4;
-                }
+                const f32x4 s4 = *reinterpret_cast<const f32x4*>(cs + tt * kRows + 16 * rt + 4 * kb);
+                const f32x4 z4 = *reinterpret_cast<const f32x4*>(cz + tt * kRows + 16 * rt + 4 * kb);
 #pragma unroll
                 for (int c = 0; c < MT; ++c) {
                     f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[c][0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
@@ -1168,7 +1171,7 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslice_kernel(
 template <int MT>
 int launch_kslice(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
                   const uint16_t* X, uint16_t* Y, int M, int N, int K, int gshift, hipStream_t stream) {
-    const size_t lds = kslice_lds_bytes(MT, kKsRT, K / kTBlock);
+    const size_t lds = kslice_lds_bytes(MT, kKsRT, kKsD, K / kTBlock);
     if (lds > 160 * 1024 || static_cast<uint64_t>(N) * (K / 2) >= (uint64_t{1} << 32) ||
         static_cast<uint64_t>(M) * K * 2 >= (uint64_t{1} << 32))
         return -1;
