@@ -527,14 +527,19 @@ int check_int4_args(const char* fn, const void* packed, const void* scales, cons
     return KC_SUCCESS;
 }
 
+// The staged kernel's LDS ceiling: all of a CU's 160 KB.  Beyond the 64 KB a
+// launch gets by default (fp32 x at K > 15872) the kernel is opted in once.
+constexpr int kDefaultLds = 64 * 1024;
+constexpr int kMaxFastLds = 160 * 1024;
+
 int device_max_lds() {
     static const int v = [] {
         int dev = 0, lds = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
             lds <= 0)
-            lds = 65536;
-        return std::min(lds, 65536);
+            lds = kDefaultLds;
+        return std::min(lds, kMaxFastLds);
     }();
     return v;
 }
@@ -551,25 +556,45 @@ struct GemvArgs {
     float eps;
 };
 
+// False (nothing launched) when the kernel cannot be given the LDS it needs.
 template <int R, int CPL, int SLOT, int WPB, bool XB, bool YB, bool NORM>
-void launch_fast(const GemvArgs& a, int rows, int cols, int gshift, size_t lds, hipStream_t stream) {
+bool launch_fast(const GemvArgs& a, int rows, int cols, int gshift, size_t lds, hipStream_t stream) {
+    const auto kernel = gemv_int4_fast_kernel<R, CPL, SLOT, WPB, XB, YB, NORM>;
+    if (lds > static_cast<size_t>(kDefaultLds)) {
+        static const bool opted_in = [&] {
+            const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                kMaxFastLds) == hipSuccess;
+            if (!ok) (void)hipGetLastError();  // the caller takes another kernel
+            return ok;
+        }();
+        if (!opted_in) return false;
+    }
     const int wave_blocks = (rows + R - 1) / R;
     const unsigned grid = static_cast<unsigned>((wave_blocks + WPB - 1) / WPB);
-    gemv_int4_fast_kernel<R, CPL, SLOT, WPB, XB, YB, NORM><<<grid, WPB * kWave, lds, stream>>>(
-        a.packed, a.scales, a.zeros, a.x, a.y, rows, cols, gshift, a.gamma, a.eps);
+    kernel<<<grid, WPB * kWave, lds, stream>>>(a.packed, a.scales, a.zeros, a.x, a.y, rows, cols,
+                                               gshift, a.gamma, a.eps);
+    return true;
 }
 
 // Rows per wave and waves per workgroup: 2 rows and 4 waves up to K = 16384
-// (at most 8 weight chunks per row and lane); 1 row and 8 waves beyond.
+// (at most 8 weight chunks per row and lane), 1 row and 8 waves beyond; 4 rows
+// when each lane holds 2 or 4 whole chunks per row and N is large enough
+// (K = 4096 from N = 4096, K = 8192 from N = 8192) -- measured 4-26 % faster
+// there (gate/up 13.0 -> 11.8 us), and 2-20 % slower at N <= 1024 or with a
+// part-filled chunk (K = 5120, 14336).
 template <int CPL, bool XB, bool YB, bool NORM>
-void launch_fast_cpl(int slot, const GemvArgs& a, int rows, int cols, int gshift, size_t lds,
+bool launch_fast_cpl(int slot, const GemvArgs& a, int rows, int cols, int gshift, size_t lds,
                      hipStream_t stream) {
     constexpr int R = CPL <= 8 ? 2 : 1;
     constexpr int WPB = CPL <= 8 ? 4 : 8;
-    if (slot == 16)
-        launch_fast<R, CPL, 16, WPB, XB, YB, NORM>(a, rows, cols, gshift, lds, stream);
-    else
-        launch_fast<R, CPL, 64, WPB, XB, YB, NORM>(a, rows, cols, gshift, lds, stream);
+    if constexpr (CPL == 2 || CPL == 4) {
+        const bool four = cols == CPL * 2048 && rows >= CPL * 2048;
+        if (four && slot == 16) return launch_fast<4, CPL, 16, 4, XB, YB, NORM>(a, rows, cols, gshift, lds, stream);
+        if (four) return launch_fast<4, CPL, 64, 4, XB, YB, NORM>(a, rows, cols, gshift, lds, stream);
+    }
+    if (slot == 16) return launch_fast<R, CPL, 16, WPB, XB, YB, NORM>(a, rows, cols, gshift, lds, stream);
+    return launch_fast<R, CPL, 64, WPB, XB, YB, NORM>(a, rows, cols, gshift, lds, stream);
 }
 
 // The per-lane-x kernel for bf16 GEMVs whose K is 2048 x KW (KW 2..8):
@@ -627,13 +652,14 @@ int gemv_int4(const char* fn, const uint8_t* packed, const float* scales, const 
     if constexpr (XB && YB) {
         if (fast && launch_xl<NORM>(a, rows, cols, kc::ilog2(gs) - 5, stream)) return kc::check_launch(fn);
     }
+    bool launched = false;
     if (fast) {
         const int gshift = kc::ilog2(gs) - 5;
         const int slot = gshift >= 2 ? 16 : 64;
         const int r = static_cast<int>(rows), c = static_cast<int>(cols);
-#define KC_FAST_CASE(N)                                                            \
-    case N:                                                                        \
-        launch_fast_cpl<N, XB, YB, NORM>(slot, a, r, c, gshift, lds, stream);      \
+#define KC_FAST_CASE(N)                                                                   \
+    case N:                                                                               \
+        launched = launch_fast_cpl<N, XB, YB, NORM>(slot, a, r, c, gshift, lds, stream);  \
         break;
         switch (cpl) {
             KC_FAST_CASE(1) KC_FAST_CASE(2) KC_FAST_CASE(3) KC_FAST_CASE(4)
@@ -643,7 +669,8 @@ int gemv_int4(const char* fn, const uint8_t* packed, const float* scales, const 
             default: break;
         }
 #undef KC_FAST_CASE
-    } else {
+    }
+    if (!launched) {
         const int64_t grid = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
         if (grid > INT32_MAX)
             return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: rows=%lld too large", fn,

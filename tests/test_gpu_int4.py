@@ -126,6 +126,22 @@ def test_gemv_f32_shapes(gpu, oracle, rows, cols, gs):
     assert rel_l2(y, truth) < TOL_F32
 
 
+# Staged-kernel variants: 4 rows per wave (K = 4096 from N = 4096, K = 8192
+# from N = 8192; ragged N, 16- and 64-lane slot maps) and x beyond 64 KB of
+# LDS (fp32 x at K > 15872, up to the 160 KB of K = 32768).
+F32_STAGED_SHAPES = [(4096, 4096, 32), (4099, 4096, 64), (8192, 8192, 128), (8200, 8192, 32),
+                     (40, 16384, 128), (33, 20480, 64), (9, 32768, 128), (5, 31744, 32)]
+
+
+@pytest.mark.parametrize("rows,cols,gs", F32_STAGED_SHAPES)
+def test_gemv_f32_staged_variants(gpu, oracle, rows, cols, gs):
+    packed, scales, zeros = make_int4(rows, cols, gs, seed=rows * 5 + cols)
+    x = np.random.default_rng(cols + 1).standard_normal(cols).astype(np.float32)
+    y = _gemv_f32(gpu, packed, scales, zeros, x, rows, cols, gs)
+    truth = oracle.gemv_int4_f64(packed, scales, zeros.reshape(-1), x, rows, cols, gs)
+    assert rel_l2(y, truth) < TOL_F32
+
+
 @pytest.mark.parametrize("rows,cols,gs", SHAPES)
 def test_dequant_shapes_bit_exact(gpu, oracle, rows, cols, gs):
     packed, scales, zeros = make_int4(rows, cols, gs, seed=rows * 3 + cols)
@@ -219,7 +235,8 @@ def test_gemv_bf16_llama_shapes(gpu, oracle, rows, cols):
                                            (1000, 8192, 128), (20000, 6144, 64),
                                            (17, 16384, 256), (4099, 10240, 32),
                                            (16384, 4096, 128), (16385, 4096, 128),
-                                           (100, 8192, 512), (9, 4096, 2048)])
+                                           (100, 8192, 512), (9, 4096, 2048),
+                                           (20480, 4096, 32), (16392, 4096, 256)])
 def test_gemv_bf16_other_shapes(gpu, oracle, rows, cols, gs):
     packed, scales, zeros = make_int4(rows, cols, gs, seed=rows + cols)
     xb = normal_bf16(cols, seed=cols)

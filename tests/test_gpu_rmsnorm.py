@@ -117,6 +117,7 @@ def _fused(torch, packed, scales, zeros, hb, gb, rows, cols, gs, eps=1e-5, gamma
 
 @pytest.mark.parametrize("rows,cols,gs,goff", [(6144, 4096, 128, 0), (512, 14336, 128, 0),
                                                (20000, 8192, 128, 0), (28672, 4096, 128, 0),
+                                               (17000, 4096, 32, 0),
                                                (300, 20480, 128, 0), (77, 1024, 64, 0),
                                                (33, 2080, 32, 0), (40, 384, 128, 1),
                                                (16, 96, 24, 0)])
