@@ -15,7 +15,7 @@
 //     sum_k W x = s * (sum_k n' x - (8 + z) * sum_k x)        per chunk
 // The per-chunk sum of x is computed once per workgroup while x is staged in
 // LDS (gemv_int4_fast_kernel), or once per lane for the one chunk it owns
-// (gemv_int4_xl_kernel, bf16 with K = 2048 x 2..8: no LDS staging).  With bf16 x each nibble becomes the exact bf16 (128 + n') by one
+// (gemv_int4_xl_kernel, K = 2048 x 2..8: no LDS staging).  With bf16 x each nibble becomes the exact bf16 (128 + n') by one
 // bitwise op, ((d ^ 0x00080008) & 0x000F000F) | 0x43004300 (v_bitop3_b32), and
 // pairs of them meet pairs of x in v_dot2_f32_bf16 (exact products, fp32
 // accumulation); the extra 128 * sum x is removed with the zero point.  With
@@ -340,12 +340,14 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_int4_fast_kernel(
 // With NORM, x = bf16(gamma h) and each wave adds its lanes' sums of h^2 to
 // the partials, so the row sums are scaled by rms_inv at the end.
 // ---------------------------------------------------------------------------
-template <int R, int KW, int RGW, bool NORM>
+template <int R, int KW, int RGW, bool NORM, bool BF16 = true>
 __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
     const uint8_t* __restrict__ packed, const float* __restrict__ scales,
-    const uint8_t* __restrict__ zeros, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+    const uint8_t* __restrict__ zeros, const void* __restrict__ x, void* __restrict__ y,
     int rows, int cols, int gshift, const uint16_t* __restrict__ gamma, float eps) {
     static_assert(R % 4 == 0, "rows are reduced across the wave four at a time");
+    static_assert(BF16 || !NORM, "the fused RMSNorm takes bf16 x");
+    constexpr int kXQ = BF16 ? 4 : 8;  // 16-byte quads of x per 32-k chunk
     __shared__ float part[RGW][KW][R + 1];  // row sums, then the sum of h^2
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x >> 6;
@@ -357,10 +359,10 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
     const int64_t rbytes = cols >> 1;
 
     // loads: x chunk (and gamma), then scales and zero bytes, then weights
-    const u32x4* xs = reinterpret_cast<const u32x4*>(x) + c * 4;
-    u32x4 xq[4], gq[NORM ? 4 : 1];
+    const u32x4* xs = static_cast<const u32x4*>(x) + c * kXQ;
+    u32x4 xq[kXQ], gq[NORM ? 4 : 1];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) xq[q] = xs[q];
+    for (int q = 0; q < kXQ; ++q) xq[q] = xs[q];
     if constexpr (NORM) {
         const u32x4* gsrc = reinterpret_cast<const u32x4*>(gamma) + c * 4;
 #pragma unroll
@@ -390,7 +392,7 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
     u32x4 xp[4];
     float xsm = 0.0f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < (BF16 ? 4 : 0); ++q) {
         u32x4 d = xq[q];
         if constexpr (NORM) {
             const uint32_t h4[4] = {d.x, d.y, d.z, d.w};
@@ -413,12 +415,20 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
         xsm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.z), as_bf16x2(ones), xsm, false);
         xsm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.w), as_bf16x2(ones), xsm, false);
     }
+    if constexpr (!BF16) {  // fp32 x: raw order, offset 8 (dot8_f32)
+#pragma unroll
+        for (int q = 0; q < kXQ; ++q)
+            xsm += (__uint_as_float(xq[q].x) + __uint_as_float(xq[q].y)) +
+                   (__uint_as_float(xq[q].z) + __uint_as_float(xq[q].w));
+    }
     const NibConsts nk = nib_consts();
+    constexpr float kOff = BF16 ? 136.0f : 8.0f;
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t z = (g & 1) ? (zb[r] >> 4) : (zb[r] & 0xFu);
-        acc[r] = fmaf(sv[r], chunk_dot<true>(w[r], xp, nk), -sv[r] * static_cast<float>(136u + z) * xsm);
+        const float dot = BF16 ? chunk_dot<true>(w[r], xp, nk) : chunk_dot<false>(w[r], xq, nk);
+        acc[r] = fmaf(sv[r], dot, -sv[r] * (kOff + static_cast<float>(z)) * xsm);
     }
 #pragma unroll
     for (int r4 = 0; r4 < R; r4 += 4) {
@@ -441,7 +451,7 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
             for (int k = 1; k < KW; ++k) ss += part[rg][k][R];
             t *= 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
         }
-        if (row0 + lane < rows) y[row0 + lane] = kc::f32_to_bf16(t);
+        if (row0 + lane < rows) store_y<BF16>(y, row0 + lane, t);
     }
 }
 
@@ -597,24 +607,26 @@ bool launch_fast_cpl(int slot, const GemvArgs& a, int rows, int cols, int gshift
     return launch_fast<R, CPL, 64, WPB, XB, YB, NORM>(a, rows, cols, gshift, lds, stream);
 }
 
-// The per-lane-x kernel for bf16 GEMVs whose K is 2048 x KW (KW 2..8):
+// The per-lane-x kernel for GEMVs whose K is 2048 x KW (KW 2..8):
 // R = 4 rows per wave (8 for KW >= 3 with N >= 16384), two row groups per
 // workgroup at KW = 2; at KW = 2 only up to N = 16384 (the staged kernel is
 // as fast or faster on the larger K = 4096 shapes).  False when it does not
 // apply.
-template <bool NORM>
+template <bool NORM, bool BF16>
 bool launch_xl(const GemvArgs& a, int64_t rows, int64_t cols, int gshift, hipStream_t stream) {
     if (cols % 2048 != 0 || rows > INT32_MAX) return false;
     const int kw = static_cast<int>(cols / 2048);
     if (kw < 2 || kw > 8 || (kw == 2 && rows > 16384)) return false;
+    // fp32 x: 3-18 % faster than the staged kernel up to N = 6144 (cfg0 5.27
+    // -> 5.12 us, K 14336 14.8 -> 12.9, K 16384 16.7 -> 13.8), slower from
+    // N = 14336 (the staged kernel's 4 rows per wave)
+    if (!BF16 && rows >= 8192) return false;
     const int r = static_cast<int>(rows), c = static_cast<int>(cols);
     const bool wide = kw >= 3 && rows >= 16384;
-    const auto* xp = static_cast<const uint16_t*>(a.x);
-    auto* yp = static_cast<uint16_t*>(a.y);
 #define KC_XL(KWV, RV, RGWV)                                                                     \
-    gemv_int4_xl_kernel<RV, KWV, RGWV, NORM><<<static_cast<unsigned>((r + RV * RGWV - 1) / (RV * RGWV)), \
+    gemv_int4_xl_kernel<RV, KWV, RGWV, NORM, BF16><<<static_cast<unsigned>((r + RV * RGWV - 1) / (RV * RGWV)), \
                                                KWV * RGWV * kWave, 0, stream>>>(                 \
-        a.packed, a.scales, a.zeros, xp, yp, r, c, gshift, a.gamma, a.eps)
+        a.packed, a.scales, a.zeros, a.x, a.y, r, c, gshift, a.gamma, a.eps)
 #define KC_XL_CASE(KWV)                  \
     case KWV:                            \
         if (wide) KC_XL(KWV, 8, 1);      \
@@ -649,8 +661,8 @@ int gemv_int4(const char* fn, const uint8_t* packed, const float* scales, const 
                       (!NORM || kc::aligned(gamma, 16)) &&
                       lds <= static_cast<size_t>(device_max_lds());
     const GemvArgs a{packed, scales, zeros, x, y, gamma, eps};
-    if constexpr (XB && YB) {
-        if (fast && launch_xl<NORM>(a, rows, cols, kc::ilog2(gs) - 5, stream)) return kc::check_launch(fn);
+    if constexpr (XB == YB) {
+        if (fast && launch_xl<NORM, XB>(a, rows, cols, kc::ilog2(gs) - 5, stream)) return kc::check_launch(fn);
     }
     bool launched = false;
     if (fast) {

@@ -129,8 +129,12 @@ def test_gemv_f32_shapes(gpu, oracle, rows, cols, gs):
 # Staged-kernel variants: 4 rows per wave (K = 4096 from N = 4096, K = 8192
 # from N = 8192; ragged N, 16- and 64-lane slot maps) and x beyond 64 KB of
 # LDS (fp32 x at K > 15872, up to the 160 KB of K = 32768).
-F32_STAGED_SHAPES = [(4096, 4096, 32), (4099, 4096, 64), (8192, 8192, 128), (8200, 8192, 32),
-                     (40, 16384, 128), (33, 20480, 64), (9, 32768, 128), (5, 31744, 32)]
+# Below N = 8192 with K = 2048 x 2..8 the fp32 GEMV takes the per-lane-x
+# kernel instead (ragged N, groups 32..256).
+F32_STAGED_SHAPES = [(8192, 4096, 32), (8195, 4096, 64), (8192, 8192, 128), (8200, 8192, 32),
+                     (8200, 16384, 128), (33, 20480, 64), (9, 32768, 128), (5, 31744, 32),
+                     (4096, 4096, 32), (4099, 4096, 64), (8191, 4096, 128), (100, 6144, 64),
+                     (4097, 14336, 128), (17, 8192, 256), (40, 16384, 128)]
 
 
 @pytest.mark.parametrize("rows,cols,gs", F32_STAGED_SHAPES)
