@@ -325,7 +325,8 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_int4_fast_kernel(
 
 
 // ---------------------------------------------------------------------------
-// GEMV with K split across waves and x per lane (bf16, K a multiple of 2048).
+// GEMV with K split across waves and x per lane (K a multiple of 2048; bf16
+// x and y, or fp32 x and y below N = 8192).
 //
 // A workgroup of KW x RGW waves computes RGW groups of R rows; wave (kw, rg)
 // takes chunk c = 64 kw + lane (32 k) of each of its R rows.  A lane loads
@@ -338,7 +339,9 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_int4_fast_kernel(
 // N <= 6144 a few per cent; K 16384 / 8192 with N 4096: 9.8 -> 8.6, 5.6 ->
 // 5.4 us); the gate/up shape (K 4096, N 28672) keeps the staged kernel.
 // With NORM, x = bf16(gamma h) and each wave adds its lanes' sums of h^2 to
-// the partials, so the row sums are scaled by rms_inv at the end.
+// the partials, so the row sums are scaled by rms_inv at the end.  With fp32
+// x a lane loads its chunk's 32 values (128 bytes) in their own order and
+// folds with offset 8, as the staged kernel's fp32 decode does.
 // ---------------------------------------------------------------------------
 template <int R, int KW, int RGW, bool NORM, bool BF16 = true>
 __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
