@@ -194,8 +194,8 @@ int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
  * fp8_quant.py:55-60):  Y[m, n] = sx[m] * sw[n] * sum_k e4m3(qx[m,k]) *
  * e4m3(qw[n,k]).  qx [M, K] per-token codes with scales sx [M], qw [N, K]
  * per-output-channel codes with scales sw [N] (the quantizers below), Y
- * [M, N] row-major bf16 (RNE) or fp32.  K % 16 == 0, qx and qw 16-byte
- * aligned. */
+ * [M, N] row-major bf16 (RNE) or fp32.  K % 16 == 0 (K == 0 writes Y = 0),
+ * qx and qw 16-byte aligned. */
 int kc_gemm_fp8_w8a8_bf16(const int8_t* d_qx, const float* d_sx, const int8_t* d_qw,
                           const float* d_sw, uint16_t* d_y, int64_t M, int64_t N,
                           int64_t K, kc_stream_t stream);

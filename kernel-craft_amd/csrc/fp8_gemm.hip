@@ -258,6 +258,16 @@ __global__ __launch_bounds__(kThreads) void gemm_fp8_kernel(
     }
 }
 
+// Y = 0 for an empty contraction (K == 0): the GEMM kernel's prologue
+// always loads its first K step, so it is never launched with K == 0.
+template <typename T>
+__global__ void fill_zero_kernel(T* y, int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += stride)
+        y[i] = T(0);
+}
+
 template <bool YBF16>
 int gemm_fp8(const char* fn, const int8_t* qx, const float* sx, const int8_t* qw, const float* sw,
              void* y, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
@@ -267,6 +277,16 @@ int gemm_fp8(const char* fn, const int8_t* qx, const float* sx, const int8_t* qw
     if (K % 16 != 0)
         return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: K=%lld must be a multiple of 16", fn,
                              (long long)K);
+    if (K == 0) {  // qx and qw hold no bytes and may be null
+        if (!y) return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: null device pointer", fn);
+        const int64_t n = M * N;
+        const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((n + 255) / 256, 4096));
+        if constexpr (YBF16)
+            fill_zero_kernel<<<blocks, 256, 0, stream>>>(static_cast<uint16_t*>(y), n);
+        else
+            fill_zero_kernel<<<blocks, 256, 0, stream>>>(static_cast<float*>(y), n);
+        return kc::check_launch(fn);
+    }
     if (!qx || !sx || !qw || !sw || !y)
         return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: null device pointer", fn);
     if (!kc::aligned(qx, 16) || !kc::aligned(qw, 16))

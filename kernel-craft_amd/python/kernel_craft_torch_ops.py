@@ -3,26 +3,34 @@ kernel_craft_torch_ops.py
 PyTorch operators over libkernels.so, the MI355X (gfx950) HIP build of
 kernel-craft's quantized-inference kernels, loaded through ctypes.
 
-This module keeps the reference bridge's interface
-(``src/python/kernel_craft_torch_ops.py`` in kernel-craft): the same library
-discovery order (``KERNEL_CRAFT_LIB``, ``../../build/libkernels.so``,
-``../../libkernels.so``, ``/usr/local/lib/kernel_craft/libkernels.so``,
-reference :68-87), ``RTLD_GLOBAL`` loading (:96), the same ctypes prototypes
-(:101-168), the same public functions with the same arguments, output
-allocations and OTEL span names/attributes (:265-381), and the same
-``torch.library`` schema strings under the ``kernel_craft`` namespace
-(:428-479).  On ROCm PyTorch, GPU tensors are ``device.type == "cuda"`` and
+The module keeps the interface of kernel-craft's bridge
+(``src/python/kernel_craft_torch_ops.py``):
+
+* the library is found through ``KERNEL_CRAFT_LIB``, then
+  ``../../build/libkernels.so``, ``../../libkernels.so`` and
+  ``/usr/local/lib/kernel_craft/libkernels.so`` relative to this file
+  (reference :68-87), and loaded with ``RTLD_GLOBAL`` (:96);
+* the seven symbols the reference binds on load (:101-168) are bound here
+  too, so a library missing any of them fails every op, as there;
+* the public operators keep their names, arguments, output allocations and
+  span names/attributes (:193-421);
+* ``torch.ops.kernel_craft.*`` is registered with the reference's schema
+  strings for the CPU and CUDA dispatch keys (:428-479).
+
+On ROCm PyTorch a GPU tensor has ``device.type == "cuda"`` and
 ``torch.cuda.current_stream().cuda_stream`` is a ``hipStream_t``.
 
-Differences from the reference, all of them additions:
+What this module adds:
 
-* after every launcher call the library's error channel
-  (``kc_get_last_error``) is read and a ``RuntimeError`` raised on failure,
-  where the reference silently returns whatever the output buffer holds;
-* inputs must live on a GPU: there is no CPU fallback, and a CPU tensor
-  raises ``ValueError`` instead of handing a host pointer to a kernel;
-* extra operators for the paths the reference lacks (bf16 GEMV, the M>1
-  MFMA GEMM, bf16 FP8 quantization and fused SmoothQuant).
+* every input is checked (device, dtype, element count against the shape
+  arguments) before anything is launched, and a mismatch raises
+  ``ValueError``: the kernels trust the pointers they are given;
+* the library's error channel (``kc_get_last_error``) is read after each
+  call and a failure raises ``RuntimeError``;
+* there is no CPU fallback: a CPU tensor is an error;
+* operators for the entry points the reference lacks (bf16 GEMV and its
+  chain, the M > 1 GEMM, RMSNorm and its fusions, bf16 and fused-SmoothQuant
+  FP8 quantization, the FP8 GEMM, checkpoint conversion).
 
 Usage
 -----
@@ -33,13 +41,11 @@ Usage
     q, scales = kc_ops.fp8_quantize(x, per_token=True)
     x_hat     = kc_ops.fp8_dequantize(q, scales, rows, cols, per_token=True)
 
-Building libkernels.so
-----------------------
-::
-
-    make -C kernel-craft_amd          # produces build/libkernels.so
+Build the library with ``make -C kernel-craft_amd`` (writes
+``build/libkernels.so``).
 """
 
+import contextlib
 import ctypes
 import os
 from pathlib import Path
@@ -47,32 +53,33 @@ from typing import Optional, Tuple
 
 try:
     from kernel_craft_otel import kernel_span
-except ImportError:  # pragma: no cover - the OTEL module ships beside this one
-    from contextlib import nullcontext as kernel_span
+except ImportError:  # the tracing module ships beside this one
+    @contextlib.contextmanager
+    def kernel_span(name, **attrs):
+        yield None
 
 # ---------------------------------------------------------------------------
-# Library discovery (reference :68-87)
+# Loading the library
 # ---------------------------------------------------------------------------
+
+
+def _candidates() -> list:
+    here = Path(__file__).resolve().parent
+    found = [os.environ["KERNEL_CRAFT_LIB"]] if "KERNEL_CRAFT_LIB" in os.environ else []
+    return found + [here.parent.parent / "build" / "libkernels.so",
+                    here.parent.parent / "libkernels.so",
+                    Path("/usr/local/lib/kernel_craft/libkernels.so")]
 
 
 def _find_lib() -> str:
-    """Return path to libkernels.so, searching standard locations."""
-    candidates = []
-    if "KERNEL_CRAFT_LIB" in os.environ:
-        candidates.append(os.environ["KERNEL_CRAFT_LIB"])
-    here = Path(__file__).resolve().parent
-    candidates += [
-        here.parent.parent / "build" / "libkernels.so",
-        here.parent.parent / "libkernels.so",
-        Path("/usr/local/lib/kernel_craft/libkernels.so"),
-    ]
-    for p in candidates:
+    """First existing libkernels.so in the discovery order; FileNotFoundError
+    naming every place looked at otherwise."""
+    paths = _candidates()
+    for p in paths:
         if Path(p).exists():
             return str(p)
-    raise FileNotFoundError(
-        "libkernels.so not found. Build with: make -C kernel-craft_amd\n"
-        f"Searched: {[str(c) for c in candidates]}"
-    )
+    raise FileNotFoundError("libkernels.so not found (build it with: make -C kernel-craft_amd); "
+                            f"looked at {[str(p) for p in paths]}")
 
 
 _LIB: Optional[ctypes.CDLL] = None
@@ -81,8 +88,9 @@ _LIB: Optional[ctypes.CDLL] = None
 def _get_lib() -> ctypes.CDLL:
     global _LIB
     if _LIB is None:
-        _LIB = ctypes.CDLL(_find_lib(), mode=ctypes.RTLD_GLOBAL)
-        _setup_prototypes(_LIB)
+        lib = ctypes.CDLL(_find_lib(), mode=ctypes.RTLD_GLOBAL)
+        _setup_prototypes(lib)
+        _LIB = lib
     return _LIB
 
 
@@ -90,10 +98,10 @@ _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _i64 = ctypes.c_int64
 _b = ctypes.c_bool
+_f = ctypes.c_float
 
-# name -> (argtypes, restype).  The first seven are the reference's own
-# prototypes (reference :105-168); the reference binds them all at load time,
-# so a missing symbol fails every op, exactly as there.
+# name -> (argtypes, restype).  The first seven are the symbols the
+# reference binds at load time (reference :105-168).
 PROTOTYPES = {
     "launch_flash_attention": ([_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _b, _vp], None),
     "launch_paged_attention": ([_vp] * 6 + [_i] * 6 + [_vp], None),
@@ -102,8 +110,9 @@ PROTOTYPES = {
     "launch_quantize_fp8": ([_vp, _vp, _vp, _i, _i, _b, _vp], None),
     "launch_dequantize_fp8": ([_vp, _vp, _vp, _i, _i, _b, _vp], None),
     "launch_verify_draft_tokens": ([_vp] * 7 + [_i, _i, _vp], None),
-    # error channel and extensions (no reference counterpart)
+    # further reference launchers, the error channel and the extensions
     "launch_smoothquant_scale": ([_vp, _vp, _vp, _i, _i, _vp], None),
+    "launch_rmsnorm": ([_vp, _vp, _vp, _i, _i, _f, _vp], None),
     "kc_get_last_error": ([], _i),
     "kc_peek_last_error": ([], _i),
     "kc_last_error_string": ([], ctypes.c_char_p),
@@ -125,14 +134,14 @@ PROTOTYPES = {
     "kc_quantize_fp8_smooth_div_f32": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp], _i),
     "kc_quantize_fp8_smooth_div_bf16": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp], _i),
     "kc_quantize_fp8_smooth_mul_bf16": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp], _i),
-    "launch_rmsnorm": ([_vp, _vp, _vp, _i, _i, ctypes.c_float, _vp], None),
-    "kc_rmsnorm_bf16": ([_vp, _vp, _vp, _i, _i, ctypes.c_float, _vp], _i),
-    "kc_rmsnorm_gemv_int4_bf16": ([_vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
+    "kc_rmsnorm_bf16": ([_vp, _vp, _vp, _i, _i, _f, _vp], _i),
+    "kc_rmsnorm_gemv_int4_bf16": ([_vp, _vp, _f, _vp, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
 }
 
 
 def _setup_prototypes(lib: ctypes.CDLL) -> None:
-    """Set ctypes argtypes/restype for every launcher."""
+    """Bind argtypes/restype of every symbol in PROTOTYPES (AttributeError
+    for a symbol the library does not export)."""
     for name, (argtypes, restype) in PROTOTYPES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
@@ -140,35 +149,63 @@ def _setup_prototypes(lib: ctypes.CDLL) -> None:
 
 
 # ---------------------------------------------------------------------------
-# Helpers
+# Arguments and errors
 # ---------------------------------------------------------------------------
 
 
 def _stream() -> ctypes.c_void_p:
-    """Return the current HIP stream as a ctypes void pointer."""
+    """The current torch stream (a hipStream_t) for the launchers."""
     import torch
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
 def _ptr(t) -> ctypes.c_void_p:
-    """Return data_ptr of a torch tensor as ctypes void pointer."""
+    """Device address of a tensor's first element."""
     return ctypes.c_void_p(t.data_ptr())
 
 
-def _on_gpu(*tensors) -> None:
+def _arg(name: str, t, dtypes=None, numel: Optional[int] = None):
+    """``t`` made contiguous after checking that it has one of ``dtypes``
+    and holds ``numel`` elements; ValueError otherwise.  Every op checks all
+    of its arguments this way, then their device with ``_on_gpu``, before
+    it allocates or launches anything."""
+    if dtypes is not None:
+        allowed = dtypes if isinstance(dtypes, tuple) else (dtypes,)
+        if t.dtype not in allowed:
+            raise ValueError(f"{name} has dtype {t.dtype}; expected "
+                             f"{' or '.join(str(d) for d in allowed)}")
+    if numel is not None and t.numel() != numel:
+        raise ValueError(f"{name} holds {t.numel()} elements; the shape arguments need {numel}")
+    return t.contiguous()
+
+
+def _on_gpu(op: str, *tensors) -> None:
+    """ValueError unless every tensor lives on a GPU."""
     for t in tensors:
-        if t.device.type != "cuda":
-            raise ValueError(
-                "kernel_craft ops run on the GPU only; got a tensor on "
-                f"{t.device} (there is no CPU fallback)")
+        if t is not None and t.device.type != "cuda":
+            raise ValueError(f"{op}: a tensor is on {t.device}; kernel_craft ops run on the "
+                             "GPU only (there is no CPU fallback)")
+
+
+def _int4_weights(op: str, packed, scales, zeros, rows: int, cols: int, group_size: int):
+    """Validated (packed, scales, zeros) of an INT4 layer [rows, cols]: the
+    reference layout, packed [rows, cols/2] u8, scales [rows, G] fp32,
+    zeros [rows, G/2] u8 with G = cols / group_size.  Bad shape arguments
+    are left to the library, which rejects them with a message."""
+    import torch
+    G = cols // group_size if group_size > 0 else 0
+    ok = rows >= 0 and cols >= 0 and group_size > 0
+    return (_arg(f"{op}: packed", packed, torch.uint8, rows * (cols // 2) if ok else None),
+            _arg(f"{op}: scales", scales, torch.float32, rows * G if ok else None),
+            _arg(f"{op}: zeros", zeros, torch.uint8, rows * (G // 2) if ok else None))
 
 
 def _check(name: str, status: Optional[int] = None) -> None:
-    """Raise if the call recorded an error (void launchers) or returned one."""
+    """RuntimeError if the call returned a non-zero status or (void
+    launchers) left an error in the library's channel; clears the channel."""
     lib = _get_lib()
     code = lib.kc_get_last_error()
-    if status:
-        code = status
+    code = status or code
     if code:
         msg = lib.kc_last_error_string().decode(errors="replace")
         raise RuntimeError(f"{name} failed (kc_status {code}): {msg}")
@@ -181,139 +218,141 @@ def last_error() -> Tuple[int, str]:
     return lib.kc_get_last_error(), msg
 
 
+def _stub_op(op: str, symbol: str, span_attrs: dict, pointer_args, int_args):
+    """An op whose launcher this build exports as a stub (outside the
+    quantized-inference path): the call is made so that the library's
+    not-implemented error surfaces as RuntimeError, inside the same span the
+    reference opens for it."""
+    with kernel_span(op, **span_attrs):
+        getattr(_get_lib(), symbol)(*[_ptr(t) for t in pointer_args], *int_args, _stream())
+    _check(op)
+
+
 # ---------------------------------------------------------------------------
-# Public API -- the reference's operators (reference :193-421)
+# The reference's operators (reference :193-421)
 # ---------------------------------------------------------------------------
 
 
 def flash_attention(Q, K, V, H_kv: int, causal: bool = False):
-    """FlashAttention prefill: out of scope for this build; the library's
-    launcher is a stub that reports KC_ERR_NOT_IMPLEMENTED."""
+    """Prefill attention [B, H, N, d] (reference op; this library's launcher
+    is a stub, so the call raises RuntimeError)."""
     import torch
-    Q, K, V = Q.contiguous(), K.contiguous(), V.contiguous()
-    _on_gpu(Q, K, V)
+    Q, K, V = (_arg("flash_attention: " + n, t, torch.float32) for n, t in
+               (("Q", Q), ("K", K), ("V", V)))
+    _on_gpu("flash_attention", Q, K, V)
     B, H, N, d = Q.shape
-    O = torch.zeros(B, H, N, d, dtype=torch.float32, device=Q.device)
-    with kernel_span("flash_attention", batch=B, heads=H, kv_heads=H_kv,
-                     seq_len=N, head_dim=d, causal=causal):
-        _get_lib().launch_flash_attention(
-            _ptr(Q), _ptr(K), _ptr(V), _ptr(O), B, H, H_kv, N, d, causal, _stream())
-    _check("flash_attention")
-    return O
+    out = torch.zeros(B, H, N, d, dtype=torch.float32, device=Q.device)
+    _stub_op("flash_attention", "launch_flash_attention",
+             dict(batch=B, heads=H, kv_heads=H_kv, seq_len=N, head_dim=d, causal=causal),
+             (Q, K, V, out), (B, H, H_kv, N, d, causal))
+    return out
 
 
 def paged_attention(Q, block_table, K_pool, V_pool, seq_lens, H_kv: int, block_size: int):
-    """PagedAttention decode: out of scope for this build (stub launcher)."""
+    """Decode attention over a paged KV cache, output [B, H, d] (reference
+    op; stub launcher, raises RuntimeError)."""
     import torch
-    Q, block_table = Q.contiguous(), block_table.contiguous()
-    K_pool, V_pool, seq_lens = K_pool.contiguous(), V_pool.contiguous(), seq_lens.contiguous()
-    _on_gpu(Q, block_table, K_pool, V_pool, seq_lens)
+    Q, K_pool, V_pool = (_arg("paged_attention: " + n, t, torch.float32) for n, t in
+                         (("Q", Q), ("K_pool", K_pool), ("V_pool", V_pool)))
+    block_table = _arg("paged_attention: block_table", block_table, torch.int32)
+    seq_lens = _arg("paged_attention: seq_lens", seq_lens, torch.int32)
+    _on_gpu("paged_attention", Q, block_table, K_pool, V_pool, seq_lens)
     B, H, d = Q.shape
-    max_blocks = block_table.shape[1]
-    O = torch.zeros(B, H, d, dtype=torch.float32, device=Q.device)
-    with kernel_span("paged_attention", batch=B, heads=H, kv_heads=H_kv,
-                     seq_len=int(seq_lens.max().item()), block_size=block_size):
-        _get_lib().launch_paged_attention(
-            _ptr(Q), _ptr(block_table), _ptr(K_pool), _ptr(V_pool), _ptr(O), _ptr(seq_lens),
-            B, H, H_kv, d, block_size, max_blocks, _stream())
-    _check("paged_attention")
-    return O
+    out = torch.zeros(B, H, d, dtype=torch.float32, device=Q.device)
+    _stub_op("paged_attention", "launch_paged_attention",
+             dict(batch=B, heads=H, kv_heads=H_kv, seq_len=int(seq_lens.max().item()),
+                  block_size=block_size),
+             (Q, block_table, K_pool, V_pool, out, seq_lens),
+             (B, H, H_kv, d, block_size, block_table.shape[1]))
+    return out
+
+
+def speculative_verify(draft_probs, target_probs, draft_tokens, rand_vals, rand_vals2) -> Tuple:
+    """Draft-token acceptance for speculative decoding, returning int32
+    (accepted [K], corrected [K]) (reference op; stub launcher, raises
+    RuntimeError)."""
+    import torch
+    draft_probs, target_probs, rand_vals, rand_vals2 = (
+        _arg("speculative_verify: " + n, t, torch.float32) for n, t in
+        (("draft_probs", draft_probs), ("target_probs", target_probs),
+         ("rand_vals", rand_vals), ("rand_vals2", rand_vals2)))
+    draft_tokens = _arg("speculative_verify: draft_tokens", draft_tokens, torch.int32)
+    _on_gpu("speculative_verify", draft_probs, target_probs, draft_tokens, rand_vals, rand_vals2)
+    K, vocab = draft_probs.shape
+    accepted = torch.zeros(K, dtype=torch.int32, device=draft_probs.device)
+    corrected = torch.zeros(K, dtype=torch.int32, device=draft_probs.device)
+    _stub_op("speculative_verify", "launch_verify_draft_tokens",
+             dict(num_tokens=K, vocab_size=vocab),
+             (draft_probs, target_probs, draft_tokens, rand_vals, rand_vals2, accepted,
+              corrected), (K, vocab))
+    return accepted, corrected
 
 
 def int4_dequantize(packed, scales, zeros, rows: int, cols: int, group_size: int = 128):
-    """
-    Dequantize INT4 packed weights to FP32.
-
-    :param packed     torch.Tensor [rows, cols/2] uint8 GPU
-    :param scales     torch.Tensor [rows, cols/group_size] float32 GPU
-    :param zeros      torch.Tensor [rows, cols/group_size/2] uint8 GPU
-    :return:          torch.Tensor [rows, cols] float32 GPU
-    """
+    """INT4 layer -> fp32 W [rows, cols], W[n, k] = (sext4(q) - z) * s
+    (launch_dequantize_int4)."""
     import torch
-    packed, scales, zeros = packed.contiguous(), scales.contiguous(), zeros.contiguous()
-    _on_gpu(packed, scales, zeros)
-    output = torch.zeros(rows, cols, dtype=torch.float32, device=packed.device)
-    _get_lib().launch_dequantize_int4(
-        _ptr(packed), _ptr(scales), _ptr(zeros), _ptr(output), rows, cols, group_size, _stream())
+    packed, scales, zeros = _int4_weights("int4_dequantize", packed, scales, zeros, rows, cols,
+                                          group_size)
+    _on_gpu("int4_dequantize", packed, scales, zeros)
+    out = torch.zeros(rows, cols, dtype=torch.float32, device=packed.device)
+    _get_lib().launch_dequantize_int4(_ptr(packed), _ptr(scales), _ptr(zeros), _ptr(out),
+                                      rows, cols, group_size, _stream())
     _check("int4_dequantize")
-    return output
+    return out
 
 
 def int4_gemv(packed, scales, zeros, x, rows: int, cols: int, group_size: int = 128):
-    """
-    INT4 weight GEMV: y = W_int4 * x (dequantize on the fly).
-
-    :param x          torch.Tensor [cols] float32 GPU
-    :return:          torch.Tensor [rows] float32 GPU
-    """
+    """y [rows] = W x for an INT4 layer and fp32 x [cols], fp32 accumulation
+    (launch_gemv_int4)."""
     import torch
-    packed, scales, zeros, x = (packed.contiguous(), scales.contiguous(),
-                                zeros.contiguous(), x.contiguous())
-    _on_gpu(packed, scales, zeros, x)
+    packed, scales, zeros = _int4_weights("int4_gemv", packed, scales, zeros, rows, cols,
+                                          group_size)
+    x = _arg("int4_gemv: x", x, torch.float32, cols)
+    _on_gpu("int4_gemv", packed, scales, zeros, x)
     y = torch.zeros(rows, dtype=torch.float32, device=packed.device)
     with kernel_span("int4_gemv", rows=rows, cols=cols, group_size=group_size):
-        _get_lib().launch_gemv_int4(
-            _ptr(packed), _ptr(scales), _ptr(zeros), _ptr(x), _ptr(y),
-            rows, cols, group_size, _stream())
+        _get_lib().launch_gemv_int4(_ptr(packed), _ptr(scales), _ptr(zeros), _ptr(x), _ptr(y),
+                                    rows, cols, group_size, _stream())
     _check("int4_gemv")
     return y
 
 
 def fp8_quantize(x, per_token: bool = True) -> Tuple:
-    """
-    Quantize FP32 activations to FP8 E4M3.
+    """fp32 x [rows, cols] -> (int8 E4M3 codes [rows, cols], fp32 scales
+    [rows] per token or [1]) (launch_quantize_fp8).
 
-    :return: (quantized: int8 [rows, cols], scales: float32 [rows] or [1])
-
-    As in the reference, per-tensor mode reads its scale from the freshly
-    zeroed ``scales`` buffer, so every code saturates (reference :345-347).
-    """
+    Per-tensor mode reads its scale from the freshly zeroed scales buffer, as
+    the reference bridge does (reference :345-347), so every code saturates
+    to +-448."""
     import torch
-    x = x.contiguous()
-    _on_gpu(x)
+    x = _arg("fp8_quantize: x", x, torch.float32)
+    _on_gpu("fp8_quantize", x)
     rows, cols = x.shape
     q = torch.zeros(rows, cols, dtype=torch.int8, device=x.device)
-    n_scales = rows if per_token else 1
-    scales = torch.zeros(n_scales, dtype=torch.float32, device=x.device)
+    scales = torch.zeros(rows if per_token else 1, dtype=torch.float32, device=x.device)
     with kernel_span("fp8_quantize", rows=rows, cols=cols, per_token=per_token):
-        _get_lib().launch_quantize_fp8(
-            _ptr(x), _ptr(q), _ptr(scales), rows, cols, per_token, _stream())
+        _get_lib().launch_quantize_fp8(_ptr(x), _ptr(q), _ptr(scales), rows, cols, per_token,
+                                       _stream())
     _check("fp8_quantize")
     return q, scales
 
 
 def fp8_dequantize(q, scales, rows: int, cols: int, per_token: bool = True):
-    """
-    Dequantize FP8 E4M3 activations back to FP32.
-
-    :return: torch.Tensor [rows, cols] float32 GPU
-    """
+    """int8 E4M3 codes [rows, cols] and their scales -> fp32 [rows, cols]
+    (launch_dequantize_fp8)."""
     import torch
-    q, scales = q.contiguous(), scales.contiguous()
-    _on_gpu(q, scales)
-    output = torch.zeros(rows, cols, dtype=torch.float32, device=q.device)
-    _get_lib().launch_dequantize_fp8(
-        _ptr(q), _ptr(scales), _ptr(output), rows, cols, per_token, _stream())
+    q = _arg("fp8_dequantize: q", q, (torch.int8, torch.uint8), rows * cols)
+    scales = _arg("fp8_dequantize: scales", scales, torch.float32,
+                  rows if per_token else None)
+    if not per_token and scales.numel() < 1:
+        raise ValueError("fp8_dequantize: per-tensor mode needs one scale")
+    _on_gpu("fp8_dequantize", q, scales)
+    out = torch.zeros(rows, cols, dtype=torch.float32, device=q.device)
+    _get_lib().launch_dequantize_fp8(_ptr(q), _ptr(scales), _ptr(out), rows, cols, per_token,
+                                     _stream())
     _check("fp8_dequantize")
-    return output
-
-
-def speculative_verify(draft_probs, target_probs, draft_tokens, rand_vals, rand_vals2) -> Tuple:
-    """Speculative-decoding verification: out of scope (stub launcher)."""
-    import torch
-    draft_probs, target_probs = draft_probs.contiguous(), target_probs.contiguous()
-    draft_tokens, rand_vals, rand_vals2 = (draft_tokens.contiguous(), rand_vals.contiguous(),
-                                           rand_vals2.contiguous())
-    _on_gpu(draft_probs, target_probs, draft_tokens, rand_vals, rand_vals2)
-    K, vocab = draft_probs.shape
-    accepted = torch.zeros(K, dtype=torch.int32, device=draft_probs.device)
-    corrected = torch.zeros(K, dtype=torch.int32, device=draft_probs.device)
-    with kernel_span("speculative_verify", num_tokens=K, vocab_size=vocab):
-        _get_lib().launch_verify_draft_tokens(
-            _ptr(draft_probs), _ptr(target_probs), _ptr(draft_tokens), _ptr(rand_vals),
-            _ptr(rand_vals2), _ptr(accepted), _ptr(corrected), K, vocab, _stream())
-    _check("speculative_verify")
-    return accepted, corrected
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -322,11 +361,12 @@ def speculative_verify(draft_probs, target_probs, draft_tokens, rand_vals, rand_
 
 
 def smoothquant_scale(x, smooth_scales):
-    """out[r, c] = x[r, c] / smooth_scales[c] (launch_smoothquant_scale)."""
+    """out[r, c] = x[r, c] / smooth_scales[c], fp32 (launch_smoothquant_scale)."""
     import torch
-    x, smooth_scales = x.contiguous(), smooth_scales.contiguous()
-    _on_gpu(x, smooth_scales)
+    x = _arg("smoothquant_scale: x", x, torch.float32)
     rows, cols = x.shape
+    smooth_scales = _arg("smoothquant_scale: smooth_scales", smooth_scales, torch.float32, cols)
+    _on_gpu("smoothquant_scale", x, smooth_scales)
     out = torch.zeros(rows, cols, dtype=torch.float32, device=x.device)
     _get_lib().launch_smoothquant_scale(_ptr(x), _ptr(smooth_scales), _ptr(out), rows, cols,
                                         _stream())
@@ -335,11 +375,12 @@ def smoothquant_scale(x, smooth_scales):
 
 
 def int4_gemv_bf16(packed, scales, zeros, x, rows: int, cols: int, group_size: int = 128):
-    """y = W_int4 * x with bf16 x [cols] and bf16 y [rows], fp32 accumulation."""
+    """y [rows] bf16 = W x for bf16 x [cols], fp32 accumulation (kc_gemv_int4_bf16)."""
     import torch
-    packed, scales, zeros, x = (packed.contiguous(), scales.contiguous(),
-                                zeros.contiguous(), x.contiguous())
-    _on_gpu(packed, scales, zeros, x)
+    packed, scales, zeros = _int4_weights("int4_gemv_bf16", packed, scales, zeros, rows, cols,
+                                          group_size)
+    x = _arg("int4_gemv_bf16: x", x, torch.bfloat16, cols)
+    _on_gpu("int4_gemv_bf16", packed, scales, zeros, x)
     y = torch.empty(rows, dtype=torch.bfloat16, device=packed.device)
     with kernel_span("int4_gemv_bf16", rows=rows, cols=cols, group_size=group_size):
         st = _get_lib().kc_gemv_int4_bf16(_ptr(packed), _ptr(scales), _ptr(zeros), _ptr(x),
@@ -357,21 +398,46 @@ class GemvOp(ctypes.Structure):
 
 
 def int4_gemv_bf16_chain(ops) -> None:
-    """Runs int4_gemv_bf16 for each op in order, from one call: ops is a list
-    of (packed, scales, zeros, x, y, rows, cols, group_size) with bf16 x and
-    y tensors already allocated; an op may take an earlier op's y (or a
-    contiguous slice of it) as its x."""
+    """int4_gemv_bf16 for each op in order, from one call.  ``ops`` is a list
+    of (packed, scales, zeros, x, y, rows, cols, group_size) with bf16 x and y
+    already allocated and contiguous (the op writes into y, so a copy would
+    lose the result); an op's x may be an earlier op's y or a contiguous
+    slice of it."""
+    import torch
     arr = (GemvOp * max(1, len(ops)))()
     for i, (packed, scales, zeros, x, y, rows, cols, gs) in enumerate(ops):
-        for t in (packed, scales, zeros, x, y):
-            if not t.is_contiguous():
-                raise ValueError("int4_gemv_bf16_chain: tensors must be contiguous")
-        _on_gpu(packed, scales, zeros, x, y)
-        arr[i] = GemvOp(_ptr(packed), _ptr(scales), _ptr(zeros), _ptr(x), _ptr(y), rows, cols, gs, 0)
+        name = f"int4_gemv_bf16_chain op {i}"
+        if not (x.is_contiguous() and y.is_contiguous()):
+            raise ValueError(f"{name}: x and y must be contiguous")
+        packed, scales, zeros = _int4_weights(name, packed, scales, zeros, rows, cols, gs)
+        _arg(f"{name}: x", x, torch.bfloat16, cols)
+        _arg(f"{name}: y", y, torch.bfloat16, rows)
+        _on_gpu(name, packed, scales, zeros, x, y)
+        arr[i] = GemvOp(_ptr(packed), _ptr(scales), _ptr(zeros), _ptr(x), _ptr(y), rows, cols,
+                        gs, 0)
     with kernel_span("int4_gemv_bf16_chain", ops=len(ops)):
         st = _get_lib().kc_gemv_int4_bf16_chain(ctypes.cast(arr, ctypes.c_void_p), len(ops),
                                                 _stream())
     _check("int4_gemv_bf16_chain", st)
+
+
+def int4_gemm_bf16(packed, scales, zeros, x, rows: int, cols: int, group_size: int = 128):
+    """Y [m, rows] bf16 = X W^T for bf16 X [m, cols], 1 <= m <= 64, on matrix
+    cores (kc_gemm_int4_bf16)."""
+    import torch
+    packed, scales, zeros = _int4_weights("int4_gemm_bf16", packed, scales, zeros, rows, cols,
+                                          group_size)
+    x = _arg("int4_gemm_bf16: x", x, torch.bfloat16)
+    if x.dim() != 2 or x.shape[1] != cols:
+        raise ValueError(f"int4_gemm_bf16: x must be [m, {cols}], not {list(x.shape)}")
+    _on_gpu("int4_gemm_bf16", packed, scales, zeros, x)
+    m = x.shape[0]
+    y = torch.empty(m, rows, dtype=torch.bfloat16, device=packed.device)
+    with kernel_span("int4_gemm_bf16", m=m, rows=rows, cols=cols, group_size=group_size):
+        st = _get_lib().kc_gemm_int4_bf16(_ptr(packed), _ptr(scales), _ptr(zeros), _ptr(x),
+                                          _ptr(y), m, rows, cols, group_size, _stream())
+    _check("int4_gemm_bf16", st)
+    return y
 
 
 def act_order_permutation(g_idx, group_size: int):
@@ -400,10 +466,12 @@ def convert_gptq(qweight, qzeros, scales, g_idx=None, group_size: int = 128, zer
     x[perm] (act-order checkpoints).  zero_offset is 1 for the original
     AutoGPTQ format (zero points stored minus one), 0 for its v2."""
     import torch
-    qweight, qzeros, scales = qweight.contiguous(), qzeros.contiguous(), scales.contiguous()
-    _on_gpu(qweight, qzeros, scales)
+    qweight = _arg("convert_gptq: qweight", qweight, torch.int32)
     K, N = qweight.shape[0] * 8, qweight.shape[1]
-    G = K // group_size
+    G = K // group_size if group_size > 0 else 0
+    qzeros = _arg("convert_gptq: qzeros", qzeros, torch.int32, G * (N // 8))
+    scales = _arg("convert_gptq: scales", scales, torch.float16, G * N)
+    _on_gpu("convert_gptq", qweight, qzeros, scales)
     perm = None if g_idx is None else act_order_permutation(g_idx, group_size)
     dperm = None if perm is None else perm.to(qweight.device)
     packed = torch.empty(N, K // 2, dtype=torch.uint8, device=qweight.device)
@@ -423,10 +491,12 @@ def convert_awq(qweight, qzeros, scales, group_size: int = 128):
     [G, N/8], scales fp16 [G, N]) to the reference layout: returns (packed
     u8 [N, K/2], scales fp32 [N, G], zeros u8 [N, G/2])."""
     import torch
-    qweight, qzeros, scales = qweight.contiguous(), qzeros.contiguous(), scales.contiguous()
-    _on_gpu(qweight, qzeros, scales)
+    qweight = _arg("convert_awq: qweight", qweight, torch.int32)
     K, N = qweight.shape[0], qweight.shape[1] * 8
-    G = K // group_size
+    G = K // group_size if group_size > 0 else 0
+    qzeros = _arg("convert_awq: qzeros", qzeros, torch.int32, G * (N // 8))
+    scales = _arg("convert_awq: scales", scales, torch.float16, G * N)
+    _on_gpu("convert_awq", qweight, qzeros, scales)
     packed = torch.empty(N, K // 2, dtype=torch.uint8, device=qweight.device)
     out_s = torch.empty(N, G, dtype=torch.float32, device=qweight.device)
     zeros = torch.empty(N, G // 2, dtype=torch.uint8, device=qweight.device)
@@ -445,12 +515,17 @@ def fp8_gemm_w8a8(qx, sx, qw, sw, out_dtype=None):
     out_dtype torch.bfloat16 (default) or torch.float32."""
     import torch
     out_dtype = torch.bfloat16 if out_dtype is None else out_dtype
-    qx, sx, qw, sw = qx.contiguous(), sx.contiguous(), qw.contiguous(), sw.contiguous()
-    _on_gpu(qx, sx, qw, sw)
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"fp8_gemm_w8a8: out_dtype must be bfloat16 or float32, not {out_dtype}")
+    qx = _arg("fp8_gemm_w8a8: qx", qx, (torch.int8, torch.uint8))
+    qw = _arg("fp8_gemm_w8a8: qw", qw, (torch.int8, torch.uint8))
+    if qx.dim() != 2 or qw.dim() != 2 or qw.shape[1] != qx.shape[1]:
+        raise ValueError("fp8_gemm_w8a8: qx [M, K] and qw [N, K] must share K")
     M, K = qx.shape
     N = qw.shape[0]
-    if qw.shape[1] != K or sx.numel() != M or sw.numel() != N:
-        raise ValueError("fp8_gemm_w8a8: shapes do not match")
+    sx = _arg("fp8_gemm_w8a8: sx", sx, torch.float32, M)
+    sw = _arg("fp8_gemm_w8a8: sw", sw, torch.float32, N)
+    _on_gpu("fp8_gemm_w8a8", qx, sx, qw, sw)
     y = torch.empty(M, N, dtype=out_dtype, device=qx.device)
     fn = (_get_lib().kc_gemm_fp8_w8a8_bf16 if out_dtype == torch.bfloat16
           else _get_lib().kc_gemm_fp8_w8a8_f32)
@@ -464,21 +539,18 @@ def rmsnorm(x, g, eps: float = 1e-6):
     """y = g * x / sqrt(mean(x^2, -1) + eps) per row (rmsnorm.cu:40-70):
     fp32 x and g through launch_rmsnorm, bf16 through kc_rmsnorm_bf16."""
     import torch
-    x, g = x.contiguous(), g.contiguous()
-    _on_gpu(x, g)
+    x = _arg("rmsnorm: x", x, (torch.float32, torch.bfloat16))
     D = x.shape[-1]
     rows = x.numel() // max(D, 1)
-    if g.numel() != D or g.dtype != x.dtype:
-        raise ValueError("rmsnorm: g must hold D values of x's dtype")
+    g = _arg("rmsnorm: g", g, x.dtype, D)
+    _on_gpu("rmsnorm", x, g)
     y = torch.empty_like(x)
     with kernel_span("rmsnorm", rows=rows, d=D):
         if x.dtype == torch.float32:
             _get_lib().launch_rmsnorm(_ptr(x), _ptr(g), _ptr(y), rows, D, eps, _stream())
             st = None
-        elif x.dtype == torch.bfloat16:
-            st = _get_lib().kc_rmsnorm_bf16(_ptr(x), _ptr(g), _ptr(y), rows, D, eps, _stream())
         else:
-            raise TypeError("rmsnorm: float32 or bfloat16 tensors")
+            st = _get_lib().kc_rmsnorm_bf16(_ptr(x), _ptr(g), _ptr(y), rows, D, eps, _stream())
     _check("rmsnorm", st)
     return y
 
@@ -488,9 +560,11 @@ def rmsnorm_int4_gemv_bf16(h, gamma, packed, scales, zeros, rows: int, cols: int
     """y = W_int4 * bf16(rmsnorm(h) * gamma) in one launch: bf16 h, gamma
     [cols], bf16 y [rows] (kc_rmsnorm_gemv_int4_bf16)."""
     import torch
-    h, gamma, packed, scales, zeros = (h.contiguous(), gamma.contiguous(), packed.contiguous(),
-                                       scales.contiguous(), zeros.contiguous())
-    _on_gpu(h, gamma, packed, scales, zeros)
+    packed, scales, zeros = _int4_weights("rmsnorm_int4_gemv_bf16", packed, scales, zeros, rows,
+                                          cols, group_size)
+    h = _arg("rmsnorm_int4_gemv_bf16: h", h, torch.bfloat16, cols)
+    gamma = _arg("rmsnorm_int4_gemv_bf16: gamma", gamma, torch.bfloat16, cols)
+    _on_gpu("rmsnorm_int4_gemv_bf16", h, gamma, packed, scales, zeros)
     y = torch.empty(rows, dtype=torch.bfloat16, device=packed.device)
     with kernel_span("rmsnorm_int4_gemv_bf16", rows=rows, cols=cols, group_size=group_size):
         st = _get_lib().kc_rmsnorm_gemv_int4_bf16(_ptr(h), _ptr(gamma), eps, _ptr(packed),
@@ -500,27 +574,12 @@ def rmsnorm_int4_gemv_bf16(h, gamma, packed, scales, zeros, rows: int, cols: int
     return y
 
 
-def int4_gemm_bf16(packed, scales, zeros, x, rows: int, cols: int, group_size: int = 128):
-    """Y = X W^T for X bf16 [m, cols] (m <= 64) on matrix cores; Y bf16 [m, rows]."""
-    import torch
-    packed, scales, zeros, x = (packed.contiguous(), scales.contiguous(),
-                                zeros.contiguous(), x.contiguous())
-    _on_gpu(packed, scales, zeros, x)
-    m = x.shape[0]
-    y = torch.empty(m, rows, dtype=torch.bfloat16, device=packed.device)
-    with kernel_span("int4_gemm_bf16", m=m, rows=rows, cols=cols, group_size=group_size):
-        st = _get_lib().kc_gemm_int4_bf16(_ptr(packed), _ptr(scales), _ptr(zeros), _ptr(x),
-                                          _ptr(y), m, rows, cols, group_size, _stream())
-    _check("int4_gemm_bf16", st)
-    return y
-
-
 def fp8_quantize_rows(x) -> Tuple:
     """Per-row FP8 quantization of a bf16 or fp32 [rows, cols] tensor: per
     token for activations, per output channel for a weight matrix."""
     import torch
-    x = x.contiguous()
-    _on_gpu(x)
+    x = _arg("fp8_quantize_rows: x", x, (torch.float32, torch.bfloat16))
+    _on_gpu("fp8_quantize_rows", x)
     rows, cols = x.shape
     q = torch.empty(rows, cols, dtype=torch.int8, device=x.device)
     s = torch.empty(rows, dtype=torch.float32, device=x.device)
@@ -536,8 +595,8 @@ def fp8_quantize_rows(x) -> Tuple:
 def col_absmax(x):
     """Per-column max |x| of a bf16 or fp32 [rows, cols] tensor."""
     import torch
-    x = x.contiguous()
-    _on_gpu(x)
+    x = _arg("col_absmax: x", x, (torch.float32, torch.bfloat16))
+    _on_gpu("col_absmax", x)
     rows, cols = x.shape
     out = torch.empty(cols, dtype=torch.float32, device=x.device)
     lib = _get_lib()
@@ -550,8 +609,9 @@ def col_absmax(x):
 def smooth_factors(amax_x, amax_w):
     """SmoothQuant factors (alpha = 0.5) from per-channel absmax of X and W."""
     import torch
-    amax_x, amax_w = amax_x.contiguous(), amax_w.contiguous()
-    _on_gpu(amax_x, amax_w)
+    amax_x = _arg("smooth_factors: amax_x", amax_x, torch.float32)
+    amax_w = _arg("smooth_factors: amax_w", amax_w, torch.float32, amax_x.numel())
+    _on_gpu("smooth_factors", amax_x, amax_w)
     s = torch.empty_like(amax_x)
     st = _get_lib().kc_smooth_factors(_ptr(amax_x), _ptr(amax_w), _ptr(s), amax_x.numel(),
                                       _stream())
@@ -563,21 +623,21 @@ def fp8_quantize_smooth(x, smooth, mode: str = "div") -> Tuple:
     """Fused SmoothQuant + per-row FP8: ``div`` quantizes x / s (activations),
     ``mul`` quantizes x * s (weights, bf16 only)."""
     import torch
-    x, smooth = x.contiguous(), smooth.contiguous()
-    _on_gpu(x, smooth)
+    if mode not in ("div", "mul"):
+        raise ValueError(f"mode must be 'div' or 'mul', not {mode!r}")
+    x = _arg("fp8_quantize_smooth: x", x,
+             (torch.float32, torch.bfloat16) if mode == "div" else torch.bfloat16)
     rows, cols = x.shape
+    smooth = _arg("fp8_quantize_smooth: smooth", smooth, torch.float32, cols)
+    _on_gpu("fp8_quantize_smooth", x, smooth)
     q = torch.empty(rows, cols, dtype=torch.int8, device=x.device)
     s = torch.empty(rows, dtype=torch.float32, device=x.device)
     lib = _get_lib()
     if mode == "div":
         fn = lib.kc_quantize_fp8_smooth_div_bf16 if x.dtype == torch.bfloat16 \
             else lib.kc_quantize_fp8_smooth_div_f32
-    elif mode == "mul":
-        if x.dtype != torch.bfloat16:
-            raise ValueError("mode='mul' takes a bf16 weight matrix")
-        fn = lib.kc_quantize_fp8_smooth_mul_bf16
     else:
-        raise ValueError(f"mode must be 'div' or 'mul', not {mode!r}")
+        fn = lib.kc_quantize_fp8_smooth_mul_bf16
     with kernel_span("fp8_quantize_smooth", rows=rows, cols=cols, mode=mode):
         st = fn(_ptr(x), _ptr(smooth), _ptr(q), _ptr(s), rows, cols, _stream())
     _check("fp8_quantize_smooth", st)
@@ -585,7 +645,7 @@ def fp8_quantize_smooth(x, smooth, mode: str = "div") -> Tuple:
 
 
 # ---------------------------------------------------------------------------
-# torch.library registration (reference :428-479)
+# torch.ops.kernel_craft (reference :428-479)
 # ---------------------------------------------------------------------------
 
 SCHEMAS = {
@@ -606,29 +666,21 @@ SCHEMAS = {
 
 
 def _register_torch_library() -> None:
-    """Register kernel_craft ops in the torch.ops namespace."""
+    """Define SCHEMAS under torch.ops.kernel_craft and bind each to the
+    function of the same name for the CPU and CUDA dispatch keys (CPU
+    tensors then fail the device check inside the op).  The Library objects
+    are kept in module globals: dropping them would unregister the ops."""
     import torch
 
-    lib = torch.library.Library("kernel_craft", "DEF")
-    for schema in SCHEMAS.values():
-        lib.define(schema)
-    impl = torch.library.Library("kernel_craft", "IMPL")
-    fns = {
-        "flash_attention": flash_attention,
-        "paged_attention": paged_attention,
-        "int4_dequantize": int4_dequantize,
-        "int4_gemv": int4_gemv,
-        "fp8_quantize": fp8_quantize,
-        "fp8_dequantize": fp8_dequantize,
-        "speculative_verify": speculative_verify,
-    }
-    # Registered for both keys as in the reference; CPU tensors are rejected
-    # by _on_gpu inside each op.
-    for device in ("CPU", "CUDA"):
-        for name, fn in fns.items():
-            impl.impl(name, fn, device)
-    globals()["_torch_lib_def"] = lib
-    globals()["_torch_lib_impl"] = impl
+    defs = torch.library.Library("kernel_craft", "DEF")
+    impls = torch.library.Library("kernel_craft", "IMPL")
+    ops = globals()
+    for name, schema in SCHEMAS.items():
+        defs.define(schema)
+        for key in ("CPU", "CUDA"):
+            impls.impl(name, ops[name], key)
+    ops["_torch_lib_def"] = defs
+    ops["_torch_lib_impl"] = impls
 
 
 try:

@@ -15,9 +15,10 @@
 //    reads whatever buffer it is given;
 //  * a launcher that reports an error (kc_get_last_error) raises
 //    RuntimeError with the library's message; a failed HIP call too;
+//  * `rmsnorm` (:759-800,873) runs the library's launch_rmsnorm;
 //  * the functions outside this path (attention, speculative decoding,
-//    collectives, Mamba, RMSNorm) are registered under their names and
-//    raise NotImplementedError, as the library's C stubs report
+//    collectives, Mamba) are registered under their names and raise
+//    NotImplementedError, as the library's C stubs report
 //    KC_ERR_NOT_IMPLEMENTED.
 #include <hip/hip_runtime_api.h>
 #include <pybind11/numpy.h>

@@ -162,11 +162,97 @@ def test_cpu_tensors_rejected():
         torch.ops.kernel_craft.fp8_quantize(x, True)
 
 
-def test_otel_span_noop_records_attributes():
+def test_otel_local_spans_record_only_inside_a_recorder():
+    """Without opentelemetry-api, spans are local records: attributes (and
+    device timing) only while a recorded_spans() block collects them."""
     import kernel_craft_otel as otel
     importlib.reload(otel)
+    if otel._HAS_OTEL_API:
+        pytest.skip("opentelemetry-api is installed: spans come from OTEL")
     with otel.kernel_span("int4_gemv", rows=256, cols=512, group_size=128) as span:
         pass
-    if not otel._HAS_OTEL_API:
-        assert span.attributes == {"rows": 256, "cols": 512, "group_size": 128}
+    assert not span.is_recording() and span.attributes == {}
+    with otel.recorded_spans() as spans:
+        with otel.kernel_span("int4_gemv", rows=256, cols=512, group_size=128):
+            with otel.kernel_span("fp8_quantize", rows=16, cols=128, per_token=True):
+                pass
+    assert [s.name for s in spans] == ["fp8_quantize", "int4_gemv"]
+    assert spans[1].attributes == {"rows": 256, "cols": 512, "group_size": 128}
+    assert spans[0].attributes["per_token"] is True
+    # no GPU here: no device timing, so no kernel.cuda_ms
+    assert otel.CUDA_MS_ATTR not in spans[0].attributes
+    assert spans[0].end_ns >= spans[0].start_ns
     otel.setup_tracing()   # no-op without opentelemetry; must not raise
+
+
+def test_otel_timer_skips_capture_and_missing_gpu(monkeypatch):
+    """Device timing is never attempted while the stream is being captured
+    into a graph, nor without a visible GPU."""
+    import kernel_craft_otel as otel
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    assert otel._DeviceTimer.begin() is None
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    assert otel._DeviceTimer.begin() is None
+
+
+def test_bridge_span_fallback_accepts_attributes(tmp_path):
+    """If the tracing module cannot be imported, the bridge's stand-in span
+    takes the same keyword attributes and does nothing."""
+    code = (
+        "import sys, builtins; sys.path.insert(0, %r)\n"
+        "real = builtins.__import__\n"
+        "def imp(name, *a, **k):\n"
+        "    if name == 'kernel_craft_otel': raise ImportError(name)\n"
+        "    return real(name, *a, **k)\n"
+        "builtins.__import__ = imp\n"
+        "import kernel_craft_torch_ops as o\n"
+        "with o.kernel_span('int4_gemv', rows=1, cols=2, group_size=3) as s:\n"
+        "    print('ok', s)\n" % str(kc_abi.ROOT / "kernel-craft_amd" / "python"))
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True)
+    assert "ok None" in out.stdout, out.stderr
+
+
+@pytest.mark.parametrize("call, match", [
+    (lambda: ops.int4_gemv(torch.zeros(8, 64, dtype=torch.uint8), torch.zeros(8, 1),
+                           torch.zeros(8, 0, dtype=torch.uint8),
+                           torch.zeros(128, dtype=torch.float16), 8, 128, 128), "dtype"),
+    (lambda: ops.int4_gemv(torch.zeros(8, 64, dtype=torch.uint8), torch.zeros(8, 1),
+                           torch.zeros(8, 0, dtype=torch.uint8), torch.zeros(64), 8, 128, 128),
+     "elements"),
+    (lambda: ops.int4_gemv_bf16(torch.zeros(8, 64, dtype=torch.uint8), torch.zeros(8, 1),
+                                torch.zeros(8, 0, dtype=torch.uint8), torch.zeros(128),
+                                8, 128, 128), "dtype"),
+    (lambda: ops.int4_gemv_bf16(torch.zeros(8, 32, dtype=torch.uint8), torch.zeros(8, 1),
+                                torch.zeros(8, 0, dtype=torch.uint8),
+                                torch.zeros(128, dtype=torch.bfloat16), 8, 128, 128), "elements"),
+    (lambda: ops.int4_gemm_bf16(torch.zeros(8, 64, dtype=torch.uint8), torch.zeros(8, 1),
+                                torch.zeros(8, 1, dtype=torch.uint8),
+                                torch.zeros(4, 128, dtype=torch.bfloat16), 8, 128, 64), "scales"),
+    (lambda: ops.rmsnorm_int4_gemv_bf16(torch.zeros(128, dtype=torch.float16),
+                                        torch.zeros(128, dtype=torch.bfloat16),
+                                        torch.zeros(8, 64, dtype=torch.uint8), torch.zeros(8, 1),
+                                        torch.zeros(8, 0, dtype=torch.uint8), 8, 128, 128),
+     "dtype"),
+    (lambda: ops.fp8_quantize_rows(torch.zeros(4, 64, dtype=torch.float16)), "dtype"),
+    (lambda: ops.col_absmax(torch.zeros(4, 64, dtype=torch.float16)), "dtype"),
+    (lambda: ops.fp8_quantize_smooth(torch.zeros(4, 64, dtype=torch.float16), torch.ones(64)),
+     "dtype"),
+    (lambda: ops.fp8_quantize_smooth(torch.zeros(4, 64), torch.ones(64), mode="mul"), "dtype"),
+    (lambda: ops.fp8_quantize_smooth(torch.zeros(4, 64, dtype=torch.bfloat16), torch.ones(32)),
+     "elements"),
+    (lambda: ops.fp8_quantize(torch.zeros(4, 64, dtype=torch.bfloat16)), "dtype"),
+    (lambda: ops.fp8_dequantize(torch.zeros(4, 64, dtype=torch.int8), torch.ones(3), 4, 64),
+     "elements"),
+    (lambda: ops.fp8_gemm_w8a8(torch.zeros(4, 64, dtype=torch.int8), torch.ones(4),
+                               torch.zeros(8, 32, dtype=torch.int8), torch.ones(8)), "share K"),
+    (lambda: ops.smooth_factors(torch.ones(8), torch.ones(7)), "elements"),
+    (lambda: ops.rmsnorm(torch.zeros(2, 64, dtype=torch.float16), torch.ones(64)), "dtype"),
+])
+def test_bridge_validates_inputs_before_launch(call, match):
+    """Wrong dtypes and sizes are rejected on the host with ValueError before
+    any pointer reaches a kernel (a bf16 read of an fp16 buffer is fine, an
+    fp32 read of it runs past its end)."""
+    with pytest.raises(ValueError, match=match):
+        call()

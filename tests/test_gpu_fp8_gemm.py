@@ -152,3 +152,25 @@ def test_argument_errors(gpu):
     assert st == 1
     L.kc_get_last_error()
     assert L.kc_gemm_fp8_w8a8_bf16(d, d, d, d, d, 0, 4, 16, None) == 0
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+def test_empty_contraction_writes_zeros(gpu, bf16):
+    """K == 0: Y is the empty sum, 0, for every (m, n); the GEMM kernel (whose
+    prologue always loads a first K step) is not launched."""
+    torch = gpu
+    L = kc_abi.lib()
+    M, N = 37, 301   # M * N odd: the last element is a lone half word in bf16
+    dt = torch.bfloat16 if bf16 else torch.float32
+    y = torch.full((M, N), 7.0, dtype=dt, device="cuda")
+    sx = torch.ones(M, device="cuda")
+    sw = torch.ones(N, device="cuda")
+    qx = torch.empty(M, 0, dtype=torch.int8, device="cuda")
+    qw = torch.empty(N, 0, dtype=torch.int8, device="cuda")
+    fn = L.kc_gemm_fp8_w8a8_bf16 if bf16 else L.kc_gemm_fp8_w8a8_f32
+    for _ in range(2):
+        st = fn(ptr(qx), ptr(sx), ptr(qw), ptr(sw), ptr(y), M, N, 0, stream())
+        assert st == 0, L.kc_last_error_string()
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(y).item() == 0
+        y.fill_(-3.0)
