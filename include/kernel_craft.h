@@ -138,7 +138,11 @@ int kc_gemv_int4_bf16_chain(const kc_gemv_op* ops, int n_ops, kc_stream_t stream
 
 /* RMSNorm with bf16 input, weight and output (fp32 arithmetic, output
  * rounded to nearest even): the bf16 counterpart of launch_rmsnorm,
- * rmsnorm.cu:40-70.  x, y [rows, D]; g [D]. */
+ * rmsnorm.cu:40-70.  x, y [rows, D]; g [D].  Both RMSNorms sum the squares
+ * in one fixed order: lane l of 64 accumulates, with one FMA each, the
+ * elements i with floor(i / P) mod 64 == l (P = 4 fp32, 8 bf16 values per 16
+ * bytes) in increasing i, then the 64 sums meet in a xor butterfly (offsets
+ * 32, 16, ..., 1). */
 int kc_rmsnorm_bf16(const uint16_t* d_x, const uint16_t* d_g, uint16_t* d_y,
                     int rows, int D, float eps, kc_stream_t stream);
 
@@ -156,6 +160,20 @@ int kc_rmsnorm_gemv_int4_bf16(const uint16_t* d_h, const uint16_t* d_gamma,
                               const float* d_scales, const uint8_t* d_zeros,
                               uint16_t* d_y, int rows, int cols,
                               int group_size, kc_stream_t stream);
+
+/* The RMSNorm in front of an FP8 linear, fused into its per-token
+ * quantizer (no counterpart in the reference, where rmsnorm.cu:83-88 and
+ * fp8_quant.cu:201-226 are two launches with the normalized rows in memory
+ * between them):
+ *   y[r, i]   = bf16((gamma[i] * h[r, i]) * rms_inv_r)     (kc_rmsnorm_bf16)
+ *   scales[r] = absmax_r(y) / 448 (1 for an all-zero row)
+ *   codes     = E4M3_rne(clamp(y / scales[r], +-448))     (kc_quantize_fp8_per_token_bf16)
+ * h [rows, D] bf16, gamma [D] bf16, codes [rows, D] int8 bit patterns, scales
+ * [rows] fp32.  Bit-identical to kc_rmsnorm_bf16 followed by
+ * kc_quantize_fp8_per_token_bf16 on its output.  D == 0 writes nothing. */
+int kc_rmsnorm_quantize_fp8_bf16(const uint16_t* d_h, const uint16_t* d_gamma,
+                                 float eps, int8_t* d_codes, float* d_scales,
+                                 int64_t rows, int64_t D, kc_stream_t stream);
 
 /* GPTQ / AWQ INT4 checkpoints to the layout above (no counterpart in the
  * reference, which only describes its format as GPTQ/AWQ-style,

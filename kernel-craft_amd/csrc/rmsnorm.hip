@@ -1,5 +1,6 @@
-// rmsnorm.hip -- RMSNorm on gfx950 (MI355X), the op in front of a decoder
-// layer's first GEMV.
+// rmsnorm.hip -- RMSNorm on gfx950 (MI355X), the op in front of each
+// quantized linear of a decoder layer, and its fusion into the FP8 per-token
+// quantizer.
 //
 // The reference (rmsnorm.cu:40-70) computes, per row x of length D,
 //     rms_inv = rsqrtf(sum_i x_i^2 / D + eps),   y_i = g_i * x_i * rms_inv
@@ -11,9 +12,18 @@
 // square root, the expression of the reference's CPU check
 // (tests/test_mamba_ops.cpp:89-101); the CUDA kernel's rsqrtf differs from
 // it by a few ulp.  The product is evaluated as (g_i * x_i) * rms_inv, in
-// the reference's order.  Rows whose pointers or D are not 16-byte
-// granular take a scalar loop with the same arithmetic.
-#include "kc_common.hpp"
+// the reference's order.
+//
+// Summation order (every kernel here, so results do not depend on the
+// route a shape takes): with P values per 16-byte slot (4 fp32, 8 bf16),
+// lane l accumulates, with one FMA each, the squares of the elements i with
+// floor(i / P) mod 64 == l in increasing i; the 64 lane sums are then added
+// by the butterfly v += v[lane ^ o] for o = 32, 16, 8, 4, 2, 1.  Rows whose
+// pointers or D are not 16-byte granular take a scalar loop that visits the
+// elements in the same order.
+#include <type_traits>
+
+#include "fp8_common.hpp"
 
 namespace {
 
@@ -117,6 +127,26 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_wave_kernel(const typename E
     }
 }
 
+// Sum of squares of a row in the canonical order (see the header): lane
+// `lane` of the wave takes the P-element slots lane, lane + 64, ...
+template <bool BF16>
+__device__ __forceinline__ float row_sumsq_scalar(const typename Elem<BF16>::T* x, int64_t base,
+                                                  int D, int lane) {
+    constexpr int P = Elem<BF16>::kPerSlot;
+    float ss = 0.0f;
+    for (int s = lane; s * P < D; s += kWave) {
+#pragma unroll
+        for (int e = 0; e < P; ++e) {
+            const int i = s * P + e;
+            if (i < D) {
+                const float v = Elem<BF16>::get(x, base + i);
+                ss = fmaf(v, v, ss);
+            }
+        }
+    }
+    return kc::wave_sum(ss);
+}
+
 // Any D and alignment: two passes over the row (the second from the cache).
 template <bool BF16>
 __global__ __launch_bounds__(kThreads) void rmsnorm_generic_kernel(const typename Elem<BF16>::T* __restrict__ x,
@@ -127,12 +157,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_generic_kernel(const typenam
     const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
     if (row >= rows) return;
     const int64_t base = static_cast<int64_t>(row) * D;
-    float ss = 0.0f;
-    for (int i = lane; i < D; i += kWave) {
-        const float v = Elem<BF16>::get(x, base + i);
-        ss = fmaf(v, v, ss);
-    }
-    ss = kc::wave_sum(ss);
+    const float ss = row_sumsq_scalar<BF16>(x, base, D, lane);
     const float rms_inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
     for (int i = lane; i < D; i += kWave)
         Elem<BF16>::put(y, base + i, (Elem<BF16>::get(g, i) * Elem<BF16>::get(x, base + i)) * rms_inv);
@@ -158,6 +183,118 @@ int rmsnorm(const char* fn, const typename Elem<BF16>::T* x, const typename Elem
     return kc::check_launch(fn);
 }
 
+// ---------------------------------------------------------------------------
+// RMSNorm -> FP8 per-token quantization in one pass (bf16 h and gamma):
+//   y_i          = bf16((gamma_i * h_i) * rms_inv)      as kc_rmsnorm_bf16
+//   codes, scale = per-token E4M3 of the row y          as kc_quantize_fp8_per_token_bf16
+// rms_inv uses the canonical summation order; y is rounded to bf16 and
+// quantized from registers, so the normalized row never goes to memory.
+// Every y is a rounded product, so a NaN among them is quiet and the absmax
+// (fmaxf from 0) skips it, as the quantizer's does; it then encodes to +448.
+// ---------------------------------------------------------------------------
+
+// y of 8 values (one slot) as packed bf16, from h and gamma slots.
+__device__ __forceinline__ u32x4 norm_slot(const u32x4 hv, const u32x4 gv, float rms_inv) {
+    float v[8], g[8];
+    unpack<true>(hv, v);
+    unpack<true>(gv, g);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (g[e] * v[e]) * rms_inv;
+    return pack<true>(v);
+}
+
+__device__ __forceinline__ float absmax_bf16x8(float m, const u32x4 y) {
+    using kc::fp8::absmax4;
+    using kc::fp8::bf16x4_to_f32;
+    return absmax4(absmax4(m, bf16x4_to_f32(y.x, y.y)), bf16x4_to_f32(y.z, y.w));
+}
+
+// Vector path: D % 8 == 0, 16-byte aligned h and gamma, 8-byte aligned codes,
+// D <= NS * 512.  One wave per row, lane l holding slots l, l + 64, ...
+template <int NS>
+__global__ __launch_bounds__(kThreads) void rmsnorm_fp8_wave_kernel(
+    const uint16_t* __restrict__ h, const uint16_t* __restrict__ gamma, int8_t* __restrict__ out,
+    float* __restrict__ scales, int64_t rows, int D, float eps) {
+    using namespace kc::fp8;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int nslots = D / 8;
+    const u32x4* hs = reinterpret_cast<const u32x4*>(h + row * D);
+    const u32x4* gs = reinterpret_cast<const u32x4*>(gamma);
+    u32x4 xv[NS], gv[NS];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const int s = lane + j * kWave;
+        xv[j] = s < nslots ? __builtin_nontemporal_load(hs + s) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const int s = lane + j * kWave;
+        gv[j] = s < nslots ? gs[s] : u32x4{0u, 0u, 0u, 0u};
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        float v[8];
+        unpack<true>(xv[j], v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+    }
+    ss = kc::wave_sum(ss);
+    const float rms_inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        // Slots past the row hold h = gamma = 0 and give y = 0: no effect on
+        // the absmax, and they are not stored.
+        xv[j] = norm_slot(xv[j], gv[j], rms_inv);
+        m = absmax_bf16x8(m, xv[j]);
+    }
+    const RowDiv d = row_div(kc::wave_max(m));
+    if (lane == 0) scales[row] = d.s;
+    u32x2* dst = reinterpret_cast<u32x2*>(out + row * D);
+    auto emit = [&](auto fast) {
+        constexpr bool F = decltype(fast)::value;
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+            const int s = lane + j * kWave;
+            if (s < nslots) {
+                const u32x2 o{e4m3x4_div<F>(bf16x4_to_f32(xv[j].x, xv[j].y), d),
+                              e4m3x4_div<F>(bf16x4_to_f32(xv[j].z, xv[j].w), d)};
+                __builtin_nontemporal_store(o, dst + s);
+            }
+        }
+    };
+    if (d.fast) emit(std::true_type{});
+    else emit(std::false_type{});
+}
+
+// Any D and alignment: the sum of squares in the canonical order, then two
+// passes recomputing y (absmax, codes), all from the row in the cache.
+__global__ __launch_bounds__(kThreads) void rmsnorm_fp8_generic_kernel(
+    const uint16_t* __restrict__ h, const uint16_t* __restrict__ gamma, int8_t* __restrict__ out,
+    float* __restrict__ scales, int64_t rows, int D, float eps) {
+    using namespace kc::fp8;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int64_t base = row * D;
+    const float ss = row_sumsq_scalar<true>(h, base, D, lane);
+    const float rms_inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+    auto y = [&](int i) {
+        const float v = (kc::bf16_to_f32(gamma[i]) * kc::bf16_to_f32(h[base + i])) * rms_inv;
+        return kc::bf16_to_f32(kc::f32_to_bf16(v));
+    };
+    float m = 0.0f;
+    for (int i = lane; i < D; i += kWave) m = fmaxf(m, fabsf(y(i)));
+    const RowDiv d = row_div(kc::wave_max(m));
+    if (lane == 0) scales[row] = d.s;
+    for (int i = lane; i < D; i += kWave)
+        out[base + i] = static_cast<int8_t>(e4m3x1(d.fast ? div_scale<true>(y(i), d)
+                                                          : div_scale<false>(y(i), d)));
+}
+
 }  // namespace
 
 // rmsnorm.cu:83-88: asynchronous, like the reference's launcher (it does not
@@ -170,4 +307,37 @@ extern "C" void launch_rmsnorm(const float* d_x, const float* d_g, float* d_y, i
 extern "C" int kc_rmsnorm_bf16(const uint16_t* d_x, const uint16_t* d_g, uint16_t* d_y, int rows,
                                int D, float eps, kc_stream_t stream) {
     return rmsnorm<true>("kc_rmsnorm_bf16", d_x, d_g, d_y, rows, D, eps, stream);
+}
+
+extern "C" int kc_rmsnorm_quantize_fp8_bf16(const uint16_t* d_h, const uint16_t* d_gamma,
+                                            float eps, int8_t* d_codes, float* d_scales,
+                                            int64_t rows, int64_t D, kc_stream_t stream) {
+    const char* fn = "kc_rmsnorm_quantize_fp8_bf16";
+    if (rows < 0 || D < 0)
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: negative shape rows=%lld D=%lld", fn,
+                             (long long)rows, (long long)D);
+    if (D > INT32_MAX || rows > (int64_t{INT32_MAX} * kRowsPerBlock))
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: rows=%lld D=%lld too large", fn,
+                             (long long)rows, (long long)D);
+    if (rows == 0 || D == 0) return KC_SUCCESS;
+    if (!d_h || !d_gamma || !d_codes || !d_scales)
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: null device pointer", fn);
+    const unsigned grid = static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+    const int d = static_cast<int>(D);
+    const bool vec = D % 8 == 0 && kc::aligned(d_h, 16) && kc::aligned(d_gamma, 16) &&
+                     kc::aligned(d_codes, 8);
+    const int64_t ns = (D / 8 + kWave - 1) / kWave;
+    if (vec && ns <= 4)
+        rmsnorm_fp8_wave_kernel<4><<<grid, kThreads, 0, stream>>>(d_h, d_gamma, d_codes, d_scales,
+                                                                  rows, d, eps);
+    else if (vec && ns <= 8)
+        rmsnorm_fp8_wave_kernel<8><<<grid, kThreads, 0, stream>>>(d_h, d_gamma, d_codes, d_scales,
+                                                                  rows, d, eps);
+    else if (vec && ns <= 16)
+        rmsnorm_fp8_wave_kernel<16><<<grid, kThreads, 0, stream>>>(d_h, d_gamma, d_codes,
+                                                                   d_scales, rows, d, eps);
+    else
+        rmsnorm_fp8_generic_kernel<<<grid, kThreads, 0, stream>>>(d_h, d_gamma, d_codes, d_scales,
+                                                                  rows, d, eps);
+    return kc::check_launch(fn);
 }

@@ -136,6 +136,7 @@ PROTOTYPES = {
     "kc_quantize_fp8_smooth_mul_bf16": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp], _i),
     "kc_rmsnorm_bf16": ([_vp, _vp, _vp, _i, _i, _f, _vp], _i),
     "kc_rmsnorm_gemv_int4_bf16": ([_vp, _vp, _f, _vp, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
+    "kc_rmsnorm_quantize_fp8_bf16": ([_vp, _vp, _f, _vp, _vp, _i64, _i64, _vp], _i),
 }
 
 
@@ -166,16 +167,18 @@ def _ptr(t) -> ctypes.c_void_p:
 
 def _arg(name: str, t, dtypes=None, numel: Optional[int] = None):
     """``t`` made contiguous after checking that it has one of ``dtypes``
-    and holds ``numel`` elements; ValueError otherwise.  Every op checks all
-    of its arguments this way, then their device with ``_on_gpu``, before
-    it allocates or launches anything."""
+    and holds at least ``numel`` elements (what the kernels read or write
+    through it); ValueError otherwise.  Every op checks all of its arguments
+    this way, then their device with ``_on_gpu``, before it allocates or
+    launches anything."""
     if dtypes is not None:
         allowed = dtypes if isinstance(dtypes, tuple) else (dtypes,)
         if t.dtype not in allowed:
             raise ValueError(f"{name} has dtype {t.dtype}; expected "
                              f"{' or '.join(str(d) for d in allowed)}")
-    if numel is not None and t.numel() != numel:
-        raise ValueError(f"{name} holds {t.numel()} elements; the shape arguments need {numel}")
+    if numel is not None and t.numel() < numel:
+        raise ValueError(f"{name} holds {t.numel()} elements; the shape arguments need "
+                         f"at least {numel}")
     return t.contiguous()
 
 
@@ -188,16 +191,19 @@ def _on_gpu(op: str, *tensors) -> None:
 
 
 def _int4_weights(op: str, packed, scales, zeros, rows: int, cols: int, group_size: int):
-    """Validated (packed, scales, zeros) of an INT4 layer [rows, cols]: the
-    reference layout, packed [rows, cols/2] u8, scales [rows, G] fp32,
-    zeros [rows, G/2] u8 with G = cols / group_size.  Bad shape arguments
-    are left to the library, which rejects them with a message."""
+    """Validated (packed, scales, zeros) of an INT4 layer [rows, cols] in the
+    reference layout: packed [rows, cols/2] u8, scales [rows, G] fp32 and
+    zero bytes read at row stride floor(G/2) (quant_int4.cu:93,152), so the
+    last row reaches byte (rows-1)*floor(G/2) + (G-1)/2, with
+    G = cols / group_size.  Bad shape arguments are left to the library,
+    which rejects them with a message."""
     import torch
-    G = cols // group_size if group_size > 0 else 0
-    ok = rows >= 0 and cols >= 0 and group_size > 0
+    ok = rows > 0 and cols > 0 and group_size > 0
+    G = cols // group_size if ok else 0
+    zneed = (rows - 1) * (G // 2) + (G - 1) // 2 + 1 if ok and G > 0 else 0
     return (_arg(f"{op}: packed", packed, torch.uint8, rows * (cols // 2) if ok else None),
             _arg(f"{op}: scales", scales, torch.float32, rows * G if ok else None),
-            _arg(f"{op}: zeros", zeros, torch.uint8, rows * (G // 2) if ok else None))
+            _arg(f"{op}: zeros", zeros, torch.uint8, zneed))
 
 
 def _check(name: str, status: Optional[int] = None) -> None:
@@ -572,6 +578,26 @@ def rmsnorm_int4_gemv_bf16(h, gamma, packed, scales, zeros, rows: int, cols: int
                                                   group_size, _stream())
     _check("rmsnorm_int4_gemv_bf16", st)
     return y
+
+
+def rmsnorm_fp8_quantize(h, gamma, eps: float = 1e-6) -> Tuple:
+    """RMSNorm of bf16 h [T, D] with bf16 gamma [D], quantized per token to
+    FP8 in one pass: (int8 codes [T, D], fp32 scales [T]), the same bits as
+    fp8_quantize_rows(rmsnorm(h, gamma, eps)) (kc_rmsnorm_quantize_fp8_bf16)."""
+    import torch
+    h = _arg("rmsnorm_fp8_quantize: h", h, torch.bfloat16)
+    if h.dim() != 2:
+        raise ValueError("rmsnorm_fp8_quantize: h must be [T, D]")
+    T, D = h.shape
+    gamma = _arg("rmsnorm_fp8_quantize: gamma", gamma, torch.bfloat16, D)
+    _on_gpu("rmsnorm_fp8_quantize", h, gamma)
+    q = torch.empty(T, D, dtype=torch.int8, device=h.device)
+    s = torch.empty(T, dtype=torch.float32, device=h.device)
+    with kernel_span("rmsnorm_fp8_quantize", rows=T, cols=D):
+        st = _get_lib().kc_rmsnorm_quantize_fp8_bf16(_ptr(h), _ptr(gamma), eps, _ptr(q), _ptr(s),
+                                                     T, D, _stream())
+    _check("rmsnorm_fp8_quantize", st)
+    return q, s
 
 
 def fp8_quantize_rows(x) -> Tuple:

@@ -416,3 +416,66 @@ void kco_rmsnorm_bf16(const uint16_t* x, const uint16_t* g, uint16_t* y,
             y[r * D + i] = kco_f32_to_bf16(kco_bf16_to_f32(g[i]) * kco_bf16_to_f32(xr[i]) * rms_inv);
     }
 }
+
+/* Sum of squares of one row in the library's fixed order (extension; the
+ * reference's kernel sums in its own thread order, rmsnorm.cu:48-62, and its
+ * CPU check in index order): lane l in [0, 64) accumulates, with one fused
+ * multiply-add each, the elements i with floor(i / P) mod 64 == l in
+ * increasing i, where P is the number of values in 16 bytes; the 64 lane sums
+ * are then combined by the butterfly p[l] = p[l] + p[l ^ o], o = 32, ..., 1,
+ * after which every lane holds the same value. */
+static float sumsq_lanes(const float* v, int64_t D, int P) {
+    float p[64];
+    for (int l = 0; l < 64; ++l) {
+        float s = 0.0f;
+        for (int64_t slot = l; slot * P < D; slot += 64)
+            for (int e = 0; e < P && slot * P + e < D; ++e) {
+                const float x = v[slot * P + e];
+                s = fmaf(x, x, s);
+            }
+        p[l] = s;
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        float q[64];
+        for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ o];
+        memcpy(p, q, sizeof p);
+    }
+    return p[0];
+}
+
+/* kco_rmsnorm_f32 / kco_rmsnorm_bf16 with the sum of squares in the fixed
+ * order above (the library's launch_rmsnorm / kc_rmsnorm_bf16); everything
+ * else is the same expression: rms_inv = 1 / sqrt(ss / D + eps),
+ * y = (g * x) * rms_inv. */
+void kco_rmsnorm_f32_lanes(const float* x, const float* g, float* y, int64_t rows,
+                           int64_t D, float eps) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * D;
+        const float rms_inv = 1.0f / sqrtf(sumsq_lanes(xr, D, 4) / (float)D + eps);
+        for (int64_t i = 0; i < D; ++i) y[r * D + i] = g[i] * xr[i] * rms_inv;
+    }
+}
+
+void kco_rmsnorm_bf16_lanes(const uint16_t* x, const uint16_t* g, uint16_t* y,
+                            int64_t rows, int64_t D, float eps, float* row_tmp) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint16_t* xr = x + r * D;
+        for (int64_t i = 0; i < D; ++i) row_tmp[i] = kco_bf16_to_f32(xr[i]);
+        const float rms_inv = 1.0f / sqrtf(sumsq_lanes(row_tmp, D, 8) / (float)D + eps);
+        for (int64_t i = 0; i < D; ++i)
+            y[r * D + i] = kco_f32_to_bf16(kco_bf16_to_f32(g[i]) * row_tmp[i] * rms_inv);
+    }
+}
+
+/* Extension: RMSNorm -> FP8 per-token quantization, defined as the
+ * composition kco_rmsnorm_bf16_lanes, then kco_quantize_fp8_per_token_bf16 of
+ * its bf16 output, row by row (the library's kc_rmsnorm_quantize_fp8_bf16).
+ * row_tmp holds D floats, row_y D bf16 values. */
+void kco_rmsnorm_quantize_fp8_bf16(const uint16_t* h, const uint16_t* g, float eps,
+                                   int8_t* out, float* scales, int64_t rows, int64_t D,
+                                   float* row_tmp, uint16_t* row_y) {
+    for (int64_t r = 0; r < rows; ++r) {
+        kco_rmsnorm_bf16_lanes(h + r * D, g, row_y, 1, D, eps, row_tmp);
+        kco_quantize_fp8_per_token_bf16(row_y, out + r * D, scales + r, 1, D);
+    }
+}

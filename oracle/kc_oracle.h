@@ -89,6 +89,19 @@ void kco_rmsnorm_f32(const float* x, const float* g, float* y, int64_t rows,
 void kco_rmsnorm_bf16(const uint16_t* x, const uint16_t* g, uint16_t* y,
                       int64_t rows, int64_t D, float eps);
 
+/* The same with the sum of squares in the library's fixed order (lane l of
+ * 64 takes the 16-byte slots l, l + 64, ... with one FMA per element, then a
+ * xor butterfly); row_tmp holds D floats.  Extension. */
+void kco_rmsnorm_f32_lanes(const float* x, const float* g, float* y, int64_t rows,
+                           int64_t D, float eps);
+void kco_rmsnorm_bf16_lanes(const uint16_t* x, const uint16_t* g, uint16_t* y,
+                            int64_t rows, int64_t D, float eps, float* row_tmp);
+/* Extension: kco_rmsnorm_bf16_lanes then kco_quantize_fp8_per_token_bf16 on
+ * its output, per row (row_tmp: D floats, row_y: D bf16 values). */
+void kco_rmsnorm_quantize_fp8_bf16(const uint16_t* h, const uint16_t* g, float eps,
+                                   int8_t* out, float* scales, int64_t rows, int64_t D,
+                                   float* row_tmp, uint16_t* row_y);
+
 #ifdef __cplusplus
 }
 #endif

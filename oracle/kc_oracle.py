@@ -47,6 +47,10 @@ _SIGS = {
     "kco_quantize_fp8_smooth_mul_bf16": ([_P, _P, _P, _P, _I64, _I64], None),
     "kco_rmsnorm_f32": ([_P, _P, _P, _I64, _I64, ctypes.c_float], None),
     "kco_rmsnorm_bf16": ([_P, _P, _P, _I64, _I64, ctypes.c_float], None),
+    "kco_rmsnorm_f32_lanes": ([_P, _P, _P, _I64, _I64, ctypes.c_float], None),
+    "kco_rmsnorm_bf16_lanes": ([_P, _P, _P, _I64, _I64, ctypes.c_float, _P], None),
+    "kco_rmsnorm_quantize_fp8_bf16": ([_P, _P, ctypes.c_float, _P, _P, _I64, _I64, _P, _P],
+                                      None),
 }
 
 
@@ -198,6 +202,40 @@ def rmsnorm(x, g, eps=1e-6):
     y = np.empty_like(x2)
     fn(_p(x2), _p(g), _p(y), x2.shape[0], x2.shape[1], float(eps))
     return y.reshape(x.shape)
+
+
+def rmsnorm_lanes(x, g, eps=1e-6):
+    """RMSNorm with the sum of squares in the library's fixed lane order
+    (launch_rmsnorm / kc_rmsnorm_bf16): fp32 in, fp32 out; bf16 bit patterns
+    (uint16) in, bf16 bits out."""
+    if np.asarray(x).dtype == np.uint16:
+        x, g = _c(x, np.uint16), _c(g, np.uint16)
+        x2 = x.reshape(-1, x.shape[-1])
+        y = np.empty_like(x2)
+        tmp = np.empty(x2.shape[1], np.float32)
+        lib().kco_rmsnorm_bf16_lanes(_p(x2), _p(g), _p(y), x2.shape[0], x2.shape[1],
+                                     float(eps), _p(tmp))
+    else:
+        x, g = _c(x, np.float32), _c(g, np.float32)
+        x2 = x.reshape(-1, x.shape[-1])
+        y = np.empty_like(x2)
+        lib().kco_rmsnorm_f32_lanes(_p(x2), _p(g), _p(y), x2.shape[0], x2.shape[1],
+                                    float(eps))
+    return y.reshape(x.shape)
+
+
+def rmsnorm_quantize_fp8_bf16(h_bf16, g_bf16, eps=1e-6):
+    """(codes int8 [T, D], scales fp32 [T]) of rmsnorm_lanes(h, g) (bf16)
+    quantized per token, computed row by row in C."""
+    h_bf16, g_bf16 = _c(h_bf16, np.uint16), _c(g_bf16, np.uint16)
+    T, D = h_bf16.shape
+    q = np.empty((T, D), np.int8)
+    s = np.empty(T, np.float32)
+    tmp = np.empty(max(D, 1), np.float32)
+    ytmp = np.empty(max(D, 1), np.uint16)
+    lib().kco_rmsnorm_quantize_fp8_bf16(_p(h_bf16), _p(g_bf16), float(eps), _p(q), _p(s), T, D,
+                                        _p(tmp), _p(ytmp))
+    return q, s
 
 
 def col_absmax(x):

@@ -216,16 +216,24 @@ def test_bridge_span_fallback_accepts_attributes(tmp_path):
 
 @pytest.mark.parametrize("call, match", [
     (lambda: ops.int4_gemv(torch.zeros(8, 64, dtype=torch.uint8), torch.zeros(8, 1),
-                           torch.zeros(8, 0, dtype=torch.uint8),
+                           torch.zeros(8, 1, dtype=torch.uint8),
                            torch.zeros(128, dtype=torch.float16), 8, 128, 128), "dtype"),
     (lambda: ops.int4_gemv(torch.zeros(8, 64, dtype=torch.uint8), torch.zeros(8, 1),
-                           torch.zeros(8, 0, dtype=torch.uint8), torch.zeros(64), 8, 128, 128),
+                           torch.zeros(8, 1, dtype=torch.uint8), torch.zeros(64), 8, 128, 128),
      "elements"),
+    # one group per row: the zero row stride is 0 and every row reads byte 0
+    (lambda: ops.int4_gemv(torch.zeros(8, 64, dtype=torch.uint8), torch.zeros(8, 1),
+                           torch.zeros(8, 0, dtype=torch.uint8), torch.zeros(128), 8, 128, 128),
+     "zeros"),
+    # three groups: stride 1, the last row reads byte 7 + 1
+    (lambda: ops.int4_gemv(torch.zeros(8, 192, dtype=torch.uint8), torch.zeros(8, 3),
+                           torch.zeros(8, dtype=torch.uint8), torch.zeros(384), 8, 384, 128),
+     "zeros"),
     (lambda: ops.int4_gemv_bf16(torch.zeros(8, 64, dtype=torch.uint8), torch.zeros(8, 1),
-                                torch.zeros(8, 0, dtype=torch.uint8), torch.zeros(128),
+                                torch.zeros(8, 1, dtype=torch.uint8), torch.zeros(128),
                                 8, 128, 128), "dtype"),
     (lambda: ops.int4_gemv_bf16(torch.zeros(8, 32, dtype=torch.uint8), torch.zeros(8, 1),
-                                torch.zeros(8, 0, dtype=torch.uint8),
+                                torch.zeros(8, 1, dtype=torch.uint8),
                                 torch.zeros(128, dtype=torch.bfloat16), 8, 128, 128), "elements"),
     (lambda: ops.int4_gemm_bf16(torch.zeros(8, 64, dtype=torch.uint8), torch.zeros(8, 1),
                                 torch.zeros(8, 1, dtype=torch.uint8),
@@ -233,7 +241,7 @@ def test_bridge_span_fallback_accepts_attributes(tmp_path):
     (lambda: ops.rmsnorm_int4_gemv_bf16(torch.zeros(128, dtype=torch.float16),
                                         torch.zeros(128, dtype=torch.bfloat16),
                                         torch.zeros(8, 64, dtype=torch.uint8), torch.zeros(8, 1),
-                                        torch.zeros(8, 0, dtype=torch.uint8), 8, 128, 128),
+                                        torch.zeros(8, 1, dtype=torch.uint8), 8, 128, 128),
      "dtype"),
     (lambda: ops.fp8_quantize_rows(torch.zeros(4, 64, dtype=torch.float16)), "dtype"),
     (lambda: ops.col_absmax(torch.zeros(4, 64, dtype=torch.float16)), "dtype"),

@@ -1,11 +1,13 @@
 """RMSNorm and the fused RMSNorm -> INT4 GEMV on the GPU vs the CPU oracle.
 
-Bars: launch_rmsnorm within the reference tests' own max-abs bars (1e-5 for
-rows of 8 and 64 values, 1e-4 beyond; tests/test_mamba_ops.cpp:219-300,
-test_mamba_bindings.py:251-300) of the oracle, which reproduces the
-reference's CPU check bit for bit.  The kernel sums the squares in another
-order (and with FMA, as nvcc contracts the reference kernel), so a bf16
-output may sit one unit in the last place from the oracle's.  The fused
+Bars: launch_rmsnorm and kc_rmsnorm_bf16 bit for bit against the oracle's
+fixed-order restatement (kco_rmsnorm_*_lanes: the library's summation order,
+with FMA), and within the reference tests' own max-abs bars (1e-5 for rows
+of 8 and 64 values, 1e-4 beyond; tests/test_mamba_ops.cpp:219-300,
+test_mamba_bindings.py:251-300) of the oracle of the reference's CPU check,
+which sums in index order.  The fused RMSNorm -> FP8 quantizer bit for bit
+against the oracle composition (fixed-order RMSNorm, then the per-token
+quantizer on its bf16 output) and against the two library launches.  The fused
 GEMV's bf16 output is held to relative L2 3e-3 of the fp64 GEMV of its own
 bf16 input (bf16(gamma h), scaled by rms_inv), and to the bf16 bar, 1e-2,
 of the unrounded fp64 composition.
@@ -66,6 +68,7 @@ def test_rmsnorm_f32_shapes(gpu, oracle, rows, D, offset):
     g = rng.uniform(0.5, 1.5, D).astype(np.float32)
     y = _rmsnorm_f32(gpu, x, g, 1e-6, offset)
     if rows:
+        np.testing.assert_array_equal(y, oracle.rmsnorm_lanes(x, g, 1e-6))
         exp = oracle.rmsnorm(x, g, 1e-6)
         assert np.max(np.abs(y - exp)) <= 2e-5 * np.max(np.abs(exp))
 
@@ -80,7 +83,8 @@ def test_rmsnorm_unit_and_constant_rows(gpu):
     assert np.max(np.abs(np.sqrt(np.mean(y.astype(np.float64) ** 2, axis=1)) - 1.0)) < 1e-4
 
 
-@pytest.mark.parametrize("rows,D", [(1, 4096), (16, 4096), (7, 8192), (3, 14336), (5, 100)])
+@pytest.mark.parametrize("rows,D", [(1, 4096), (16, 4096), (7, 8192), (3, 14336), (5, 100),
+                                    (4, 20000)])
 def test_rmsnorm_bf16(gpu, oracle, rows, D):
     L = kc_abi.lib()
     rng = np.random.default_rng(D + rows)
@@ -92,6 +96,7 @@ def test_rmsnorm_bf16(gpu, oracle, rows, D):
     st = L.kc_rmsnorm_bf16(ptr(dx), ptr(dg), ptr(dy), rows, D, 1e-5, stream())
     kc_abi.check("kc_rmsnorm_bf16", st)
     gpu.cuda.synchronize()
+    np.testing.assert_array_equal(_bits(dy), oracle.rmsnorm_lanes(xb, gb, 1e-5))
     got = bf16_bits_to_f32(_bits(dy))
     exp = bf16_bits_to_f32(oracle.rmsnorm(xb, gb, 1e-5))
     ulp = np.abs(exp) * 2.0 ** -7 + 1e-30
@@ -193,3 +198,112 @@ def test_rmsnorm_gemv_argument_errors(gpu):
     st = L.kc_rmsnorm_bf16(ptr(dh), ptr(dh), ptr(dy), -1, cols, 1e-5, stream())
     assert st == 1
     L.kc_get_last_error()
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm -> FP8 per-token quantization (kc_rmsnorm_quantize_fp8_bf16)
+# ---------------------------------------------------------------------------
+
+def _norm_fp8(torch, hb, gb, eps=1e-6, offset=0):
+    """kc_rmsnorm_quantize_fp8_bf16 through the C ABI; offset (in elements)
+    moves h, gamma and the codes off their alignment (generic kernel)."""
+    L = kc_abi.lib()
+    T, D = hb.shape
+    hbuf = torch.zeros(T * D + offset, dtype=torch.bfloat16, device="cuda")
+    hbuf[offset:] = _dev_bf16(torch, hb.reshape(-1))
+    gbuf = torch.zeros(D + offset, dtype=torch.bfloat16, device="cuda")
+    gbuf[offset:] = _dev_bf16(torch, gb)
+    qbuf = torch.full((T * D + offset,), 0x55, dtype=torch.int8, device="cuda")
+    s = torch.full((T,), float("nan"), dtype=torch.float32, device="cuda")
+    print(f"kc_rmsnorm_quantize_fp8_bf16 T={T} D={D} offset={offset}", flush=True)
+    st = L.kc_rmsnorm_quantize_fp8_bf16(ptr(hbuf[offset:]), ptr(gbuf[offset:]), eps,
+                                        ptr(qbuf[offset:]), ptr(s), T, D, stream())
+    kc_abi.check("kc_rmsnorm_quantize_fp8_bf16", st)
+    torch.cuda.synchronize()
+    return qbuf[offset:].cpu().numpy().reshape(T, D), s.cpu().numpy()
+
+
+def _special_rows(hb):
+    """Rows the reference's arithmetic treats specially, planted in place."""
+    T, D = hb.shape
+    specials = [
+        np.zeros(D, np.uint16),                                      # zero row
+        np.full(D, 0x8000, np.uint16),                               # -0 row
+        np.where(np.arange(D) == 3, 0x7FC0, hb[0]).astype(np.uint16),  # one quiet NaN
+        np.where(np.arange(D) == 5, 0x7F81, hb[0]).astype(np.uint16),  # one signalling NaN
+        np.where(np.arange(D) == 7, 0xFF80, hb[0]).astype(np.uint16),  # -inf
+        f32_to_bf16_bits(np.full(D, 2.0 ** -70, np.float32)),        # tiny: absmax < 2^-60?
+        np.full(D, 0x7F7F, np.uint16),                               # bf16 max: ss overflows
+        np.where(np.arange(D) % 97 == 0, 0x0001, 0).astype(np.uint16),  # subnormals only
+    ]
+    for i, row in enumerate(specials[:T]):
+        hb[i] = row
+    return hb
+
+
+@pytest.mark.parametrize("T", [1, 7, 4096, 16384])
+@pytest.mark.parametrize("D", [4096, 8192])
+def test_rmsnorm_quantize_fp8_bit_exact(gpu, oracle, T, D):
+    """Codes and scales bit for bit against the oracle composition
+    kco_rmsnorm_bf16_lanes -> kco_quantize_fp8_per_token_bf16, with special
+    rows planted at the top (zero, -0, NaN, sNaN, -inf, tiny, overflowing,
+    subnormal)."""
+    hb = normal_bf16((T, D), seed=T + D, std=2.0)
+    hb = _special_rows(hb)
+    rng = np.random.default_rng(D)
+    gb = f32_to_bf16_bits(rng.uniform(0.25, 2.0, D).astype(np.float32))
+    q, s = _norm_fp8(gpu, hb, gb)
+    eq, es = oracle.rmsnorm_quantize_fp8_bf16(hb, gb, 1e-6)
+    np.testing.assert_array_equal(s, es)
+    np.testing.assert_array_equal(q, eq)
+
+
+@pytest.mark.parametrize("T,D,offset", [(5, 100, 0), (3, 4104, 1), (4, 20000, 0), (9, 512, 0),
+                                        (6, 2048, 0), (2, 8, 0), (3, 1, 0), (0, 64, 0)])
+def test_rmsnorm_quantize_fp8_shapes(gpu, oracle, T, D, offset):
+    """Short rows, rows past 8192 values and unaligned buffers (the generic
+    kernel) keep the same summation order, so the same bits."""
+    hb = normal_bf16((T, D), seed=T * 7 + D, std=1.5)
+    gb = f32_to_bf16_bits(np.random.default_rng(D).uniform(0.5, 1.5, D).astype(np.float32))
+    q, s = _norm_fp8(gpu, hb, gb, 1e-5, offset)
+    if T:
+        eq, es = oracle.rmsnorm_quantize_fp8_bf16(hb, gb, 1e-5)
+        np.testing.assert_array_equal(s, es)
+        np.testing.assert_array_equal(q, eq)
+
+
+def test_rmsnorm_quantize_fp8_equals_two_launches(gpu):
+    """The fused launch equals kc_rmsnorm_bf16 followed by
+    kc_quantize_fp8_per_token_bf16 on its output, bit for bit (cfg4 rows)."""
+    L = kc_abi.lib()
+    T, D = 512, 8192
+    hb = normal_bf16((T, D), seed=77)
+    gb = f32_to_bf16_bits(np.random.default_rng(78).uniform(0.5, 1.5, D).astype(np.float32))
+    q, s = _norm_fp8(gpu, hb, gb, 1e-6)
+    dh, dg = _dev_bf16(gpu, hb), _dev_bf16(gpu, gb)
+    dy = gpu.empty(T, D, dtype=gpu.bfloat16, device="cuda")
+    dq = gpu.empty(T, D, dtype=gpu.int8, device="cuda")
+    ds = gpu.empty(T, dtype=gpu.float32, device="cuda")
+    print("kc_rmsnorm_bf16 + kc_quantize_fp8_per_token_bf16", flush=True)
+    kc_abi.check("kc_rmsnorm_bf16", L.kc_rmsnorm_bf16(ptr(dh), ptr(dg), ptr(dy), T, D, 1e-6,
+                                                      stream()))
+    kc_abi.check("kc_quantize_fp8_per_token_bf16",
+                 L.kc_quantize_fp8_per_token_bf16(ptr(dy), ptr(dq), ptr(ds), T, D, stream()))
+    gpu.cuda.synchronize()
+    np.testing.assert_array_equal(q, dq.cpu().numpy())
+    np.testing.assert_array_equal(s, ds.cpu().numpy())
+
+
+def test_rmsnorm_quantize_fp8_argument_errors(gpu):
+    L = kc_abi.lib()
+    d = gpu.zeros(64, dtype=gpu.bfloat16, device="cuda")
+    q = gpu.zeros(64, dtype=gpu.int8, device="cuda")
+    s = gpu.zeros(1, dtype=gpu.float32, device="cuda")
+    L.kc_get_last_error()
+    assert L.kc_rmsnorm_quantize_fp8_bf16(ptr(d), None, 1e-6, ptr(q), ptr(s), 1, 64, stream()) == 1
+    assert b"null" in L.kc_last_error_string()
+    assert L.kc_rmsnorm_quantize_fp8_bf16(ptr(d), ptr(d), 1e-6, ptr(q), ptr(s), -1, 64,
+                                          stream()) == 1
+    L.kc_get_last_error()
+    assert L.kc_rmsnorm_quantize_fp8_bf16(None, None, 1e-6, None, None, 0, 64, stream()) == 0
+    assert L.kc_get_last_error() == 0

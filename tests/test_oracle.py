@@ -14,7 +14,8 @@ import numpy as np
 import pytest
 import torch
 
-from kc_data import bf16_bits_to_f32, f32_to_bf16_bits, make_int4, outlier_activations, rel_l2
+from kc_data import (bf16_bits_to_f32, f32_to_bf16_bits, make_int4, normal_bf16,
+                     outlier_activations, rel_l2)
 
 
 def _kat(golden, name):
@@ -561,3 +562,139 @@ def test_rmsnorm_bf16_is_rounded_f32(oracle):
     yb = oracle.rmsnorm(xb, gb, 1e-5)
     ref = oracle.rmsnorm(bf16_bits_to_f32(xb), bf16_bits_to_f32(gb), 1e-5)
     np.testing.assert_array_equal(yb, f32_to_bf16_bits(ref))
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm in the library's fixed summation order, and its FP8 fusion
+# ---------------------------------------------------------------------------
+
+def _rn32(fr):
+    """A Fraction rounded to the nearest fp32 (ties to even), as np.float32;
+    independent of the oracle (exact rational arithmetic)."""
+    from fractions import Fraction
+    if fr == 0:
+        return np.float32(0.0)
+    sign = -1 if fr < 0 else 1
+    a = abs(fr)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    ulp = Fraction(2) ** (max(e, -126) - 23)
+    q = a / ulp
+    n = q.numerator // q.denominator
+    rem = q - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    v = n * ulp
+    if v >= Fraction(2) ** 128:
+        return np.float32(sign * np.inf)
+    return np.float32(sign * float(v))
+
+
+def _sumsq_lanes_exact(v: np.ndarray, P: int) -> np.float32:
+    """The documented order, restated with exact rationals: lane l takes
+    slots l, l + 64, ... of P values, one correctly rounded FMA per element,
+    then the xor butterfly with correctly rounded adds."""
+    from fractions import Fraction
+    D = v.size
+    p = []
+    for lane in range(64):
+        s = Fraction(0)
+        for slot in range(lane, (D + P - 1) // P, 64):
+            for i in range(slot * P, min(slot * P + P, D)):
+                x = Fraction(float(v[i]))
+                s = Fraction(float(_rn32(x * x + s)))
+        p.append(s)
+    for o in (32, 16, 8, 4, 2, 1):
+        p = [Fraction(float(_rn32(p[lane] + p[lane ^ o]))) for lane in range(64)]
+    return np.float32(float(p[0]))
+
+
+def _rmsnorm_from_ss(x, g, ss, eps):
+    D = x.size
+    rms_inv = np.float32(1.0) / np.sqrt(np.float32(ss) / np.float32(D) + np.float32(eps))
+    return (g.astype(np.float32) * x.astype(np.float32)) * rms_inv
+
+
+def test_rn32_helper():
+    from fractions import Fraction
+    for v in (1.0, -3.5, 1e-40, 3.4e38, 0.1):
+        assert _rn32(Fraction(v)) == np.float32(v)
+    # a tie between two fp32 neighbours goes to the even one
+    one = Fraction(1)
+    assert _rn32(one + Fraction(1, 2 ** 24)) == np.float32(1.0)
+    assert _rn32(one + Fraction(3, 2 ** 24)) == np.float32(1.0 + 2.0 ** -22)
+
+
+@pytest.mark.parametrize("D,P", [(4096, 8), (8192, 8), (1000, 8), (4096, 4), (777, 4)])
+def test_rmsnorm_lanes_order_exact_restatement(oracle, D, P):
+    """kco_rmsnorm_*_lanes against an exact-rational restatement of the
+    documented order (FMA per element, lane slots of P values, butterfly):
+    bit for bit, on rows whose squares span many binades.  A sequential sum
+    (the reference CPU check's order) fails this on these rows."""
+    rng = np.random.default_rng(D + P)
+    x = (rng.standard_normal(D) * np.exp2(rng.integers(-12, 6, D))).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    if P == 8:
+        xb, gb = f32_to_bf16_bits(x), f32_to_bf16_bits(g)
+        xf, gf = bf16_bits_to_f32(xb), bf16_bits_to_f32(gb)
+        ss = _sumsq_lanes_exact(xf, 8)
+        want = f32_to_bf16_bits(_rmsnorm_from_ss(xf, gf, ss, 1e-6))
+        got = oracle.rmsnorm_lanes(xb[None], gb, 1e-6)[0]
+        xs = xf
+    else:
+        ss = _sumsq_lanes_exact(x, 4)
+        want = _rmsnorm_from_ss(x, g, ss, 1e-6)
+        got = oracle.rmsnorm_lanes(x[None], g, 1e-6)[0]
+        xs = x
+    np.testing.assert_array_equal(got, want)
+    seq = np.float32(0.0)                     # index order, multiply then add
+    for v in xs:
+        seq = np.float32(seq + np.float32(v * v))
+    assert seq != ss, "test rows do not separate the orders"
+
+
+def test_rmsnorm_lanes_equals_reference_check_when_sums_are_exact(oracle):
+    """With small integer inputs every partial sum of squares is exact in any
+    order, so the fixed-order RMSNorm must equal the reference CPU check's
+    restatement (pinned bit for bit by the reference KATs) exactly: this pins
+    the rest of the formula (D, eps, the square root, the product order)."""
+    rng = np.random.default_rng(31)
+    for D in (64, 768, 4096, 8192):
+        x = rng.integers(-8, 9, (3, D)).astype(np.float32)
+        g = rng.uniform(0.5, 1.5, D).astype(np.float32)
+        np.testing.assert_array_equal(oracle.rmsnorm_lanes(x, g, 1e-6), oracle.rmsnorm(x, g, 1e-6))
+        xb, gb = f32_to_bf16_bits(x), f32_to_bf16_bits(g)
+        np.testing.assert_array_equal(oracle.rmsnorm_lanes(xb, gb, 1e-5),
+                                      oracle.rmsnorm(xb, gb, 1e-5))
+
+
+@pytest.mark.parametrize("name,tol", [("rms_basic", 1e-5), ("rms_d768", 1e-4), ("rms_d4096", 1e-4),
+                                      ("rms_py_rng3", 1e-5)])
+def test_rmsnorm_lanes_within_reference_bars(oracle, golden, name, tol):
+    """The reference tests' own bars (test_mamba_ops.cpp:219-300,
+    test_mamba_bindings.py:251-262) hold for the fixed order too."""
+    y = oracle.rmsnorm_lanes(golden[f"{name}_x"], golden[f"{name}_g"], 1e-6)
+    assert np.max(np.abs(y - golden[f"{name}_expected"])) < tol
+
+
+def test_rmsnorm_quantize_fp8_is_the_composition(oracle):
+    """kco_rmsnorm_quantize_fp8_bf16 == per-token FP8 of kco_rmsnorm_bf16_lanes'
+    bf16 output, including zero, NaN, infinite and tiny rows."""
+    rng = np.random.default_rng(41)
+    T, D = 12, 4096
+    h = normal_bf16((T, D), seed=42)
+    g = f32_to_bf16_bits(rng.uniform(0.5, 1.5, D).astype(np.float32))
+    h[1] = 0                                    # all-zero row: scale 1, codes 0
+    h[2, 17] = 0x7FC0                           # NaN: the whole row is NaN -> +448
+    h[3, 5] = 0x7F80                            # +inf: inf * 0 -> NaN, others +-0
+    h[4] = f32_to_bf16_bits(np.full(D, 2.0 ** -70, np.float32))  # tiny row
+    h[5, :] = 0x8000                            # -0 row
+    q, s = oracle.rmsnorm_quantize_fp8_bf16(h, g, 1e-6)
+    y = oracle.rmsnorm_lanes(h, g, 1e-6)
+    eq, es = oracle.quantize_fp8_per_token_bf16(y)
+    np.testing.assert_array_equal(q, eq)
+    np.testing.assert_array_equal(s, es)
+    assert s[1] == 1.0 and not q[1].any()
+    assert (q[2].view(np.uint8) == 0x7E).all()
+    assert (q[5].view(np.uint8) == 0x80).all()
