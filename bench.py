@@ -65,16 +65,36 @@ def fp8_bytes(rows: int, cols: int) -> int:
     return rows * cols * 4 + rows * cols + rows * 4
 
 
+GEMV_SOURCES = ("kernel-craft_amd/csrc/quant_int4.hip", "kernel-craft_amd/csrc/int4_decode.hpp",
+                "kernel-craft_amd/csrc/kc_common.hpp")
+
+
+def source_sha256(paths=GEMV_SOURCES) -> str:
+    """sha256 over the dominant kernel's source files, in order."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in paths:
+        h.update((ROOT / rel).read_bytes())
+    return h.hexdigest()
+
+
 def read_traffic(path: Path):
-    """HBM bytes per launch of the dominant kernel, from the committed
-    rocprofv3 --pmc summary (the line `hbm_bytes_per_launch: N`), or None."""
+    """(HBM bytes per launch of the dominant kernel, note) from the committed
+    rocprofv3 --pmc summary: its `hbm_bytes_per_launch: N` line counts only
+    when its `source_sha256:` line matches the sources built now, so that a
+    changed kernel never reports the previous kernel's traffic (None then)."""
     try:
+        fields = {}
         for line in path.read_text().splitlines():
-            if line.strip().startswith("hbm_bytes_per_launch:"):
-                return int(line.split(":", 1)[1].strip())
-    except (OSError, ValueError):
-        pass
-    return None
+            if ":" in line and line.strip().split(":", 1)[0] in ("hbm_bytes_per_launch",
+                                                               "source_sha256"):
+                k, v = line.strip().split(":", 1)
+                fields[k] = v.strip()
+        if fields.get("source_sha256") != source_sha256():
+            return None, f"{path.name}: measured on other kernel sources; re-profile"
+        return int(fields["hbm_bytes_per_launch"]), f"{path.name} (sources match)"
+    except (OSError, ValueError, KeyError):
+        return None, f"{path.name}: unreadable"
 
 
 def log(*a) -> None:
@@ -123,6 +143,72 @@ def hbm(nbytes: int, us: float) -> dict:
     gbs = nbytes / (us * 1e-6) / 1e9
     return {"avg_us": round(us, 3), "bytes": nbytes, "GBps": round(gbs, 1),
             "frac": round(gbs / PEAK_HBM_GBS, 4)}
+
+
+def measure_floors(torch, dev, quick: bool = False) -> dict:
+    """What plain streams achieve on this GPU, as floors for the path's
+    kernels: reads of each GEMV's weight bytes (packed + scales + zeros) and of
+    512 MiB; read+write streams with the FP8 quantizers' 4:1 (fp32 -> E4M3)
+    and 2:1 (bf16 -> E4M3) traffic at the cfg1 / cfg4 sizes; an empty launch.
+    Each is the best over grid sizes and loads in flight per thread
+    (build/libkc_probes.so), timed like the path's kernels (events, backlog,
+    inputs rotated over 1.5 GiB so that the Infinity Cache cannot serve them)."""
+    import ctypes
+    probes = ctypes.CDLL(str(ROOT / "build" / "libkc_probes.so"))
+    probes.kcp_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                       ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    probes.kcp_stream_copy.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                       ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    probes.kcp_empty.argtypes = [ctypes.c_int, ctypes.c_void_p]
+    buf_bytes = 3 << 29                                       # 1.5 GiB
+    buf = torch.empty(buf_bytes, dtype=torch.uint8, device=dev).fill_(3)
+    grids = (512, 1024, 2048, 4096) if quick else (512, 1024, 2048, 4096, 8192)
+    sink = torch.zeros(max(grids) * 256, dtype=torch.int32, device=dev)
+    out = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+
+    def stream() -> int:
+        return torch.cuda.current_stream().cuda_stream
+
+    def best(nbytes, launch_fn, unrolls):
+        nbytes -= nbytes % 16
+        slots = max(1, (buf_bytes - nbytes) // max(nbytes, 1 << 20))
+        reps = 50 if nbytes <= (64 << 20) else 10
+        res = None
+        for grid in grids:
+            for u in unrolls:
+                def launch(j, grid=grid, u=u):
+                    off = (j % (slots + 1)) * (buf_bytes - nbytes) // max(slots, 1)
+                    off -= off % 256
+                    rc = launch_fn(buf.data_ptr() + off, nbytes, grid, u)
+                    if rc:
+                        raise RuntimeError(f"probe launch failed: hipError {rc}")
+                us = time_launches(torch, launch, reps)
+                if res is None or us < res["avg_us"]:
+                    res = {"avg_us": round(us, 3), "grid": grid, "unroll": u}
+        return res
+
+    floors = {"read": {}, "copy": {}}
+    reads = [(nm, n * k // 2 + n * (k // GS) * 4 + n * (k // GS) // 2) for nm, n, k in LLAMA]
+    reads += [("cfg0_weights", 4096 * 2048 + 4096 * 32 * 4 + 4096 * 16),
+              ("cfg3_weights", 28672 * 4096 + 28672 * 64 * 4 + 28672 * 32),
+              ("512MiB", 512 << 20)]
+    for nm, nb in reads:
+        r = best(nb, lambda ptr, n, g, u: probes.kcp_stream_read(ptr, n, sink.data_ptr(), g, u,
+                                                                  stream()), (4, 8, 16))
+        r.update(hbm(nb - nb % 16, r["avg_us"]))
+        floors["read"][nm] = r
+    copies = [("cfg1_fp32_to_e4m3", 4096 * 4096 * 4, 4),
+              ("cfg4_x_bf16_to_e4m3", 16384 * 8192 * 2, 2),
+              ("cfg4_w_bf16_to_e4m3", 28672 * 8192 * 2, 2)]
+    for nm, nb, ratio in copies:
+        r = best(nb, lambda ptr, n, g, u, ratio=ratio: probes.kcp_stream_copy(
+            ptr, n, out.data_ptr(), ratio, g, u, stream()), (1, 4, 8))
+        r.update(hbm(nb + nb // ratio, r["avg_us"]))
+        floors["copy"][nm] = r
+    floors["empty_launch_us"] = round(time_launches(
+        torch, lambda j: probes.kcp_empty(256, stream()), 200), 3)
+    del buf, out, sink
+    return floors
 
 
 def counter_probe(args, torch, lib, dev) -> int:
@@ -187,12 +273,91 @@ def counter_probe(args, torch, lib, dev) -> int:
     return 0
 
 
+def cpu_info() -> tuple:
+    """(threads the CPU legs use, the CPU model): this process's affinity,
+    capped by OMP_NUM_THREADS and at 16 (the GPU box's share of host cores)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    try:
+        n = min(n, int(os.environ.get("OMP_NUM_THREADS", n)))
+    except ValueError:
+        pass
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return max(1, min(n, 16)), model
+
+
+def cpu_baseline(torch, np, layer, xs, layer_bytes: int, seconds: float) -> dict:
+    """The CPU oracle's scalar loops timed on this host, on the same
+    algorithmic-byte basis as the GPU numbers: the decode layer's four INT4
+    GEMVs (the metric), and the cfg1 FP8 per-token quantizer (the reference
+    has no CPU FP8 path, so the oracle's is the baseline).  Each on one
+    thread and on all the threads cpu_info() allows; `seconds` bounds the
+    whole sample."""
+    import kc_oracle
+    threads, model = cpu_info()
+    host = []
+    for i, (_, n, k) in enumerate(LLAMA):
+        p, s, z = layer[i]
+        host.append((p.cpu().numpy(), s.cpu().numpy(), z.cpu().numpy(),
+                     xs[i].view(torch.int16).cpu().numpy().view(np.uint16), n, k))
+    rng = np.random.default_rng(1)
+    x1 = rng.standard_normal((4096, 4096)).astype(np.float32)
+    x1[:, rng.choice(4096, 41, replace=False)] *= np.float32(50.0)
+
+    def run(fn, budget):
+        fn()                                          # warm (pages, threads)
+        count, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            count += 1
+            if time.perf_counter() - t0 >= budget:
+                return count, time.perf_counter() - t0
+
+    def layer_fn(t):
+        return lambda: [kc_oracle.gemv_int4_bf16_f32(p, s, z, xb, n, k, GS, threads=t)
+                        for p, s, z, xb, n, k in host]
+
+    legs = {}
+    for key, t, share in (("single", 1, 0.4), ("all_cores", threads, 0.2)):
+        cnt, el = run(layer_fn(t), seconds * share)
+        legs[key] = {"value": round(cnt * layer_bytes / el / 1e9, 3), "unit": "GB/s",
+                     "threads": t, "sample": f"{cnt} decode layers ({layer_bytes} B each) "
+                                             f"in {el:.2f} s"}
+    fp8 = {}
+    fb = fp8_bytes(4096, 4096)
+    for key, t, share in (("single", 1, 0.25), ("all_cores", threads, 0.15)):
+        cnt, el = run(lambda t=t: kc_oracle.quantize_fp8_per_token(x1, threads=t), seconds * share)
+        fp8[key] = {"value": round(cnt * fb / el / 1e9, 3), "unit": "GB/s", "threads": t,
+                    "sample": f"{cnt} x cfg1 X fp32 [4096, 4096] ({fb} B) in {el:.2f} s"}
+    out = {"value": legs["all_cores"]["value"], "unit": "GB/s", "cores": threads,
+           "kind": "port",
+           "sample": (f"oracle scalar C loops (kco_gemv_int4_bf16_f32, rows split over "
+                      f"{threads} OpenMP threads) over the decode layer's 4 GEMVs: "
+                      f"{legs['all_cores']['sample']}"),
+           "single": legs["single"], "all_cores": legs["all_cores"], "fp8_cfg1": fp8,
+           "cpu_model": model, "affinity_cpus": len(os.sched_getaffinity(0))
+           if hasattr(os, "sched_getaffinity") else None}
+    log(f"# cpu baseline ({model}, {threads} threads): GEMV layer single "
+        f"{legs['single']['value']} GB/s, all {legs['all_cores']['value']} GB/s; fp8 cfg1 single "
+        f"{fp8['single']['value']} GB/s, all {fp8['all_cores']['value']} GB/s")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="bound on the CPU-baseline sample (0 skips it)")
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of HIP graphs")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -201,6 +366,9 @@ def main() -> int:
     ap.add_argument("--quant-probe", action="store_true",
                     help="for rocprofv3 --pmc: launch the cfg1 FP8 per-token quantizer 20 "
                          "times over rotating inputs and the 64 MiB copy 20 times, then exit")
+    ap.add_argument("--floor-probe", action="store_true",
+                    help="measure only the stream floors (reads of each GEMV's weight bytes, "
+                         "quantizer-shaped copies, an empty launch), print them as JSON, exit")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="for rocprofv3 --pmc: launch the cfg3 GEMMs (M 4, 16, 64) 10 times "
                          "each and the FP8 W8A8 GEMM (cfg4 shape) 3 times, then exit")
@@ -225,6 +393,9 @@ def main() -> int:
 
     if args.quant_probe or args.mfma_probe:
         return counter_probe(args, torch, lib, dev)
+    if args.floor_probe:
+        print(json.dumps({"floors": measure_floors(torch, dev)}), flush=True)
+        return 0
 
     # ---- inputs (BASELINE cfg2 distributions), rotated over > 1 GiB --------
     layer_bytes = sum(gemv_bytes(n, k) for _, n, k in LLAMA)
@@ -361,9 +532,10 @@ def main() -> int:
     dom_name, dom_n, dom_k = LLAMA[DOMINANT]
     dom_bytes = gemv_bytes(dom_n, dom_k)
     achieved = dom_bytes / (kernel_us[dom_name] * 1e-6) / 1e9
-    traffic = read_traffic(ROOT / "profiles" / "gemv_int4_bf16_gate_up_traffic.md")
+    traffic, traffic_note = read_traffic(ROOT / "profiles" / "gemv_int4_bf16_gate_up_traffic.md")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                 "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
+                "traffic_source": traffic_note,
                 "kernel": f"gemv_int4_fast_kernel bf16 gate/up N={dom_n} K={dom_k}",
                 "bytes_per_launch": dom_bytes, "avg_us": round(kernel_us[dom_name], 3)}
 
@@ -517,7 +689,29 @@ def main() -> int:
         fp8_gemm["torch_scaled_mm_TFLOPs"] = f"unavailable: {type(e).__name__}"
     log(f"# fp8 gemm cfg4 consumer: {t_gemm:.1f} us, {fp8_gemm['value']} TFLOP/s "
         f"(torch._scaled_mm: {fp8_gemm['torch_scaled_mm_TFLOPs']})")
-    del X4, W4, qx, qw, Y4
+    # ---- the FP8 linear's prologue: RMSNorm -> per-token FP8 of X [16384, 8192]
+    gam4 = torch.empty(D4, device=dev).uniform_(0.5, 1.5, generator=gen).to(torch.bfloat16)
+    xn4 = torch.empty(T4, D4, dtype=torch.bfloat16, device=dev)
+
+    def prologue_fused(j: int) -> None:
+        ck(lib.kc_rmsnorm_quantize_fp8_bf16(X4.data_ptr(), gam4.data_ptr(), 1e-6, qx.data_ptr(),
+                                            sx.data_ptr(), T4, D4, stream_ptr()),
+           "kc_rmsnorm_quantize_fp8_bf16")
+
+    def prologue_two(j: int) -> None:
+        ck(lib.kc_rmsnorm_bf16(X4.data_ptr(), gam4.data_ptr(), xn4.data_ptr(), T4, D4, 1e-6,
+                               stream_ptr()), "kc_rmsnorm_bf16")
+        ck(lib.kc_quantize_fp8_per_token_bf16(xn4.data_ptr(), qx.data_ptr(), sx.data_ptr(), T4,
+                                              D4, stream_ptr()), "kc_quantize_fp8_per_token_bf16")
+    pro_b = T4 * D4 * 2 + T4 * D4 + T4 * 4 + D4 * 2
+    prologue = hbm(pro_b, time_launches(torch, prologue_fused, 10))
+    prologue["two_launches_us"] = round(time_launches(torch, prologue_two, 10), 3)
+    prologue["config"] = ("RMSNorm (bf16 h [16384, 8192], gamma, eps 1e-6) -> per-token E4M3 "
+                          "codes + fp32 scales in one pass (kc_rmsnorm_quantize_fp8_bf16), "
+                          "against kc_rmsnorm_bf16 + kc_quantize_fp8_per_token_bf16")
+    log(f"# fp8 prologue (rmsnorm -> fp8) cfg4 X: fused {prologue['avg_us']} us "
+        f"({prologue['GBps']} GB/s), two launches {prologue['two_launches_us']} us")
+    del X4, W4, qx, qw, Y4, xn4
 
     # ---- decode fusion: the RMSNorm in front of the QKV and gate/up GEMVs ----
     # (kc_rmsnorm_bf16 then kc_gemv_int4_bf16, against the fused launch)
@@ -586,30 +780,23 @@ def main() -> int:
         f"AWQ {convert['awq']['avg_us']} us ({convert['awq']['GBps']} GB/s)")
     del srcs, dsts
 
-    # ---- CPU baseline: the oracle's scalar GEMV, one host thread ----------
+    # ---- stream floors on this GPU (see measure_floors) ------------------------
+    floors = measure_floors(torch, dev, quick=True)
+    of_floor = {nm: round(floors["read"][nm]["avg_us"] / kernel_us[nm], 4) for nm, _, _ in LLAMA}
+    of_floor["cfg0"] = round(floors["read"]["cfg0_weights"]["avg_us"] / cfg0["avg_us"], 4)
+    of_floor["fp8_cfg1_x"] = round(floors["copy"]["cfg1_fp32_to_e4m3"]["avg_us"] / fp8_us, 4)
+    of_floor["fp8_cfg4_x"] = round(floors["copy"]["cfg4_x_bf16_to_e4m3"]["avg_us"] / t_qx, 4)
+    of_floor["fp8_cfg4_w"] = round(floors["copy"]["cfg4_w_bf16_to_e4m3"]["avg_us"] / t_qw, 4)
+    of_floor["fp8_prologue"] = round(floors["copy"]["cfg4_x_bf16_to_e4m3"]["avg_us"]
+                                     / prologue["avg_us"], 4)
+    floors["kernel_fraction_of_floor"] = of_floor
+    log(f"# floors: gate/up read {floors['read']['gate_up']['avg_us']} us, cfg1 copy "
+        f"{floors['copy']['cfg1_fp32_to_e4m3']['avg_us']} us; kernel/floor {of_floor}")
+
+    # ---- CPU baseline: the oracle's scalar loops on the host cores ----------
     cpu = None
     if args.cpu_seconds > 0:
-        import kc_oracle
-        host = []
-        for i, (_, n, k) in enumerate(LLAMA):
-            p, s, z = layers[0][i]
-            host.append((p.cpu().numpy(), s.cpu().numpy(), z.cpu().numpy(),
-                         xs[i].view(torch.int16).cpu().numpy().view(np.uint16), n, k))
-        kc_oracle.gemv_int4_bf16_f32(*host[1][:4], host[1][4], host[1][5], GS)   # warm
-        nlayers = 0
-        t0 = time.perf_counter()
-        while True:
-            for p, s, z, xb, n, k in host:
-                kc_oracle.gemv_int4_bf16_f32(p, s, z, xb, n, k, GS)
-            nlayers += 1
-            if time.perf_counter() - t0 >= args.cpu_seconds:
-                break
-        cpu_s = time.perf_counter() - t0
-        cpu = {"value": round(nlayers * layer_bytes / cpu_s / 1e9, 3), "unit": "GB/s",
-               "cores": 1, "kind": "port",
-               "sample": f"{nlayers} x one decode layer (the same 4 GEMVs, "
-                         f"{layer_bytes} B) in {cpu_s:.1f} s, oracle scalar C loop"}
-        log(f"# cpu baseline: {cpu['value']} GB/s ({nlayers} layers, {cpu_s:.1f} s)")
+        cpu = cpu_baseline(torch, np, layers[0], xs, layer_bytes, args.cpu_seconds)
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
@@ -637,6 +824,8 @@ def main() -> int:
         "gemm_cfg3": cfg3,
         "convert_int4": convert,
         "decode_fusion": fusion,
+        "fp8_prologue_cfg4": prologue,
+        "floors": floors,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

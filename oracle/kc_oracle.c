@@ -479,3 +479,30 @@ void kco_rmsnorm_quantize_fp8_bf16(const uint16_t* h, const uint16_t* g, float e
         kco_quantize_fp8_per_token_bf16(row_y, out + r * D, scales + r, 1, D);
     }
 }
+
+/* ---- multi-threaded CPU baselines (bench.py's cpu_baseline leg) ---------
+ * The same arithmetic as kco_gemv_int4_bf16_f32 and kco_quantize_fp8_per_token
+ * (each row computed exactly as there), rows split over `threads` OpenMP
+ * threads with a static schedule. */
+void kco_gemv_int4_bf16_f32_mt(const uint8_t* packed, const float* scales,
+                               const uint8_t* zeros, const uint16_t* x, float* y,
+                               int64_t rows, int64_t cols, int64_t gs, int threads) {
+    const int64_t G = cols / gs;
+    const int64_t chunks = threads > 0 ? threads : 1;
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int64_t c = 0; c < chunks; ++c) {
+        const int64_t r0 = rows * c / chunks, r1 = rows * (c + 1) / chunks;
+        kco_gemv_int4_bf16_f32(packed + r0 * (cols / 2), scales + r0 * G,
+                               zeros + r0 * (G / 2), x, y + r0, r1 - r0, cols, gs);
+    }
+}
+
+void kco_quantize_fp8_per_token_mt(const float* in, int8_t* out, float* scales,
+                                   int64_t rows, int64_t cols, int threads) {
+    const int64_t chunks = threads > 0 ? threads : 1;
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int64_t c = 0; c < chunks; ++c) {
+        const int64_t r0 = rows * c / chunks, r1 = rows * (c + 1) / chunks;
+        kco_quantize_fp8_per_token(in + r0 * cols, out + r0 * cols, scales + r0, r1 - r0, cols);
+    }
+}

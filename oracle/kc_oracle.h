@@ -102,6 +102,14 @@ void kco_rmsnorm_quantize_fp8_bf16(const uint16_t* h, const uint16_t* g, float e
                                    int8_t* out, float* scales, int64_t rows, int64_t D,
                                    float* row_tmp, uint16_t* row_y);
 
+/* Multi-threaded CPU baselines: the same rows as kco_gemv_int4_bf16_f32 and
+ * kco_quantize_fp8_per_token, split over `threads` OpenMP threads. */
+void kco_gemv_int4_bf16_f32_mt(const uint8_t* packed, const float* scales,
+                               const uint8_t* zeros, const uint16_t* x, float* y,
+                               int64_t rows, int64_t cols, int64_t group_size, int threads);
+void kco_quantize_fp8_per_token_mt(const float* in, int8_t* out, float* scales,
+                                   int64_t rows, int64_t cols, int threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -47,6 +47,8 @@ _SIGS = {
     "kco_quantize_fp8_smooth_mul_bf16": ([_P, _P, _P, _P, _I64, _I64], None),
     "kco_rmsnorm_f32": ([_P, _P, _P, _I64, _I64, ctypes.c_float], None),
     "kco_rmsnorm_bf16": ([_P, _P, _P, _I64, _I64, ctypes.c_float], None),
+    "kco_gemv_int4_bf16_f32_mt": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
+    "kco_quantize_fp8_per_token_mt": ([_P, _P, _P, _I64, _I64, ctypes.c_int], None),
     "kco_rmsnorm_f32_lanes": ([_P, _P, _P, _I64, _I64, ctypes.c_float], None),
     "kco_rmsnorm_bf16_lanes": ([_P, _P, _P, _I64, _I64, ctypes.c_float, _P], None),
     "kco_rmsnorm_quantize_fp8_bf16": ([_P, _P, ctypes.c_float, _P, _P, _I64, _I64, _P, _P],
@@ -138,23 +140,32 @@ def gemm_int4_bf16_f64(packed, scales, zeros, x_bf16, m, rows, cols, group_size)
     return y
 
 
-def gemv_int4_bf16_f32(packed, scales, zeros, x_bf16, rows, cols, group_size):
+def gemv_int4_bf16_f32(packed, scales, zeros, x_bf16, rows, cols, group_size, threads=1):
+    """The scalar CPU GEMV (fp32 accumulation in index order); threads > 1
+    splits its rows over that many OpenMP threads (same results)."""
     packed, scales, zeros = _c(packed, np.uint8), _c(scales, np.float32), _c(zeros, np.uint8)
     x_bf16 = _c(x_bf16, np.uint16)
     y = np.empty(rows, np.float32)
-    lib().kco_gemv_int4_bf16_f32(_p(packed), _p(scales), _p(zeros), _p(x_bf16),
-                                 _p(y), rows, cols, group_size)
+    if threads > 1:
+        lib().kco_gemv_int4_bf16_f32_mt(_p(packed), _p(scales), _p(zeros), _p(x_bf16),
+                                        _p(y), rows, cols, group_size, int(threads))
+    else:
+        lib().kco_gemv_int4_bf16_f32(_p(packed), _p(scales), _p(zeros), _p(x_bf16),
+                                     _p(y), rows, cols, group_size)
     return y
 
 
 # ---- FP8 ------------------------------------------------------------------
 
-def quantize_fp8_per_token(x):
+def quantize_fp8_per_token(x, threads=1):
     x = _c(x, np.float32)
     rows, cols = x.shape
     q = np.empty((rows, cols), np.int8)
     s = np.empty(rows, np.float32)
-    lib().kco_quantize_fp8_per_token(_p(x), _p(q), _p(s), rows, cols)
+    if threads > 1:
+        lib().kco_quantize_fp8_per_token_mt(_p(x), _p(q), _p(s), rows, cols, int(threads))
+    else:
+        lib().kco_quantize_fp8_per_token(_p(x), _p(q), _p(s), rows, cols)
     return q, s
 
 

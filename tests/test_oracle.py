@@ -698,3 +698,20 @@ def test_rmsnorm_quantize_fp8_is_the_composition(oracle):
     assert s[1] == 1.0 and not q[1].any()
     assert (q[2].view(np.uint8) == 0x7E).all()
     assert (q[5].view(np.uint8) == 0x80).all()
+
+
+def test_multithreaded_baselines_equal_scalar(oracle):
+    """The all-core CPU baselines split rows over threads and compute each
+    row exactly as the single-thread loops do."""
+    p, s, z = make_int4(515, 1024, 128, seed=51)
+    xb = normal_bf16((1024,), seed=52)
+    y1 = oracle.gemv_int4_bf16_f32(p, s, z.reshape(-1), xb, 515, 1024, 128)
+    for t in (2, 7, 16):
+        np.testing.assert_array_equal(
+            oracle.gemv_int4_bf16_f32(p, s, z.reshape(-1), xb, 515, 1024, 128, threads=t), y1)
+    x, _ = outlier_activations(333, 4096, 0.01, 50.0, seed=53)
+    q1, s1 = oracle.quantize_fp8_per_token(x)
+    for t in (3, 8):
+        q, sc = oracle.quantize_fp8_per_token(x, threads=t)
+        np.testing.assert_array_equal(q, q1)
+        np.testing.assert_array_equal(sc, s1)
