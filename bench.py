@@ -366,6 +366,10 @@ def main() -> int:
     ap.add_argument("--quant-probe", action="store_true",
                     help="for rocprofv3 --pmc: launch the cfg1 FP8 per-token quantizer 20 "
                          "times over rotating inputs and the 64 MiB copy 20 times, then exit")
+    ap.add_argument("--gemv-probe", action="store_true",
+                    help="for rocprofv3 --pmc: each decode-layer GEMV and the cfg0 fp32 GEMV 20 "
+                         "times, the stream-read floor kernel over each shape's packed weights "
+                         "20 times, and the 64 MiB copy 20 times, then exit")
     ap.add_argument("--floor-probe", action="store_true",
                     help="measure only the stream floors (reads of each GEMV's weight bytes, "
                          "quantizer-shaped copies, an empty launch), print them as JSON, exit")
@@ -424,6 +428,46 @@ def main() -> int:
                 n, k, GS, torch.cuda.current_stream().cuda_stream)
         if st:
             raise RuntimeError(f"kc_gemv_int4_bf16 failed: {lib.kc_last_error_string().decode()}")
+
+    if args.gemv_probe:
+        # every decode shape and the cfg0 fp32 GEMV, 20 launches each over
+        # rotating weights, each followed by 20 launches of the stream-read
+        # floor kernel over the same weight bytes (best grid and unroll of
+        # measure_floors), then the 64 MiB copy that calibrates FETCH_SIZE
+        import ctypes
+        probes = ctypes.CDLL(str(ROOT / "build" / "libkc_probes.so"))
+        probes.kcp_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                           ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+        sink = torch.zeros(2048 * 256, dtype=torch.int32, device=dev)
+        x32 = torch.randn(4096, device=dev, generator=gen)
+        y32 = torch.empty(4096, device=dev)
+        for i, (name, n, k) in enumerate(LLAMA):
+            for j in range(20):
+                launch(j % copies, i)
+            torch.cuda.synchronize()
+            for j in range(20):
+                p, _, _ = layers[j % copies][i]
+                wb = n * k // 2 + n * (k // GS) * 4 + n * (k // GS) // 2
+                probes.kcp_stream_read(p.data_ptr(), n * k // 2, sink.data_ptr(), 2048, 16,
+                                       torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            print(f"gemv probe: {name} x 20, floor read x 20", flush=True)
+        o = 1                                    # O projection's weights, fp32 x and y
+        for j in range(20):
+            p, s_, z = layers[j % copies][o]
+            st = lib.kc_gemv_int4_f32_async(p.data_ptr(), s_.data_ptr(), z.data_ptr(),
+                                            x32.data_ptr(), y32.data_ptr(), 4096, 4096, GS,
+                                            torch.cuda.current_stream().cuda_stream)
+            if st:
+                raise RuntimeError(lib.kc_last_error_string().decode())
+        torch.cuda.synchronize()
+        src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print("gemv probe done: cfg0 x 20, 20 x copy of 67108864 B", flush=True)
+        return 0
 
     if args.traffic_probe:
         src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)

@@ -154,7 +154,9 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_int4_fast_kernel(
     extern __shared__ u32x4 xl[];                                    // x quads, then chunk sums
 
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform: row bases and K offsets stay in SGPRs, so the loads
+    // address with a scalar base and one shared lane offset
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int cpr = cols >> 5;                      // chunks per row
     const int nquads = cpr * kQuadsPerChunk;
     float* xsum = reinterpret_cast<float*>(xl + nquads);
@@ -353,7 +355,9 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
     constexpr int kXQ = BF16 ? 4 : 8;  // 16-byte quads of x per 32-k chunk
     __shared__ float part[RGW][KW][R + 1];  // row sums, then the sum of h^2
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform: row bases and K offsets stay in SGPRs, so the loads
+    // address with a scalar base and one shared lane offset
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int kw = wave % KW, rg = wave / KW;
     const int row0 = (blockIdx.x * RGW + rg) * R;
     const int c = kw * kWave + lane;  // cols == KW * 2048: every lane has a chunk

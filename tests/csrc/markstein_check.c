@@ -17,12 +17,28 @@
  * and row scales of every kept row must equal those of the reference's
  * two-step pipeline (IEEE x/s, absmax, IEEE division by absmax/448).
  *
+ * Mode 3 checks the row-scale route's codes completely: for every one of
+ * the 2^23 significands of s (s in [1, 2)), every E4M3 rounding boundary m
+ * (the midpoints of consecutive E4M3 magnitudes up to 448, and 2^-10 between
+ * 0 and the smallest subnormal) and every x within 4 ulps of RN(m s), both
+ * signs, the quotient bits of the two routes must agree (and so must the
+ * codes).  Both quotients lie within 2 ulps of x/s, so a code can differ only
+ * where x/s is that close to a boundary; and across the fast route's range
+ * (absmax in [2^-60, FLT_MAX], so s = absmax/448 in [2^-68.8, 2^119.2], r =
+ * 1/s normal, and every x whose code is not +-0 normal and above 2^-80) each
+ * step scales exactly with a power of two of s or x, so s in [1, 2) stands
+ * for every exponent.  Mode 4: every s significand against n random x each
+ * (all exponents that keep x/s normal), quotient bits.
+ *
  * usage: markstein_check <mode> <n> <seed>
  *   mode 0: n random scales (row scales absmax/448 with absmax in
  *           [2^-60, 2^127], and factors in [2^-120, 2^120]), 2^16 x each
  *           plus edge cases
  *   mode 1: exhaustive over all 2^32 x for the n-th fixed scale
  *   mode 2: n random rows of 512 elements through the SmoothQuant route
+ *   mode 3: every s significand x every E4M3 boundary x 9 x neighbours x 2 signs
+ *   mode 4: every s significand x n random x
+ * Modes 1, 3 and 4 run on every OpenMP thread.
  * Prints "mismatches <count>" and exits 0 when there are none.
  */
 #include <math.h>
@@ -189,7 +205,65 @@ int main(int argc, char** argv) {
         }
     } else if (mode == 1) {
         const float s = kFixed[n % (long)(sizeof(kFixed) / sizeof(kFixed[0]))];
-        for (uint64_t u = 0; u < (1ull << 32); ++u) bad += check(bits_to_f((uint32_t)u), s);
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+        for (int64_t hi = 0; hi < 65536; ++hi)
+            for (uint32_t lo = 0; lo < 65536; ++lo)
+                bad += check(bits_to_f(((uint32_t)hi << 16) | lo), s);
+    } else if (mode == 3) {
+        float bound[130];
+        int nb = 0;
+        e4m3(0.0f);  /* builds the magnitude table before the threads start */
+        bound[nb++] = 0x1p-10f;
+        {
+            float prev = 0x1p-9f;
+            for (int c = 2; c < 127; ++c) {
+                const int e = c >> 3, m = c & 7;
+                const float v = e == 0 ? ldexpf((float)m, -9) : ldexpf(1.0f + m / 8.0f, e - 7);
+                bound[nb++] = 0.5f * (prev + v);  /* exact: at most 5 significant bits */
+                prev = v;
+            }
+        }
+        long bits_bad = 0;
+#pragma omp parallel for reduction(+ : bad, bits_bad) schedule(dynamic, 4096)
+        for (int64_t man = 0; man < (1 << 23); ++man) {
+            const float s = bits_to_f(0x3F800000u | (uint32_t)man);
+            const float r = 1.0f / s;
+            for (int b = 0; b < nb; ++b) {
+                const uint32_t x0 = f_to_bits(bound[b] * s);
+                for (int d = -4; d <= 4; ++d)
+                    for (int sg = 0; sg < 2; ++sg) {
+                        const float x = bits_to_f((x0 + (uint32_t)d) | (sg ? 0x80000000u : 0u));
+                        const float want = x / s, got = kernel_div(x, s, r);
+                        if (f_to_bits(want) != f_to_bits(got)) {
+                            ++bits_bad;
+                            if (e4m3(clamp448(want)) != e4m3(clamp448(got))) {
+                                if (bad < 10) fprintf(stderr, "s=%a x=%a: codes differ\n", s, x);
+                                ++bad;
+                            }
+                        }
+                    }
+            }
+        }
+        fprintf(stderr, "boundaries %d, checks %lld, quotient-bit differences %ld\n", nb,
+                (long long)(1 << 23) * nb * 18, bits_bad);
+        bad += bits_bad;
+    } else if (mode == 4) {
+#pragma omp parallel for reduction(+ : bad) schedule(dynamic, 4096)
+        for (int64_t man = 0; man < (1 << 23); ++man) {
+            const float s = bits_to_f(0x3F800000u | (uint32_t)man);
+            uint64_t st = (uint64_t)man * 0x9E3779B97F4A7C15ull + 0x632BE59BD9B4E019ull;
+            for (long i = 0; i < n; ++i) {
+                st += 0x9E3779B97F4A7C15ull;
+                uint64_t z = st;
+                z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+                z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+                z ^= z >> 31;
+                /* exponent of x in [-101, 126]: x/s stays normal, |x| >= 2^-102 */
+                const uint32_t ex = 26u + (uint32_t)((z >> 32) % 228u);
+                const float x = bits_to_f(((uint32_t)(z >> 63) << 31) | (ex << 23) | ((uint32_t)z & 0x7FFFFFu));
+                bad += check(x, s);
+            }
+        }
     } else {
         float x[ROW], s[ROW];
         for (long k = 0; k < n; ++k) {
