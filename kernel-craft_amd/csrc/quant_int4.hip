@@ -327,16 +327,19 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_int4_fast_kernel(
 
 
 // ---------------------------------------------------------------------------
-// GEMV with K split across waves and x per lane (K a multiple of 2048; bf16
-// x and y, or fp32 x and y below N = 8192).
+// GEMV with K split across waves and x in registers per lane (K a multiple of
+// 2048; bf16 x and y, or fp32 x and y below N = 8192).
 //
 // A workgroup of KW x RGW waves computes RGW groups of R rows; wave (kw, rg)
-// takes chunk c = 64 kw + lane (32 k) of each of its R rows.  A lane loads
+// takes chunk c = 64 kw + lane (32 k) of each of its R rows.  A lane holds
 // its own chunk of x (64 bytes), permutes it into the decode's pair order and
-// sums it once, and reuses both for all R rows: x is never staged in LDS and
-// no barrier stands between a wave's loads and its arithmetic.  Each wave
-// reduces its R row sums across its lanes; the KW partial sums of a row meet
-// in LDS after the only barrier, at the end.  Measured against the
+// sums it once, and reuses both for all R rows.  With one row group per
+// workgroup the lane loads its chunk itself and no barrier stands between a
+// wave's loads and its arithmetic; with RGW > 1 the workgroup copies x into
+// LDS once (direct-to-LDS loads issued before the weights) and its waves read
+// their chunks after one barrier that waits for the copies only, the weights
+// staying in flight.  Each wave reduces its R row sums across its lanes; the
+// KW partial sums of a row meet in LDS after the last barrier.  Measured against the
 // LDS-staged kernel (K 14336 down projection: 8.8 -> 8.0 us; K 4096 with
 // N <= 6144 a few per cent; K 16384 / 8192 with N 4096: 9.8 -> 8.6, 5.6 ->
 // 5.4 us); the gate/up shape (K 4096, N 28672) keeps the staged kernel.
@@ -345,6 +348,16 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_int4_fast_kernel(
 // x a lane loads its chunk's 32 values (128 bytes) in their own order and
 // folds with offset 8, as the staged kernel's fp32 decode does.
 // ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// One global_load_lds_dwordx4: 16 bytes per lane from g into LDS at
+// lds_base + 16 lane.  Inline assembly, so that the compiler's LDS-wait
+// bookkeeping does not see it; the kernel waits for these loads itself.
+__device__ __forceinline__ void x_dma16(const void* g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base)
+                 : "memory", "m0");
+}
+
 template <int R, int KW, int RGW, bool NORM, bool BF16 = true>
 __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
     const uint8_t* __restrict__ packed, const float* __restrict__ scales,
@@ -365,11 +378,26 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
     const int g = c >> gshift;
     const int64_t rbytes = cols >> 1;
 
-    // loads: x chunk (and gamma), then scales and zero bytes, then weights
-    const u32x4* xs = static_cast<const u32x4*>(x) + c * kXQ;
+    // loads: x (and gamma), then scales and zero bytes, then weights.  With
+    // more than one row group per workgroup, x is copied into LDS once per
+    // workgroup (global_load_lds, no registers) instead of once per wave:
+    // LDS slot (t, l), t = kw' kXQ + j, holds quad j of chunk 64 kw' + l, so
+    // that a wave's reads of quad j are 64 consecutive slots.
+    constexpr bool kShare = !NORM && RGW > 1;
+    __shared__ u32x4 xsh[kShare ? KW * kXQ * kWave : 1];
     u32x4 xq[kXQ], gq[NORM ? 4 : 1];
+    const u32x4* xs = static_cast<const u32x4*>(x) + c * kXQ;
+    if constexpr (kShare) {
+        const uint32_t base = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_void_t*)xsh));
+        for (int t = wave; t < KW * kXQ; t += KW * RGW) {
+            const int kwp = t / kXQ, j = t - kwp * kXQ;
+            x_dma16(static_cast<const u32x4*>(x) + (kwp * kWave + lane) * kXQ + j,
+                    __builtin_amdgcn_readfirstlane(base + t * kWave * 16));
+        }
+    } else {
 #pragma unroll
-    for (int q = 0; q < kXQ; ++q) xq[q] = xs[q];
+        for (int q = 0; q < kXQ; ++q) xq[q] = xs[q];
+    }
     if constexpr (NORM) {
         const u32x4* gsrc = reinterpret_cast<const u32x4*>(gamma) + c * 4;
 #pragma unroll
@@ -390,6 +418,16 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
         w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(packed + rr * rbytes) + c);
     }
     __builtin_amdgcn_sched_barrier(0);  // every load above issued before any use
+    if constexpr (kShare) {
+        // The copies of x are complete once no more than the R scale, R zero
+        // and R weight loads issued after them are outstanding (vector loads
+        // complete in order); the barrier then publishes every wave's part,
+        // while the weights stay in flight.
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * R) : "memory");
+        __builtin_amdgcn_s_barrier();
+#pragma unroll
+        for (int q = 0; q < kXQ; ++q) xq[q] = xsh[(kw * kXQ + q) * kWave + lane];
+    }
 
     uint32_t sel_lo, sel_hi;  // v_perm_b32 selectors, in VGPRs
     asm volatile("v_mov_b32 %0, 0x05040100" : "=v"(sel_lo));
@@ -639,8 +677,16 @@ bool launch_xl(const GemvArgs& a, int64_t rows, int64_t cols, int gshift, hipStr
         if (wide) KC_XL(KWV, 8, 1);      \
         else KC_XL(KWV, 4, 1);           \
         break;
+    // K = 4096: two row groups per workgroup sharing x (bf16: QKV 4.49 ->
+    // 4.38 us, O 3.95 -> 3.92 against x per wave), four with fp32 x, whose
+    // per-wave copies were a third of the kernel (cfg0 4.88 -> 4.01 us).
+    // Sharing x between the two row groups of K = 14336 (down) was slower
+    // (7.9 -> 10.0 us), so K above 4096 keeps one row group per workgroup.
     switch (kw) {
-        case 2: KC_XL(2, 4, 2); break;
+        case 2:
+            if (BF16) KC_XL(2, 4, 2);
+            else KC_XL(2, 4, 4);
+            break;
         KC_XL_CASE(3) KC_XL_CASE(4) KC_XL_CASE(5) KC_XL_CASE(6) KC_XL_CASE(7) KC_XL_CASE(8)
         default: return false;
     }
