@@ -432,26 +432,40 @@ def main() -> int:
     if args.gemv_probe:
         # every decode shape and the cfg0 fp32 GEMV, 20 launches each over
         # rotating weights, each followed by 20 launches of the stream-read
-        # floor kernel over the same weight bytes (best grid and unroll of
-        # measure_floors), then the 64 MiB copy that calibrates FETCH_SIZE
+        # floor kernel over the same number of bytes (packed + scales +
+        # zeros, from a 1.5 GiB buffer at rotating offsets, with the grid and
+        # unroll measure_floors found best for that size on MI355X), then the
+        # 64 MiB copy that calibrates FETCH_SIZE
         import ctypes
         probes = ctypes.CDLL(str(ROOT / "build" / "libkc_probes.so"))
         probes.kcp_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
                                            ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
-        sink = torch.zeros(2048 * 256, dtype=torch.int32, device=dev)
+        floor_shape = {"qkv": (4096, 16), "o_proj": (2048, 8), "gate_up": (2048, 16),
+                       "down": (2048, 16)}
+        sink = torch.zeros(4096 * 256, dtype=torch.int32, device=dev)
+        fbuf_bytes = 3 << 29
+        fbuf = torch.empty(fbuf_bytes, dtype=torch.uint8, device=dev).fill_(3)
         x32 = torch.randn(4096, device=dev, generator=gen)
         y32 = torch.empty(4096, device=dev)
         for i, (name, n, k) in enumerate(LLAMA):
             for j in range(20):
                 launch(j % copies, i)
             torch.cuda.synchronize()
+            wb = n * k // 2 + n * (k // GS) * 4 + n * (k // GS) // 2
+            wb -= wb % 16
+            slots = (fbuf_bytes - wb) // wb
+            grid, unroll = floor_shape[name]
             for j in range(20):
-                p, _, _ = layers[j % copies][i]
-                wb = n * k // 2 + n * (k // GS) * 4 + n * (k // GS) // 2
-                probes.kcp_stream_read(p.data_ptr(), n * k // 2, sink.data_ptr(), 2048, 16,
-                                       torch.cuda.current_stream().cuda_stream)
+                off = (j % (slots + 1)) * ((fbuf_bytes - wb) // slots)
+                off -= off % 256
+                assert off + wb <= fbuf_bytes
+                rc = probes.kcp_stream_read(fbuf.data_ptr() + off, wb, sink.data_ptr(), grid,
+                                            unroll, torch.cuda.current_stream().cuda_stream)
+                if rc:
+                    raise RuntimeError(f"probe launch failed: hipError {rc}")
             torch.cuda.synchronize()
-            print(f"gemv probe: {name} x 20, floor read x 20", flush=True)
+            print(f"gemv probe: {name} x 20, floor read of {wb} B x 20", flush=True)
+        del fbuf
         o = 1                                    # O projection's weights, fp32 x and y
         for j in range(20):
             p, s_, z = layers[j % copies][o]
