@@ -563,12 +563,13 @@ __global__ __launch_bounds__(kThreads) void smooth_div_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// SmoothQuant statistics: column absmax.  Each block reduces a 64-row band of
-// 1024 columns in registers and folds it into d_amax with an integer atomic
-// max (non-negative fp32 values order like their bit patterns; fmaxf from 0
-// keeps NaN out).  d_amax is cleared by a fill kernel first.
+// SmoothQuant statistics: column absmax.  Each block reduces a band of
+// kAbsmaxRowsPerBlock rows of 256 bf16 (128 fp32) columns in registers and
+// folds it into d_amax with an integer atomic max (non-negative fp32 values
+// order like their bit patterns; fmaxf from 0 keeps NaN out).  d_amax is
+// cleared by a fill kernel first.
 // ---------------------------------------------------------------------------
-constexpr int kAbsmaxRowsPerBlock = 256;
+constexpr int kAbsmaxRowsPerBlock = 128;
 constexpr int kAbsmaxUnroll = 4;  // row loads in flight per thread
 
 __global__ __launch_bounds__(kThreads) void fill_zero_kernel(float* __restrict__ p, int64_t n) {
@@ -580,9 +581,14 @@ __global__ __launch_bounds__(kThreads) void fill_zero_kernel(float* __restrict__
 // A block covers a band of kAbsmaxRowsPerBlock rows and 32 16-byte column
 // slots (256 bf16 or 128 fp32 columns).  Thread t reads slot t % 32 of rows
 // t / 32, t / 32 + 8, ... (kAbsmaxUnroll loads in flight); the 8 row groups
-// are max-reduced in LDS and each column gets one atomicMax per band.  The
-// atomics, not the loads, limited the first version (64-row bands): the
-// fewer per column, the faster.
+// are max-reduced in LDS and each column gets one atomicMax per band.
+// Measured at cfg4 (X 16384 x 8192, W 28672 x 8192 bf16): 128-row bands
+// 42.8 / 74.8 us, 256-row 43.8 / 75.2, 512-row 45.2 / 76.8 (8 loads in
+// flight), 64-row 42.8 / 74.6; wider column tiles (64 slots, 1 KB of a row
+// per wave) 45-62 us.  A grid-stride form that keeps one column slot per
+// thread (each wave reading 1 KB of a row, the grid in address order) ran
+// 50-65 us: with few row phases too little is in flight, with many the
+// atomics at the end of the kernel cost more than they save.
 template <bool BF16>
 __global__ __launch_bounds__(kThreads) void col_absmax_kernel(const void* __restrict__ in,
                                                               float* __restrict__ amax,
