@@ -207,6 +207,36 @@ int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
                       uint16_t* d_y, int m, int rows, int cols, int group_size,
                       kc_stream_t stream);
 
+/* The pre-shuffled INT4 weight layout of the matrix-core kernels (the
+ * optional "MFMA-friendly" layout of the weight-format bridge; no
+ * counterpart in the reference, whose only layout is quant_int4.cu:10-13).
+ * A permutation of the reference layout's 16-byte units: rows in tiles of
+ * 16 (the last tile padded with zero rows), K in blocks of 128; block
+ * (tile t, k-block T) is the 1 KB at byte (t * cols/128 + T) * 1024, and
+ * its 16-byte unit l = 16 kb + i (i < 16, kb < 4) holds bytes
+ * 16 kb .. 16 kb + 15 of row 16 t + i's k-block T.  Scales and zeros keep
+ * the reference layout.
+ *   kc_shuffled_int4_bytes: size of the shuffled buffer of a [rows, cols]
+ *     matrix (rows rounded up to 16, times cols / 2), or -1 unless cols is a
+ *     multiple of 128.
+ *   kc_shuffle_int4_mfma: packed [rows, cols/2] -> that buffer (16-byte
+ *     aligned, not overlapping).
+ *   kc_gemm_int4_bf16_shuffled: kc_gemm_int4_bf16 on the shuffled weights.
+ *     For m >= 2 the same kernels, reading 1 KB of the layout per wave-wide
+ *     load instead of 64 bytes of each of 16 rows: bit-identical results.
+ *     m == 1 runs a matrix-core GEMV (cols = 1024 * KW, KW <= 16; other cols
+ *     take the m >= 2 kernel), within the bf16 tolerance of the reference
+ *     GEMV.  Needs cols % 128 == 0, group_size a power of two >= 128, 16-byte
+ *     aligned weights and x. */
+int64_t kc_shuffled_int4_bytes(int64_t rows, int64_t cols);
+int kc_shuffle_int4_mfma(const uint8_t* d_packed, uint8_t* d_packed_shuffled,
+                         int rows, int cols, kc_stream_t stream);
+int kc_gemm_int4_bf16_shuffled(const uint8_t* d_packed_shuffled,
+                               const float* d_scales, const uint8_t* d_zeros,
+                               const uint16_t* d_x, uint16_t* d_y, int m,
+                               int rows, int cols, int group_size,
+                               kc_stream_t stream);
+
 /* W8A8 FP8 GEMM (no counterpart in the reference, whose example dequantizes
  * the codes and multiplies in fp32, examples/python/transformer/
  * fp8_quant.py:55-60):  Y[m, n] = sx[m] * sw[n] * sum_k e4m3(qx[m,k]) *

@@ -278,7 +278,59 @@ int convert(const char* fn, const int32_t* qweight, const int32_t* qzeros, const
     return kc::check_launch(fn);
 }
 
+// ---------------------------------------------------------------------------
+// The reference layout to the shuffled layout that the matrix-core GEMMs can
+// also read (int4_gemm_mfma.hip, tile_lane_ptr).  Rows go in tiles of 16 (the
+// last tile padded with zero rows), K in T-blocks of 128 (64 bytes of a
+// row); block (tile t, T-block T) is the 1 KB at byte (t * K/128 + T) * 1024
+// and its 16-byte unit l = 16 kb + i (i < 16, kb < 4) holds bytes
+// 16 kb .. 16 kb + 15 of T-block T of row 16 t + i: the 16 bytes that lane l
+// of a wave feeds to the matrix core for that tile and T-block.  A
+// permutation of the 16-byte units, plus the pad.  One thread per output
+// unit: the writes are in address order, each read is 16 bytes of a row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void shuffle_mfma_kernel(const u32x4* __restrict__ in,
+                                                                u32x4* __restrict__ out, int64_t rows,
+                                                                int64_t cols, int64_t units) {
+    const int64_t nT = cols / 128;
+    const int64_t row_units = cols / 32;  // 16-byte units of a row
+    for (int64_t u = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; u < units;
+         u += static_cast<int64_t>(gridDim.x) * kThreads) {
+        const int64_t blk = u >> 6;
+        const int l = static_cast<int>(u & 63);
+        const int64_t tile = blk / nT, T = blk - tile * nT;
+        const int64_t row = tile * 16 + (l & 15);
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
+        if (row < rows) v = in[row * row_units + T * 4 + (l >> 4)];
+        out[u] = v;
+    }
+}
+
 }  // namespace
+
+extern "C" int64_t kc_shuffled_int4_bytes(int64_t rows, int64_t cols) {
+    if (rows < 0 || cols < 0 || cols % 128 != 0) return -1;
+    return (rows + 15) / 16 * 16 * (cols / 2);
+}
+
+extern "C" int kc_shuffle_int4_mfma(const uint8_t* d_packed, uint8_t* d_packed_shuffled, int rows,
+                                    int cols, kc_stream_t stream) {
+    const char* fn = "kc_shuffle_int4_mfma";
+    if (rows < 0 || cols < 0 || cols % 128 != 0)
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT,
+                             "%s: rows=%d cols=%d (cols must be a multiple of 128)", fn, rows, cols);
+    if (rows == 0 || cols == 0) return KC_SUCCESS;
+    if (!d_packed || !d_packed_shuffled)
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: null device pointer", fn);
+    if (!kc::aligned(d_packed, 16) || !kc::aligned(d_packed_shuffled, 16))
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: both buffers must be 16-byte aligned", fn);
+    const int64_t units = kc_shuffled_int4_bytes(rows, cols) / 16;
+    const int64_t blocks = std::min<int64_t>((units + kThreads - 1) / kThreads, 8192);
+    shuffle_mfma_kernel<<<static_cast<unsigned>(blocks), kThreads, 0, stream>>>(
+        reinterpret_cast<const u32x4*>(d_packed), reinterpret_cast<u32x4*>(d_packed_shuffled), rows,
+        cols, units);
+    return kc::check_launch(fn);
+}
 
 extern "C" int kc_convert_gptq_int4(const int32_t* d_qweight, const int32_t* d_qzeros,
                                     const uint16_t* d_scales_f16, const int32_t* d_perm, int K,

@@ -62,6 +62,30 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int kTBlock = 128;  // k per T-block: 64 bytes of each W row
 
+// The weight bytes lane (i, kb) feeds to the matrix core for T-block T of
+// the 16-row tile that starts at row r0 (a multiple of 16): 16 bytes, 32
+// nibbles.
+//   reference layout: bytes 64 T + 16 kb of row r0 + i (rows past N read
+//     row N - 1);
+//   shuffled layout (kc_shuffle_int4_mfma): the tile's T-blocks are 1 KB
+//     blocks in T order, tiles one after another, lane l's 16 bytes at byte
+//     16 l of a block -- one wave-wide load then reads 1 KB in address order
+//     instead of 64 bytes of each of 16 rows 2-8 KB apart.
+// tile_lane_ptr points at T-block 0; T-block T is kTStep<SHUF> u32x4 on.
+template <bool SHUF>
+constexpr int kTStep = SHUF ? 64 : 4;
+
+template <bool SHUF>
+__device__ __forceinline__ const u32x4* tile_lane_ptr(const uint8_t* packed, int r0, int N, int K,
+                                                      int lane) {
+    if constexpr (SHUF)  // tiles past the last (rows past the pad) read the last tile
+        return reinterpret_cast<const u32x4*>(packed + static_cast<int64_t>(min(r0 >> 4, (N + 15) / 16 - 1)) *
+                                                           (K / kTBlock) * 1024) + lane;
+    else
+        return reinterpret_cast<const u32x4*>(packed + static_cast<int64_t>(min(r0 + (lane & 15), N - 1)) * (K >> 1)) +
+               (lane >> 4);
+}
+
 // Nibble-decode constants in VGPRs (an SGPR operand halves VALU issue rate on
 // gfx950); the asm makes them opaque to the compiler.
 struct NibConsts {
@@ -311,22 +335,21 @@ __device__ __forceinline__ void compute_chunk(Acc<MT, RT>& acc, const u32x4 (&w)
     }
 }
 
-template <int RT, int TPC>
+template <int RT, int TPC, bool SHUF>
 __device__ __forceinline__ void load_weights(u32x4 (&w)[RT][TPC], const uint8_t* __restrict__ packed,
                                              int N, int64_t rbytes, int nbase, int rg, int q,
                                              int lane, int T0, KSplit ks) {
-    const int i = lane & 15, kb = lane >> 4;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        const int64_t row = min(nbase + (rg * RT + rt) * 16 + i, N - 1);
-        const u32x4* prow = reinterpret_cast<const u32x4*>(packed + row * rbytes);
+        const u32x4* prow = tile_lane_ptr<SHUF>(packed, nbase + (rg * RT + rt) * 16, N,
+                                                static_cast<int>(2 * rbytes), lane);
 #pragma unroll
         for (int t = 0; t < TPC; ++t)
-            w[rt][t] = __builtin_nontemporal_load(prow + ks.T(q, T0, t) * 4 + kb);
+            w[rt][t] = __builtin_nontemporal_load(prow + ks.T(q, T0, t) * kTStep<SHUF>);
     }
 }
 
-template <int MT, int RT, int KW, int TPC>
+template <int MT, int RT, int KW, int TPC, bool SHUF>
 __global__ __launch_bounds__((4 / RT) * KW * kWave) void gemm_int4_mfma_kernel(
     const uint8_t* __restrict__ packed, const float* __restrict__ scales,
     const uint8_t* __restrict__ zeros, const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
@@ -363,7 +386,7 @@ __global__ __launch_bounds__((4 / RT) * KW * kWave) void gemm_int4_mfma_kernel(
     load_chunk_raw<MT, RT, KW, TPC>(raw0, X, scales, zeros, M, N, K, 0, ks, nbase, G, gshift);
     if (nchunks > 1)
         load_chunk_raw<MT, RT, KW, TPC>(raw1, X, scales, zeros, M, N, K, TPC, ks, nbase, G, gshift);
-    load_weights<RT, TPC>(w0, packed, N, rbytes, nbase, rg, q, lane, 0, ks);
+    load_weights<RT, TPC, SHUF>(w0, packed, N, rbytes, nbase, rg, q, lane, 0, ks);
     stage_chunk<MT, RT, KW, TPC>(raw0, buf[0], 0, ks, gshift);
     __syncthreads();
     const NibConsts nk = nib_consts();
@@ -373,7 +396,7 @@ __global__ __launch_bounds__((4 / RT) * KW * kWave) void gemm_int4_mfma_kernel(
         const int T0 = c * TPC, T1 = T0 + TPC, T2 = T1 + TPC, T3 = T2 + TPC;
         if (c + 2 < nchunks)
             load_chunk_raw<MT, RT, KW, TPC>(raw0, X, scales, zeros, M, N, K, T2, ks, nbase, G, gshift);
-        if (c + 1 < nchunks) load_weights<RT, TPC>(w1, packed, N, rbytes, nbase, rg, q, lane, T1, ks);
+        if (c + 1 < nchunks) load_weights<RT, TPC, SHUF>(w1, packed, N, rbytes, nbase, rg, q, lane, T1, ks);
         compute_chunk<MT, RT, KW, TPC>(acc, w0, buf[0], T0, ks.nTq, q, rg, lane, nk);
         if (c + 1 >= nchunks) break;
         stage_chunk<MT, RT, KW, TPC>(raw1, buf[1], T1, ks, gshift);
@@ -381,7 +404,7 @@ __global__ __launch_bounds__((4 / RT) * KW * kWave) void gemm_int4_mfma_kernel(
         // chunk c+1: w1 / buf[1]; chunk c+2 staged from raw0; chunk c+3 -> raw1
         if (c + 3 < nchunks)
             load_chunk_raw<MT, RT, KW, TPC>(raw1, X, scales, zeros, M, N, K, T3, ks, nbase, G, gshift);
-        if (c + 2 < nchunks) load_weights<RT, TPC>(w0, packed, N, rbytes, nbase, rg, q, lane, T2, ks);
+        if (c + 2 < nchunks) load_weights<RT, TPC, SHUF>(w0, packed, N, rbytes, nbase, rg, q, lane, T2, ks);
         compute_chunk<MT, RT, KW, TPC>(acc, w1, buf[1], T1, ks.nTq, q, rg, lane, nk);
         if (c + 2 >= nchunks) break;
         stage_chunk<MT, RT, KW, TPC>(raw0, buf[0], T2, ks, gshift);
@@ -429,7 +452,7 @@ __global__ __launch_bounds__((4 / RT) * KW * kWave) void gemm_int4_mfma_kernel(
     }
 }
 
-template <int MT, int RT, int KW, int TPC>
+template <int MT, int RT, int KW, int TPC, bool SHUF>
 int launch_mfma(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
                 const uint16_t* X, uint16_t* Y, int M, int N, int K, int gshift,
                 hipStream_t stream) {
@@ -438,14 +461,14 @@ int launch_mfma(const char* fn, const uint8_t* packed, const float* scales, cons
                                              (KW - 1) * S::kRowGroups * RT * MT * kWave * 16);
     static bool attr_set = false;  // launches above 64 KB of LDS need the attribute
     if (kLds > 65536 && !attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_int4_mfma_kernel<MT, RT, KW, TPC>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_int4_mfma_kernel<MT, RT, KW, TPC, SHUF>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
                                 static_cast<int>(kLds)) != hipSuccess)
             return kc::set_error(KC_ERR_HIP, "%s: cannot reserve %zu bytes of LDS", fn, kLds);
         attr_set = true;
     }
     const unsigned grid = static_cast<unsigned>((N + S::kRowsWG - 1) / S::kRowsWG);
-    gemm_int4_mfma_kernel<MT, RT, KW, TPC><<<grid, S::kThreadsWG, kLds, stream>>>(
+    gemm_int4_mfma_kernel<MT, RT, KW, TPC, SHUF><<<grid, S::kThreadsWG, kLds, stream>>>(
         packed, scales, zeros, X, Y, M, N, K, gshift);
     return kc::check_launch(fn);
 }
@@ -489,7 +512,7 @@ __host__ __device__ constexpr size_t xres_lds_bytes(int M, int K, int G, int W, 
            static_cast<size_t>(W) * 2 * G * 16 * 4;                  // cs, cz per wave
 }
 
-template <int W, int D>
+template <int W, int D, bool SHUF>
 __global__ __launch_bounds__(W * kWave) void gemm_int4_xres_kernel(
     const uint8_t* __restrict__ packed, const float* __restrict__ scales,
     const uint8_t* __restrict__ zeros, const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
@@ -512,7 +535,7 @@ __global__ __launch_bounds__(W * kWave) void gemm_int4_xres_kernel(
 
     // This lane's weights: row row0 + i, bytes 16 kb .. 16 kb + 15 of each
     // T-block (64 bytes of the row); a ring of the next D T-blocks.
-    const u32x4* wrow = reinterpret_cast<const u32x4*>(packed + static_cast<int64_t>(min(row0 + i, N - 1)) * (K >> 1));
+    const u32x4* wrow = tile_lane_ptr<SHUF>(packed, row0, N, K, lane);
     u32x4 w[D];
 
     // Staging of a phase's X: piece p of row m is X[m][8 p .. 8 p + 7] of the
@@ -562,7 +585,7 @@ __global__ __launch_bounds__(W * kWave) void gemm_int4_xres_kernel(
                     }
                 }
 #pragma unroll
-                for (int u = 0; u < D; ++u) w[u] = wrow[min(u, nT - 1) * 4 + kb];
+                for (int u = 0; u < D; ++u) w[u] = wrow[min(u, nT - 1) * kTStep<SHUF>];
             }
             uint32_t sel_lo, sel_hi;  // v_perm_b32 selectors, in VGPRs
             asm volatile("v_mov_b32 %0, 0x05040100" : "=v"(sel_lo));
@@ -628,7 +651,12 @@ __global__ __launch_bounds__(W * kWave) void gemm_int4_xres_kernel(
                 acc.z = fmaf(s4.z, d.z, fmaf(z4.z, xs, acc.z));
                 acc.w = fmaf(s4.w, d.w, fmaf(z4.w, xs, acc.w));
                 // refill the ring slot: T-block T + D (past the end: the last one again)
-                w[u] = wrow[min(T + D, nT - 1) * 4 + kb];
+                w[u] = wrow[min(T + D, nT - 1) * kTStep<SHUF>];
+                // issued here, right after its slot's last use: left to the
+                // scheduler, the D refills sink to the end of the unrolled
+                // body and the ring drains every D T-blocks (M 4 / 8: 31.6 /
+                // 35.0 -> 31.2 / 32.7 us at K 8192, N 28672)
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         if (ph + 1 < P) {  // uniform: restage X for the next phase
@@ -662,20 +690,20 @@ inline int xres_phases(int M, int K, int G) {
     return 0;
 }
 
-template <int W, int D>
+template <int W, int D, bool SHUF>
 int launch_xres(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
                 const uint16_t* X, uint16_t* Y, int M, int N, int K, int gshift, int P,
                 hipStream_t stream) {
     const int G = (K / kTBlock) >> gshift;
     const size_t lds = xres_lds_bytes(M, K, G, W, P);
     static bool attr_set = [] {
-        return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_int4_xres_kernel<W, D>),
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_int4_xres_kernel<W, D, SHUF>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
     }();
     if (!attr_set) return kc::set_error(KC_ERR_HIP, "%s: cannot raise the LDS limit", fn);
     const int ntiles = (N + 15) / 16;
     const unsigned grid = static_cast<unsigned>((ntiles + W - 1) / W);
-    gemm_int4_xres_kernel<W, D><<<grid, W * kWave, lds, stream>>>(packed, scales, zeros, X, Y, M, N, K,
+    gemm_int4_xres_kernel<W, D, SHUF><<<grid, W * kWave, lds, stream>>>(packed, scales, zeros, X, Y, M, N, K,
                                                                    gshift, P);
     return kc::check_launch(fn);
 }
@@ -703,7 +731,7 @@ __host__ __device__ constexpr size_t xbig_lds_bytes(int M, int G, int W, int RT,
            16;                                                        // alignment slack
 }
 
-template <int W, int RT, int NTP, int D>
+template <int W, int RT, int NTP, int D, bool SHUF>
 __global__ __launch_bounds__(W * kWave) void gemm_int4_xbig_kernel(
     const uint8_t* __restrict__ packed, const float* __restrict__ scales,
     const uint8_t* __restrict__ zeros, const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
@@ -724,13 +752,12 @@ __global__ __launch_bounds__(W * kWave) void gemm_int4_xbig_kernel(
     const int ntiles = (N + 15) / 16;
     const int tile0 = min((static_cast<int>(blockIdx.x) * W + wave) * RT, ntiles - 1);
     const int i = lane & 15, kb = lane >> 4;
-    const int64_t rbytes = K >> 1;
 
     // weight rows of this lane: row 16 (tile0 + rt) + i
     const u32x4* wrow[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
-        wrow[rt] = reinterpret_cast<const u32x4*>(packed + static_cast<int64_t>(min(16 * (tile0 + rt) + i, N - 1)) * rbytes);
+        wrow[rt] = tile_lane_ptr<SHUF>(packed, 16 * (tile0 + rt), N, K, lane);
     u32x4 w[D][RT];
 
     // X staging (see gemm_int4_xres_kernel): piece p of row m within a phase
@@ -802,7 +829,7 @@ __global__ __launch_bounds__(W * kWave) void gemm_int4_xbig_kernel(
 #pragma unroll
         for (int u = 0; u < D; ++u)
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) w[u][rt] = wrow[rt][min(u, nT - 1) * 4 + kb];
+            for (int rt = 0; rt < RT; ++rt) w[u][rt] = wrow[rt][min(u, nT - 1) * kTStep<SHUF>];
         write_x(0, dv);
     }
     __syncthreads();
@@ -833,7 +860,7 @@ __global__ __launch_bounds__(W * kWave) void gemm_int4_xbig_kernel(
                 a[rt][1] = a_operand(wv.y, nk);
                 a[rt][2] = a_operand(wv.z, nk);
                 a[rt][3] = a_operand(wv.w, nk);
-                w[u][rt] = wrow[rt][min(T + D, nT - 1) * 4 + kb];   // refill the ring slot
+                w[u][rt] = wrow[rt][min(T + D, nT - 1) * kTStep<SHUF>];   // refill the ring slot
             }
             f32x4 s4[RT], z4[RT];
 #pragma unroll
@@ -899,21 +926,21 @@ __global__ __launch_bounds__(W * kWave) void gemm_int4_xbig_kernel(
     }
 }
 
-template <int W, int RT, int NTP, int D>
+template <int W, int RT, int NTP, int D, bool SHUF>
 int launch_xbig(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
                 const uint16_t* X, uint16_t* Y, int M, int N, int K, int gshift, hipStream_t stream) {
     const int G = (K / kTBlock) >> gshift;
     const size_t lds = xbig_lds_bytes(M, G, W, RT, NTP);
     if (lds > 160 * 1024) return -1;
     static bool attr_set = [] {
-        return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_int4_xbig_kernel<W, RT, NTP, D>),
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_int4_xbig_kernel<W, RT, NTP, D, SHUF>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
     }();
     if (!attr_set) return kc::set_error(KC_ERR_HIP, "%s: cannot raise the LDS limit", fn);
     const int ntiles = (N + 15) / 16;
     const int per_wg = W * RT;
     const unsigned grid = static_cast<unsigned>((ntiles + per_wg - 1) / per_wg);
-    gemm_int4_xbig_kernel<W, RT, NTP, D><<<grid, W * kWave, lds, stream>>>(packed, scales, zeros, X, Y, M, N, K, gshift);
+    gemm_int4_xbig_kernel<W, RT, NTP, D, SHUF><<<grid, W * kWave, lds, stream>>>(packed, scales, zeros, X, Y, M, N, K, gshift);
     return kc::check_launch(fn);
 }
 
@@ -965,7 +992,7 @@ __host__ __device__ constexpr size_t kslice_lds_bytes(int MT, int RT, int D, int
     return coef > red ? coef : red;
 }
 
-template <int MT, int RT, int D>
+template <int MT, int RT, int D, bool SHUF>
 __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslice_kernel(
     const uint8_t* __restrict__ packed, const float* __restrict__ scales,
     const uint8_t* __restrict__ zeros, const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
@@ -993,14 +1020,15 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslice_kernel(
     uint32_t woff[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
-        woff[rt] = static_cast<uint32_t>(min(row_base + 16 * rt + i, N - 1)) * static_cast<uint32_t>(K >> 1) + 16u * kb;
+        woff[rt] = SHUF ? static_cast<uint32_t>(min(row_base / 16 + rt, (N + 15) / 16 - 1)) * static_cast<uint32_t>(nT * 1024) + 16u * lane
+                        : static_cast<uint32_t>(min(row_base + 16 * rt + i, N - 1)) * static_cast<uint32_t>(K >> 1) + 16u * kb;
     uint32_t xoff[MT];
 #pragma unroll
     for (int c = 0; c < MT; ++c)
         xoff[c] = static_cast<uint32_t>(min(16 * c + i, M - 1)) * static_cast<uint32_t>(2 * K) + 64u * kb;
     const uint8_t* xbytes = reinterpret_cast<const uint8_t*>(X);
     auto wload = [&](int rt, int T) {
-        return *reinterpret_cast<const u32x4*>(packed + (static_cast<uint32_t>(64 * min(T, tl)) + woff[rt]));
+        return *reinterpret_cast<const u32x4*>(packed + (static_cast<uint32_t>(16 * kTStep<SHUF> * min(T, tl)) + woff[rt]));
     };
     auto xload = [&](int c, int T, int s) {
         return *reinterpret_cast<const u32x4*>(xbytes + (static_cast<uint32_t>(256 * min(T, tl) + 16 * s) + xoff[c]));
@@ -1168,30 +1196,179 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslice_kernel(
 }
 
 // Returns -1 when the kernel does not apply (LDS or 32-bit offsets).
-template <int MT>
+template <int MT, bool SHUF>
 int launch_kslice(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
                   const uint16_t* X, uint16_t* Y, int M, int N, int K, int gshift, hipStream_t stream) {
     const size_t lds = kslice_lds_bytes(MT, kKsRT, kKsD, K / kTBlock);
-    if (lds > 160 * 1024 || static_cast<uint64_t>(N) * (K / 2) >= (uint64_t{1} << 32) ||
+    if (lds > 160 * 1024 || static_cast<uint64_t>((N + 15) / 16) * 16 * (K / 2) >= (uint64_t{1} << 32) ||
         static_cast<uint64_t>(M) * K * 2 >= (uint64_t{1} << 32))
         return -1;
     static bool attr_set = [] {
-        return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_int4_kslice_kernel<MT, kKsRT, kKsD>),
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_int4_kslice_kernel<MT, kKsRT, kKsD, SHUF>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
     }();
     if (!attr_set) return kc::set_error(KC_ERR_HIP, "%s: cannot raise the LDS limit", fn);
     const unsigned grid = static_cast<unsigned>((N + 16 * kKsRT - 1) / (16 * kKsRT));
-    gemm_int4_kslice_kernel<MT, kKsRT, kKsD><<<grid, kKsWaves * kWave, lds, stream>>>(
+    gemm_int4_kslice_kernel<MT, kKsRT, kKsD, SHUF><<<grid, kKsWaves * kWave, lds, stream>>>(
         packed, scales, zeros, X, Y, M, N, K, gshift);
     return kc::check_launch(fn);
 }
 
-}  // namespace
+// ---------------------------------------------------------------------------
+// M = 1 on the shuffled layout: x is the A operand, the same 32 values in
+// every row of the 16 x 32 block (a broadcast), the weight tile the B
+// operand, so every row m of D = A B holds the 16 dot products and lane
+// (i, kb)'s first accumulator is row i's.  A workgroup of KW waves owns one
+// 16-row tile; wave w takes T-blocks kGvTPW w .. kGvTPW w + kGvTPW - 1
+// (K = 1024 KW) and issues all their loads at once: 1 KB in address order
+// each.  Per wave the x of its range is staged in LDS in the decode's pair
+// order with its T-block sums (no workgroup barrier), and each T-block is
+// folded with its scale and zero point as in the other kernels.  Measured
+// at K 4096 / 14336 against the reference-layout GEMV: gate/up 11.6 against
+// 11.9 us, down 7.35 against 7.9; slower at N <= 6144 (QKV 4.8 against 4.5,
+// O 4.1 against 3.9): fewer, longer waves.
+// ---------------------------------------------------------------------------
+constexpr int kGvTPW = 8;  // T-blocks per wave
 
-extern "C" int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
-                                 const uint8_t* d_zeros, const uint16_t* d_x, uint16_t* d_y,
-                                 int m, int rows, int cols, int group_size, kc_stream_t stream) {
-    const char* fn = "kc_gemm_int4_bf16";
+template <int KW, bool G128>
+// (the waves-per-EU floor caps the registers at 85: without it the compiler
+// takes 100, and fewer waves fit beside each other)
+__global__ __launch_bounds__(KW * kWave) __attribute__((amdgpu_waves_per_eu(6))) void gemv_int4_shuf_kernel(
+    const uint8_t* __restrict__ packed, const float* __restrict__ scales,
+    const uint8_t* __restrict__ zeros, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+    int rows, int cols, int gshift) {
+    constexpr int kQ = kGvTPW * 16;      // x quads (8 bf16) of a wave's range
+    constexpr int kQPL = kQ / kWave;     // per lane
+    __shared__ u32x4 xsh[KW][kQ];
+    __shared__ float xsum[KW][kGvTPW];
+    __shared__ float part[KW][16];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int n = lane & 15, kb = lane >> 4;
+    const int row0 = static_cast<int>(blockIdx.x) * 16;
+    const int row = min(row0 + n, rows - 1);
+    const int nT = cols / kTBlock;
+    const int G = nT >> gshift;
+    const int t0 = wave * kGvTPW;
+
+    // loads: x of the wave's range, this lane's scales and zero bytes, then
+    // the weights (vector loads complete in order)
+    u32x4 xr[kQPL];
+    const u32x4* xq = reinterpret_cast<const u32x4*>(x) + t0 * 16;
+#pragma unroll
+    for (int u = 0; u < kQPL; ++u) xr[u] = xq[lane + kWave * u];
+    float sv[kGvTPW];
+    uint32_t zv[kGvTPW];
+    if constexpr (G128) {  // one group per T-block: 8 scales and 4 zero bytes in a row
+        const f32x4* sp = reinterpret_cast<const f32x4*>(scales + static_cast<int64_t>(row) * G + t0);
+        const f32x4 s0 = sp[0], s1 = sp[1];
+        const uint32_t zw = *reinterpret_cast<const uint32_t*>(zeros + static_cast<int64_t>(row) * (G >> 1) + (t0 >> 1));
+        sv[0] = s0.x; sv[1] = s0.y; sv[2] = s0.z; sv[3] = s0.w;
+        sv[4] = s1.x; sv[5] = s1.y; sv[6] = s1.z; sv[7] = s1.w;
+#pragma unroll
+        for (int t = 0; t < kGvTPW; ++t) zv[t] = zw;
+    } else {
+#pragma unroll
+        for (int t = 0; t < kGvTPW; ++t) {
+            const int g = (t0 + t) >> gshift;
+            sv[t] = scales[static_cast<int64_t>(row) * G + g];
+            zv[t] = zeros[static_cast<int64_t>(row) * (G >> 1) + (g >> 1)];
+        }
+    }
+    u32x4 w[kGvTPW];
+    const u32x4* wp = tile_lane_ptr<true>(packed, row0, rows, cols, lane) + t0 * kTStep<true>;
+#pragma unroll
+    for (int t = 0; t < kGvTPW; ++t) w[t] = __builtin_nontemporal_load(wp + t * kTStep<true>);
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before any use
+
+    {   // x in the pair order (x0,x4)(x1,x5)(x2,x6)(x3,x7) of each 8, and T-block sums
+        uint32_t sel_lo, sel_hi;
+        asm volatile("v_mov_b32 %0, 0x05040100" : "=v"(sel_lo));
+        asm volatile("v_mov_b32 %0, 0x07060302" : "=v"(sel_hi));
+        const uint32_t ones = 0x3F803F80u;
+#pragma unroll
+        for (int u = 0; u < kQPL; ++u) {
+            const u32x4 d = xr[u];
+            u32x4 q;
+            q.x = __builtin_amdgcn_perm(d.z, d.x, sel_lo);
+            q.y = __builtin_amdgcn_perm(d.z, d.x, sel_hi);
+            q.z = __builtin_amdgcn_perm(d.w, d.y, sel_lo);
+            q.w = __builtin_amdgcn_perm(d.w, d.y, sel_hi);
+            xsh[wave][lane + kWave * u] = q;
+            float sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.x), as_bf16x2(ones), 0.0f, false);
+            sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.y), as_bf16x2(ones), sm, false);
+            sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.z), as_bf16x2(ones), sm, false);
+            sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.w), as_bf16x2(ones), sm, false);
+            sm = row16_sum(sm);  // quad lane + 64 u lies in T-block 4 u + lane / 16
+            if ((lane & 15) == 0) xsum[wave][4 * u + kb] = sm;
+        }
+    }
+    // this wave's LDS writes before its own reads (no other wave reads them)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    const NibConsts nk = nib_consts();
+    float acc = 0.0f;
+#pragma unroll
+    for (int t = 0; t < kGvTPW; ++t) {
+        const u32x4* xa = &xsh[wave][16 * t + 4 * kb];
+        const u32x4 wv = w[t];
+        const uint32_t w0 = wv.x, w1 = wv.y, w2 = wv.z, w3 = wv.w;
+        f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[0]), a_operand(w0, nk),
+                                                          f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[1]), a_operand(w1, nk), d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[2]), a_operand(w2, nk), d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[3]), a_operand(w3, nk), d, 0, 0, 0);
+        const int g = (t0 + t) >> gshift;
+        const uint32_t z = G128 ? (zv[t] >> (4 * t)) & 0xFu : ((g & 1) ? (zv[t] >> 4) : (zv[t] & 0xFu));
+        const float c2 = -sv[t] * (136.0f + static_cast<float>(z));
+        const float dx = d.x;
+        acc = fmaf(sv[t], dx, fmaf(c2, xsum[wave][t], acc));
+    }
+    if (kb == 0) part[wave][n] = acc;
+    __syncthreads();
+    if (wave == 0 && lane < 16) {
+        float tot = part[0][lane];
+#pragma unroll
+        for (int k = 1; k < KW; ++k) tot += part[k][lane];
+        if (row0 + lane < rows) y[row0 + lane] = kc::f32_to_bf16(tot);
+    }
+}
+
+template <int KW>
+int launch_gemv_shuf(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
+                     const uint16_t* x, uint16_t* y, int rows, int cols, int gshift, hipStream_t stream) {
+    const unsigned grid = static_cast<unsigned>((rows + 15) / 16);
+    // 8 scales of a row at once: 16-byte aligned when the row's scales are
+    // (G = K / 128 a multiple of 8) and the array is
+    if (gshift == 0 && kc::aligned(scales, 16) && kc::aligned(zeros, 4))
+        gemv_int4_shuf_kernel<KW, true><<<grid, KW * kWave, 0, stream>>>(packed, scales, zeros, x, y, rows,
+                                                                          cols, gshift);
+    else
+        gemv_int4_shuf_kernel<KW, false><<<grid, KW * kWave, 0, stream>>>(packed, scales, zeros, x, y, rows,
+                                                                           cols, gshift);
+    return kc::check_launch(fn);
+}
+
+// -1 when the kernel does not apply (K not 1024 KW with KW <= 16).
+int gemv_shuf(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
+              const uint16_t* x, uint16_t* y, int rows, int cols, int gshift, hipStream_t stream) {
+    if (cols % 1024 != 0) return -1;
+    switch (cols / 1024) {
+#define KC_GV(KWV) \
+    case KWV: return launch_gemv_shuf<KWV>(fn, packed, scales, zeros, x, y, rows, cols, gshift, stream);
+        KC_GV(1) KC_GV(2) KC_GV(3) KC_GV(4) KC_GV(5) KC_GV(6) KC_GV(7) KC_GV(8)
+        KC_GV(9) KC_GV(10) KC_GV(11) KC_GV(12) KC_GV(13) KC_GV(14) KC_GV(15) KC_GV(16)
+#undef KC_GV
+        default: return -1;
+    }
+}
+
+template <bool SHUF>
+int gemm_int4(const char* fn, const uint8_t* d_packed, const float* d_scales,
+              const uint8_t* d_zeros, const uint16_t* d_x, uint16_t* d_y, int m, int rows,
+              int cols, int group_size, hipStream_t stream) {
     if (m < 0 || m > 64)
         return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: m=%d must be in [0, 64]", fn, m);
     if (rows < 0 || cols < 0 || group_size <= 0 || cols % 2 != 0 || cols % group_size != 0)
@@ -1204,7 +1381,20 @@ extern "C" int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
     const bool fast = cols > 0 && cols % kTBlock == 0 && group_size % kTBlock == 0 &&
                       kc::is_pow2(group_size) && kc::aligned(d_packed, 16) &&
                       kc::aligned(d_x, 16);
-    if (!fast || m == 1) {
+    if constexpr (SHUF) {
+        // only the matrix-core kernels read the shuffled layout
+        if (!fast)
+            return kc::set_error(KC_ERR_INVALID_ARGUMENT,
+                                 "%s: the shuffled layout needs cols a multiple of 128, group_size a "
+                                 "power of two >= 128, and 16-byte aligned weights and x (cols=%d "
+                                 "group_size=%d)",
+                                 fn, cols, group_size);
+        if (m == 1) {
+            const int st = gemv_shuf(fn, d_packed, d_scales, d_zeros, d_x, d_y, rows, cols,
+                                     kc::ilog2(group_size) - 7, stream);
+            if (st >= 0) return st;  // else the X-resident kernel below, at M = 1
+        }
+    } else if (!fast || m == 1) {
         // One GEMV per activation row: same results, no matrix cores (and for
         // a single row the GEMV streams the weights faster: K 8192, N 28672,
         // 20.4 us against 28.3 us for the X-resident kernel below).
@@ -1223,7 +1413,7 @@ extern "C" int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
     if (m <= kXresBestM) {
         const int P = xres_phases(m, cols, (cols / kTBlock) >> gshift);
         if (P > 0)
-            return launch_xres<kXresW, kXresD>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols,
+            return launch_xres<kXresW, kXresD, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols,
                                                gshift, P, stream);
     }
     // M 9..64: the K-split kernel (K 8192, N 28672, MI355X: M 16 / 32 / 48 /
@@ -1234,24 +1424,24 @@ extern "C" int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
     if (m > kXresBestM) {
         int st = -1;
         switch ((m + 15) / 16) {
-            case 1: st = launch_kslice<1>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
-            case 2: st = launch_kslice<2>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
-            case 3: st = launch_kslice<3>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
-            default: st = launch_kslice<4>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+            case 1: st = launch_kslice<1, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+            case 2: st = launch_kslice<2, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+            case 3: st = launch_kslice<3, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+            default: st = launch_kslice<4, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
         }
         if (st >= 0) return st;
     }
     if (m <= kXresMaxM) {
         const int P = xres_phases(m, cols, (cols / kTBlock) >> gshift);
         if (P > 0)
-            return launch_xres<kXresW, kXresD>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols,
+            return launch_xres<kXresW, kXresD, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols,
                                                gshift, P, stream);
     }
     // M 33..64: the four-tile X-resident kernel when its LDS fits (K 8192,
     // N 28672: M 33 / 48 / 64 in 86 / 90 / 94 us against 105 / 119 / 125 us
     // below; at M 17..32 the kernel below is faster, 65-77 us against 80-85)
     if (m > 32 && (cols / kTBlock) % 8 == 0) {
-        const int st = launch_xbig<7, 1, 2, 8>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols,
+        const int st = launch_xbig<7, 1, 2, 8, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols,
                                                gshift, stream);
         if (st >= 0) return st;
     }
@@ -1260,9 +1450,25 @@ extern "C" int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
     // (KW = 1: measured on MI355X at K 8192, N 28672, splitting K across the
     // waves of a workgroup was slower for every M.)
     switch ((m + 15) / 16) {
-        case 1: return launch_mfma<1, 1, 1, 8>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream);
-        case 2: return launch_mfma<2, 1, 1, 4>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream);
-        case 3: return launch_mfma<3, 2, 1, 2>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream);
-        default: return launch_mfma<4, 2, 1, 2>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream);
+        case 1: return launch_mfma<1, 1, 1, 8, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream);
+        case 2: return launch_mfma<2, 1, 1, 4, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream);
+        case 3: return launch_mfma<3, 2, 1, 2, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream);
+        default: return launch_mfma<4, 2, 1, 2, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream);
     }
+}
+
+}  // namespace
+
+extern "C" int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
+                                 const uint8_t* d_zeros, const uint16_t* d_x, uint16_t* d_y,
+                                 int m, int rows, int cols, int group_size, kc_stream_t stream) {
+    return gemm_int4<false>("kc_gemm_int4_bf16", d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols,
+                            group_size, stream);
+}
+
+extern "C" int kc_gemm_int4_bf16_shuffled(const uint8_t* d_packed_shuffled, const float* d_scales,
+                                          const uint8_t* d_zeros, const uint16_t* d_x, uint16_t* d_y,
+                                          int m, int rows, int cols, int group_size, kc_stream_t stream) {
+    return gemm_int4<true>("kc_gemm_int4_bf16_shuffled", d_packed_shuffled, d_scales, d_zeros, d_x, d_y,
+                           m, rows, cols, group_size, stream);
 }

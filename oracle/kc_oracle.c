@@ -26,6 +26,9 @@
  *   kco_smoothquant_scale            KAT test_fp8_quant.cpp:99-135, numpy divide.
  *   extensions                       composition identities with the pinned
  *                                    functions above (fused == two-step).
+ *   kco_shuffle_int4_mfma            a numpy reshape/transpose restatement of the
+ *                                    layout, a bijection check on unit indices, and
+ *                                    the GEMMs on both layouts agreeing bit for bit.
  *   kco_rmsnorm_*                    reference KATs test_mamba_ops.cpp:219-300 (glibc
  *                                    srand/rand recipes) and test_mamba_bindings.py:
  *                                    251-290 (golden fixtures); constant rows, scale
@@ -159,6 +162,23 @@ void kco_dequantize_int4(const uint8_t* packed, const float* scales,
             if (c1 < cols) out[r * cols + c1] = (float)(kco_sext4(p >> 4) - z1) * s1;
         }
     }
+}
+
+/* The shuffled layout of the matrix-core kernels (no reference counterpart;
+ * the reference has only the layout of quant_int4.cu:10-13): 16-byte unit l
+ * (= 16 kb + i) of 1 KB block (tile t, k-block T) at byte (t * cols/128 + T)
+ * * 1024 holds bytes 16 kb .. 16 kb + 15 of row 16 t + i's k-block T (64
+ * bytes per k-block); rows past `rows` are zero.  cols % 128 == 0. */
+void kco_shuffle_int4_mfma(const uint8_t* packed, uint8_t* out, int64_t rows, int64_t cols) {
+    const int64_t nT = cols / 128, tiles = (rows + 15) / 16, rbytes = cols / 2;
+    for (int64_t t = 0; t < tiles; ++t)
+        for (int64_t T = 0; T < nT; ++T)
+            for (int l = 0; l < 64; ++l) {
+                uint8_t* dst = out + ((t * nT + T) * 64 + l) * 16;
+                const int64_t row = 16 * t + (l % 16);
+                if (row < rows) memcpy(dst, packed + row * rbytes + 64 * T + 16 * (l / 16), 16);
+                else memset(dst, 0, 16);
+            }
 }
 
 /* One dequantized weight exactly as quant_int4.cu:158-159 forms it. */

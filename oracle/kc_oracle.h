@@ -36,6 +36,9 @@ uint64_t kco_e4m3_sweep_mismatches(uint32_t start, uint64_t count,
 void kco_dequantize_int4(const uint8_t* packed, const float* scales,
                          const uint8_t* zeros, float* out,
                          int64_t rows, int64_t cols, int64_t group_size);
+/* the shuffled layout of the matrix-core GEMMs: [ceil(rows/16)*16, cols/2]
+ * bytes, a permutation of 16-byte units plus zero pad rows (cols % 128 == 0) */
+void kco_shuffle_int4_mfma(const uint8_t* packed, uint8_t* out, int64_t rows, int64_t cols);
 /* fp64 dot of the reference's fp32-dequantized weights with x (truth) */
 void kco_gemv_int4_f64(const uint8_t* packed, const float* scales,
                        const uint8_t* zeros, const float* x, double* y,

@@ -30,6 +30,7 @@ _SIGS = {
     "kco_e4m3_sweep_mismatches": ([ctypes.c_uint32, ctypes.c_uint64, _P,
                                    ctypes.POINTER(ctypes.c_uint32)], ctypes.c_uint64),
     "kco_dequantize_int4": ([_P, _P, _P, _P, _I64, _I64, _I64], None),
+    "kco_shuffle_int4_mfma": ([_P, _P, _I64, _I64], None),
     "kco_gemv_int4_f64": ([_P, _P, _P, _P, _P, _I64, _I64, _I64], None),
     "kco_gemv_int4_refkernel_f32": ([_P, _P, _P, _P, _P, _I64, _I64, _I64], None),
     "kco_gemm_int4_bf16_f64": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64], None),
@@ -109,6 +110,15 @@ def dequantize_int4(packed, scales, zeros, rows, cols, group_size):
     out = np.empty((rows, cols), np.float32)
     lib().kco_dequantize_int4(_p(packed), _p(scales), _p(zeros), _p(out),
                               rows, cols, group_size)
+    return out
+
+
+def shuffle_int4_mfma(packed, rows, cols):
+    """The matrix-core GEMMs' shuffled layout of packed [rows, cols/2]:
+    [ceil(rows/16)*16 * cols/2] bytes (kco_shuffle_int4_mfma)."""
+    packed = _c(packed, np.uint8)
+    out = np.empty(((rows + 15) // 16) * 16 * (cols // 2), np.uint8)
+    lib().kco_shuffle_int4_mfma(_p(packed), _p(out), rows, cols)
     return out
 
 

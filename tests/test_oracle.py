@@ -715,3 +715,47 @@ def test_multithreaded_baselines_equal_scalar(oracle):
         q, sc = oracle.quantize_fp8_per_token(x, threads=t)
         np.testing.assert_array_equal(q, q1)
         np.testing.assert_array_equal(sc, s1)
+
+
+# ---------------------------------------------------------------------------
+# The shuffled INT4 layout (kco_shuffle_int4_mfma)
+# ---------------------------------------------------------------------------
+
+def _shuffle_numpy(packed, rows, cols):
+    """The layout restated with reshapes: pad rows to 16, view each row as
+    [k-block T][kb][16 bytes], reorder to [tile][T][kb][row in tile][16 B]."""
+    tiles = (rows + 15) // 16
+    p = np.zeros((tiles * 16, cols // 2), np.uint8)
+    p[:rows] = packed
+    v = p.reshape(tiles, 16, cols // 128, 4, 16)          # tile, i, T, kb, byte
+    return v.transpose(0, 2, 3, 1, 4).reshape(-1)          # tile, T, kb, i, byte
+
+
+@pytest.mark.parametrize("rows,cols", [(16, 128), (1, 128), (33, 256), (100, 1152), (48, 4096)])
+def test_shuffle_int4_mfma_layout(oracle, rows, cols):
+    rng = np.random.default_rng(rows + cols)
+    packed = rng.integers(0, 256, (rows, cols // 2), dtype=np.uint8)
+    np.testing.assert_array_equal(oracle.shuffle_int4_mfma(packed, rows, cols),
+                                  _shuffle_numpy(packed, rows, cols))
+
+
+@pytest.mark.parametrize("rows,cols", [(32, 256), (21, 384)])
+def test_shuffle_int4_mfma_is_a_bijection_of_units(oracle, rows, cols):
+    """Tag every 16-byte unit of the input with its index: the output holds
+    each index exactly once, and zeros only in the pad rows; unit l of block
+    (t, T) comes from row 16 t + l % 16, bytes 64 T + 16 (l // 16)."""
+    units = rows * cols // 32
+    tags = np.arange(1, units + 1, dtype=np.uint32)
+    packed = np.zeros((units, 16), np.uint8)
+    packed[:, :4] = tags.view(np.uint8).reshape(units, 4)
+    packed = packed.reshape(rows, cols // 2)
+    out = oracle.shuffle_int4_mfma(packed, rows, cols).reshape(-1, 16)
+    got = out[:, :4].copy().view(np.uint32).reshape(-1)
+    assert sorted(got[got != 0].tolist()) == tags.tolist()
+    assert (got == 0).sum() == ((rows + 15) // 16 * 16 - rows) * cols // 32
+    nT = cols // 128
+    for u in range(out.shape[0]):
+        t, T, l = u // (64 * nT), (u // 64) % nT, u % 64
+        row = 16 * t + l % 16
+        want = 0 if row >= rows else row * (cols // 32) + 4 * T + l // 16 + 1
+        assert got[u] == want
