@@ -1219,28 +1219,27 @@ int launch_kslice(const char* fn, const uint8_t* packed, const float* scales, co
 // every row of the 16 x 32 block (a broadcast), the weight tile the B
 // operand, so every row m of D = A B holds the 16 dot products and lane
 // (i, kb)'s first accumulator is row i's.  A workgroup of KW waves owns one
-// 16-row tile; wave w takes T-blocks kGvTPW w .. kGvTPW w + kGvTPW - 1
-// (K = 1024 KW) and issues all their loads at once: 1 KB in address order
-// each.  Per wave the x of its range is staged in LDS in the decode's pair
+// 16-row tile; wave w takes T-blocks TPW w .. TPW w + TPW - 1
+// (K = 128 TPW KW, TPW 4 or 8) and issues all their loads at once: 1 KB in
+// address order each.  Per wave the x of its range is staged in LDS in the decode's pair
 // order with its T-block sums (no workgroup barrier), and each T-block is
 // folded with its scale and zero point as in the other kernels.  Measured
-// at K 4096 / 14336 against the reference-layout GEMV: gate/up 11.6 against
-// 11.9 us, down 7.35 against 7.9; slower at N <= 6144 (QKV 4.8 against 4.5,
-// O 4.1 against 3.9): fewer, longer waves.
+// at K 4096 / 14336 against the reference-layout GEMV (bf16, rotating
+// weights): gate/up 11.9-12.0 against 12.1-12.2 us, down 7.9 against 8.6,
+// O 3.96 against 3.97, QKV 4.93 against 4.75.
 // ---------------------------------------------------------------------------
-constexpr int kGvTPW = 8;  // T-blocks per wave
-
-template <int KW, bool G128>
+template <int KW, int TPW, bool G128>
 // (the waves-per-EU floor caps the registers at 85: without it the compiler
 // takes 100, and fewer waves fit beside each other)
 __global__ __launch_bounds__(KW * kWave) __attribute__((amdgpu_waves_per_eu(6))) void gemv_int4_shuf_kernel(
     const uint8_t* __restrict__ packed, const float* __restrict__ scales,
     const uint8_t* __restrict__ zeros, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
     int rows, int cols, int gshift) {
-    constexpr int kQ = kGvTPW * 16;      // x quads (8 bf16) of a wave's range
+    static_assert(TPW == 4 || TPW == 8 || TPW == 16, "T-blocks per wave");
+    constexpr int kQ = TPW * 16;         // x quads (8 bf16) of a wave's range
     constexpr int kQPL = kQ / kWave;     // per lane
     __shared__ u32x4 xsh[KW][kQ];
-    __shared__ float xsum[KW][kGvTPW];
+    __shared__ float xsum[KW][TPW];
     __shared__ float part[KW][16];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -1249,7 +1248,7 @@ __global__ __launch_bounds__(KW * kWave) __attribute__((amdgpu_waves_per_eu(6)))
     const int row = min(row0 + n, rows - 1);
     const int nT = cols / kTBlock;
     const int G = nT >> gshift;
-    const int t0 = wave * kGvTPW;
+    const int t0 = wave * TPW;
 
     // loads: x of the wave's range, this lane's scales and zero bytes, then
     // the weights (vector loads complete in order)
@@ -1257,28 +1256,33 @@ __global__ __launch_bounds__(KW * kWave) __attribute__((amdgpu_waves_per_eu(6)))
     const u32x4* xq = reinterpret_cast<const u32x4*>(x) + t0 * 16;
 #pragma unroll
     for (int u = 0; u < kQPL; ++u) xr[u] = xq[lane + kWave * u];
-    float sv[kGvTPW];
-    uint32_t zv[kGvTPW];
-    if constexpr (G128) {  // one group per T-block: 8 scales and 4 zero bytes in a row
+    float sv[TPW];
+    uint32_t zv[TPW];
+    if constexpr (G128) {  // one group per T-block: TPW scales and TPW / 2 zero bytes in a row
         const f32x4* sp = reinterpret_cast<const f32x4*>(scales + static_cast<int64_t>(row) * G + t0);
-        const f32x4 s0 = sp[0], s1 = sp[1];
-        const uint32_t zw = *reinterpret_cast<const uint32_t*>(zeros + static_cast<int64_t>(row) * (G >> 1) + (t0 >> 1));
-        sv[0] = s0.x; sv[1] = s0.y; sv[2] = s0.z; sv[3] = s0.w;
-        sv[4] = s1.x; sv[5] = s1.y; sv[6] = s1.z; sv[7] = s1.w;
 #pragma unroll
-        for (int t = 0; t < kGvTPW; ++t) zv[t] = zw;
+        for (int i = 0; i < TPW / 4; ++i) {
+            const f32x4 s4 = sp[i];
+            sv[4 * i] = s4.x; sv[4 * i + 1] = s4.y; sv[4 * i + 2] = s4.z; sv[4 * i + 3] = s4.w;
+        }
+        const uint8_t* zp = zeros + static_cast<int64_t>(row) * (G >> 1) + (t0 >> 1);
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+            if constexpr (TPW == 4) zv[t] = *reinterpret_cast<const uint16_t*>(zp);
+            else zv[t] = reinterpret_cast<const uint32_t*>(zp)[t / 8];
+        }
     } else {
 #pragma unroll
-        for (int t = 0; t < kGvTPW; ++t) {
+        for (int t = 0; t < TPW; ++t) {
             const int g = (t0 + t) >> gshift;
             sv[t] = scales[static_cast<int64_t>(row) * G + g];
             zv[t] = zeros[static_cast<int64_t>(row) * (G >> 1) + (g >> 1)];
         }
     }
-    u32x4 w[kGvTPW];
+    u32x4 w[TPW];
     const u32x4* wp = tile_lane_ptr<true>(packed, row0, rows, cols, lane) + t0 * kTStep<true>;
 #pragma unroll
-    for (int t = 0; t < kGvTPW; ++t) w[t] = __builtin_nontemporal_load(wp + t * kTStep<true>);
+    for (int t = 0; t < TPW; ++t) w[t] = __builtin_nontemporal_load(wp + t * kTStep<true>);
     __builtin_amdgcn_sched_barrier(0);  // every load issued before any use
 
     {   // x in the pair order (x0,x4)(x1,x5)(x2,x6)(x3,x7) of each 8, and T-block sums
@@ -1311,7 +1315,7 @@ __global__ __launch_bounds__(KW * kWave) __attribute__((amdgpu_waves_per_eu(6)))
     const NibConsts nk = nib_consts();
     float acc = 0.0f;
 #pragma unroll
-    for (int t = 0; t < kGvTPW; ++t) {
+    for (int t = 0; t < TPW; ++t) {
         const u32x4* xa = &xsh[wave][16 * t + 4 * kb];
         const u32x4 wv = w[t];
         const uint32_t w0 = wv.x, w1 = wv.y, w2 = wv.z, w3 = wv.w;
@@ -1321,7 +1325,7 @@ __global__ __launch_bounds__(KW * kWave) __attribute__((amdgpu_waves_per_eu(6)))
         d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[2]), a_operand(w2, nk), d, 0, 0, 0);
         d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[3]), a_operand(w3, nk), d, 0, 0, 0);
         const int g = (t0 + t) >> gshift;
-        const uint32_t z = G128 ? (zv[t] >> (4 * t)) & 0xFu : ((g & 1) ? (zv[t] >> 4) : (zv[t] & 0xFu));
+        const uint32_t z = G128 ? (zv[t] >> (4 * (t % 8))) & 0xFu : ((g & 1) ? (zv[t] >> 4) : (zv[t] & 0xFu));
         const float c2 = -sv[t] * (136.0f + static_cast<float>(z));
         const float dx = d.x;
         acc = fmaf(sv[t], dx, fmaf(c2, xsum[wave][t], acc));
@@ -1336,33 +1340,44 @@ __global__ __launch_bounds__(KW * kWave) __attribute__((amdgpu_waves_per_eu(6)))
     }
 }
 
-template <int KW>
+template <int KW, int TPW>
 int launch_gemv_shuf(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
                      const uint16_t* x, uint16_t* y, int rows, int cols, int gshift, hipStream_t stream) {
     const unsigned grid = static_cast<unsigned>((rows + 15) / 16);
     // 8 scales of a row at once: 16-byte aligned when the row's scales are
     // (G = K / 128 a multiple of 8) and the array is
     if (gshift == 0 && kc::aligned(scales, 16) && kc::aligned(zeros, 4))
-        gemv_int4_shuf_kernel<KW, true><<<grid, KW * kWave, 0, stream>>>(packed, scales, zeros, x, y, rows,
+        gemv_int4_shuf_kernel<KW, TPW, true><<<grid, KW * kWave, 0, stream>>>(packed, scales, zeros, x, y, rows,
                                                                           cols, gshift);
     else
-        gemv_int4_shuf_kernel<KW, false><<<grid, KW * kWave, 0, stream>>>(packed, scales, zeros, x, y, rows,
+        gemv_int4_shuf_kernel<KW, TPW, false><<<grid, KW * kWave, 0, stream>>>(packed, scales, zeros, x, y, rows,
                                                                            cols, gshift);
     return kc::check_launch(fn);
 }
 
-// -1 when the kernel does not apply (K not 1024 KW with KW <= 16).
+// Up to N = 8192 (and K = 8192) four T-blocks per wave, twice the waves:
+// QKV 5.16 -> 4.93 us, O 4.14 -> 3.96 us; the same elsewhere.
+constexpr int kGvSmallRows = 8192;
+
+// -1 when the kernel does not apply (K not 128 TPW KW with KW <= 16).
 int gemv_shuf(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
               const uint16_t* x, uint16_t* y, int rows, int cols, int gshift, hipStream_t stream) {
+#define KC_GV(KWV, TPWV) \
+    case KWV: return launch_gemv_shuf<KWV, TPWV>(fn, packed, scales, zeros, x, y, rows, cols, gshift, stream);
+    if (rows <= kGvSmallRows && cols % 512 == 0 && cols / 512 <= 16) {
+        switch (cols / 512) {
+            KC_GV(1, 4) KC_GV(2, 4) KC_GV(3, 4) KC_GV(4, 4) KC_GV(5, 4) KC_GV(6, 4) KC_GV(7, 4) KC_GV(8, 4)
+            KC_GV(9, 4) KC_GV(10, 4) KC_GV(11, 4) KC_GV(12, 4) KC_GV(13, 4) KC_GV(14, 4) KC_GV(15, 4) KC_GV(16, 4)
+            default: break;
+        }
+    }
     if (cols % 1024 != 0) return -1;
     switch (cols / 1024) {
-#define KC_GV(KWV) \
-    case KWV: return launch_gemv_shuf<KWV>(fn, packed, scales, zeros, x, y, rows, cols, gshift, stream);
-        KC_GV(1) KC_GV(2) KC_GV(3) KC_GV(4) KC_GV(5) KC_GV(6) KC_GV(7) KC_GV(8)
-        KC_GV(9) KC_GV(10) KC_GV(11) KC_GV(12) KC_GV(13) KC_GV(14) KC_GV(15) KC_GV(16)
-#undef KC_GV
+        KC_GV(1, 8) KC_GV(2, 8) KC_GV(3, 8) KC_GV(4, 8) KC_GV(5, 8) KC_GV(6, 8) KC_GV(7, 8) KC_GV(8, 8)
+        KC_GV(9, 8) KC_GV(10, 8) KC_GV(11, 8) KC_GV(12, 8) KC_GV(13, 8) KC_GV(14, 8) KC_GV(15, 8) KC_GV(16, 8)
         default: return -1;
     }
+#undef KC_GV
 }
 
 template <bool SHUF>

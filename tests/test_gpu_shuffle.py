@@ -98,8 +98,12 @@ def test_gemm_shuffled_equals_reference_layout(gpu, m, rows, cols, gs):
                                           (4096, 14336, 128),
                                           # K 1024 KW with KW 1, 3, 16; groups of 256, 512
                                           (300, 1024, 128), (1000, 3072, 256), (77, 16384, 512),
-                                          # K not a multiple of 1024: the X-resident kernel at M = 1
-                                          (250, 1152, 128), (33, 640, 128)])
+                                          # N <= 8192 and K <= 8192: four T-blocks per wave
+                                          # (K 512 KW: 1536, 8192)
+                                          (100, 1536, 128), (500, 8192, 128), (8192, 2048, 256),
+                                          # K not a multiple of 1024 past N = 8192, or of 512:
+                                          # the X-resident kernel at M = 1
+                                          (9000, 1536, 128), (250, 1152, 128), (33, 640, 128)])
 def test_gemv_shuffled_vs_oracle(gpu, oracle, rows, cols, gs):
     torch = gpu
     packed, scales, zeros = make_int4(rows, cols, gs, seed=rows * 7 + cols)
