@@ -587,6 +587,50 @@ def main() -> int:
         kernel_us[name] = e0.elapsed_time(e1) * 1e3 / reps
         log(f"# {name:8s} N={n:6d} K={k:6d}: {kernel_us[name]:7.2f} us/launch, "
             f"{gemv_bytes(n, k) / kernel_us[name] / 1e3:7.1f} GB/s")
+    # ---- the same GEMVs on the pre-shuffled layout (kc_shuffle_int4_mfma once,
+    # then kc_gemm_int4_bf16_shuffled at M = 1): the matrix-core GEMV, which
+    # reads each 16-row tile 1 KB at a time; same bytes, same rotation
+    shuf = [[None] * len(LLAMA) for _ in range(copies)]
+    for r in range(copies):
+        for i, (_, n, k) in enumerate(LLAMA):
+            p = layers[r][i][0]
+            sbuf = torch.empty(lib.kc_shuffled_int4_bytes(n, k), dtype=torch.uint8, device=dev)
+            if lib.kc_shuffle_int4_mfma(p.data_ptr(), sbuf.data_ptr(), n, k,
+                                        torch.cuda.current_stream().cuda_stream):
+                raise RuntimeError(f"kc_shuffle_int4_mfma: {lib.kc_last_error_string().decode()}")
+            shuf[r][i] = sbuf
+    ys_sh = [torch.empty(1, n, dtype=torch.bfloat16, device=dev) for _, n, _ in LLAMA]
+    xs2 = [x.view(1, -1) for x in xs]
+
+    def launch_shuf(r: int, i: int) -> None:
+        _, n, k = LLAMA[i]
+        _, s_, z = layers[r][i]
+        st = lib.kc_gemm_int4_bf16_shuffled(shuf[r][i].data_ptr(), s_.data_ptr(), z.data_ptr(),
+                                            xs2[i].data_ptr(), ys_sh[i].data_ptr(), 1, n, k, GS,
+                                            torch.cuda.current_stream().cuda_stream)
+        if st:
+            raise RuntimeError(f"kc_gemm_int4_bf16_shuffled: {lib.kc_last_error_string().decode()}")
+    shuffled_us = {}
+    for i, (name, n, k) in enumerate(LLAMA):
+        launch_shuf(0, i)
+        launch(0, i)
+        torch.cuda.synchronize()
+        err = ((ys_sh[i].float().view(-1) - ys[i].float()).norm() / ys[i].float().norm()).item()
+        if not err < 3e-3:
+            print(f"bench.py: shuffled-layout GEMV disagrees for {name}: rel L2 {err:.3e}",
+                  file=sys.stderr)
+            return 1
+        shuffled_us[name] = time_launches(torch, lambda j, i=i: launch_shuf(j % copies, i), reps)
+        log(f"# {name:8s} shuffled layout: {shuffled_us[name]:7.2f} us/launch "
+            f"(reference layout {kernel_us[name]:.2f})")
+    shuffled = {"kernel_us": {k: round(v, 3) for k, v in shuffled_us.items()},
+                "sum_us": round(sum(shuffled_us.values()), 3),
+                "reference_layout_sum_us": round(sum(kernel_us.values()), 3),
+                "config": "the decode layer's GEMVs at M = 1 on the pre-shuffled layout "
+                          "(kc_shuffle_int4_mfma, kc_gemm_int4_bf16_shuffled), one launch each, "
+                          "events as kernel_us"}
+    del shuf
+
     dom_name, dom_n, dom_k = LLAMA[DOMINANT]
     dom_bytes = gemv_bytes(dom_n, dom_k)
     achieved = dom_bytes / (kernel_us[dom_name] * 1e-6) / 1e9
@@ -650,7 +694,38 @@ def main() -> int:
         r["TFLOPs"] = round(2.0 * m * n3 * k3 / (r["avg_us"] * 1e-6) / 1e12, 2)
         cfg3[f"M{m}"] = r
         log(f"# cfg3 MFMA GEMM M={m:2d}: {r['avg_us']} us, {r['GBps']} GB/s, {r['TFLOPs']} TFLOP/s")
-    del c3
+    # the same GEMMs on the pre-shuffled layout: bit-identical outputs
+    c3s = []
+    for p, _, _ in c3:
+        sbuf = torch.empty(lib.kc_shuffled_int4_bytes(n3, k3), dtype=torch.uint8, device=dev)
+        ck(lib.kc_shuffle_int4_mfma(p.data_ptr(), sbuf.data_ptr(), n3, k3, stream_ptr()),
+           "kc_shuffle_int4_mfma")
+        c3s.append(sbuf)
+    cfg3_shuf = {}
+    for m in (4, 16, 64):
+        x3 = torch.randn(m, k3, device=dev, generator=gen).to(torch.bfloat16)
+        y3 = torch.empty(m, n3, dtype=torch.bfloat16, device=dev)
+        y3r = torch.empty(m, n3, dtype=torch.bfloat16, device=dev)
+
+        def launch_cfg3s(j: int, m=m, x3=x3, y3=y3) -> None:
+            _, sc, z = c3[j % c3_copies]
+            ck(lib.kc_gemm_int4_bf16_shuffled(c3s[j % c3_copies].data_ptr(), sc.data_ptr(),
+                                              z.data_ptr(), x3.data_ptr(), y3.data_ptr(), m, n3, k3,
+                                              GS, stream_ptr()), "kc_gemm_int4_bf16_shuffled")
+        p, sc, z = c3[0]
+        ck(lib.kc_gemm_int4_bf16(p.data_ptr(), sc.data_ptr(), z.data_ptr(), x3.data_ptr(),
+                                 y3r.data_ptr(), m, n3, k3, GS, stream_ptr()), "kc_gemm_int4_bf16")
+        launch_cfg3s(0)
+        torch.cuda.synchronize()
+        if not torch.equal(y3.view(torch.int16), y3r.view(torch.int16)):
+            print(f"bench.py: shuffled-layout GEMM differs at M={m}", file=sys.stderr)
+            return 1
+        nbytes = w3_bytes + m * k3 * 2 + m * n3 * 2
+        r = hbm(nbytes, time_launches(torch, launch_cfg3s, 50))
+        r["TFLOPs"] = round(2.0 * m * n3 * k3 / (r["avg_us"] * 1e-6) / 1e12, 2)
+        cfg3_shuf[f"M{m}"] = r
+        log(f"# cfg3 GEMM, shuffled layout, M={m:2d}: {r['avg_us']} us, {r['GBps']} GB/s")
+    del c3, c3s
 
     # ---- BASELINE cfg1: FP8 per-token X and per-channel W, fp32 [4096, 4096] -
     frows = fcols = 4096
@@ -880,6 +955,8 @@ def main() -> int:
         "fp8_gemm_cfg4": fp8_gemm,
         "gemv_cfg0": cfg0,
         "gemm_cfg3": cfg3,
+        "gemm_cfg3_shuffled": cfg3_shuf,
+        "gemv_shuffled_layout": shuffled,
         "convert_int4": convert,
         "decode_fusion": fusion,
         "fp8_prologue_cfg4": prologue,

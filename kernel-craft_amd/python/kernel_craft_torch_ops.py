@@ -121,6 +121,9 @@ PROTOTYPES = {
     "kc_gemv_int4_bf16": ([_vp] * 5 + [_i, _i, _i, _vp], _i),
     "kc_gemm_int4_bf16": ([_vp] * 5 + [_i, _i, _i, _i, _vp], _i),
     "kc_gemv_int4_bf16_chain": ([_vp, _i, _vp], _i),
+    "kc_shuffled_int4_bytes": ([_i64, _i64], _i64),
+    "kc_shuffle_int4_mfma": ([_vp, _vp, _i, _i, _vp], _i),
+    "kc_gemm_int4_bf16_shuffled": ([_vp] * 5 + [_i, _i, _i, _i, _vp], _i),
     "kc_convert_gptq_int4": ([_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp], _i),
     "kc_convert_awq_int4": ([_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp], _i),
     "kc_gemm_fp8_w8a8_bf16": ([_vp] * 5 + [_i64, _i64, _i64, _vp], _i),
@@ -190,20 +193,28 @@ def _on_gpu(op: str, *tensors) -> None:
                              "GPU only (there is no CPU fallback)")
 
 
-def _int4_weights(op: str, packed, scales, zeros, rows: int, cols: int, group_size: int):
-    """Validated (packed, scales, zeros) of an INT4 layer [rows, cols] in the
-    reference layout: packed [rows, cols/2] u8, scales [rows, G] fp32 and
-    zero bytes read at row stride floor(G/2) (quant_int4.cu:93,152), so the
-    last row reaches byte (rows-1)*floor(G/2) + (G-1)/2, with
+def _int4_meta(op: str, scales, zeros, rows: int, cols: int, group_size: int):
+    """Validated (scales, zeros) of an INT4 layer [rows, cols]: scales [rows,
+    G] fp32 and zero bytes read at row stride floor(G/2) (quant_int4.cu:93,
+    152), so the last row reaches byte (rows-1)*floor(G/2) + (G-1)/2, with
     G = cols / group_size.  Bad shape arguments are left to the library,
     which rejects them with a message."""
     import torch
     ok = rows > 0 and cols > 0 and group_size > 0
     G = cols // group_size if ok else 0
     zneed = (rows - 1) * (G // 2) + (G - 1) // 2 + 1 if ok and G > 0 else 0
-    return (_arg(f"{op}: packed", packed, torch.uint8, rows * (cols // 2) if ok else None),
-            _arg(f"{op}: scales", scales, torch.float32, rows * G if ok else None),
+    return (_arg(f"{op}: scales", scales, torch.float32, rows * G if ok else None),
             _arg(f"{op}: zeros", zeros, torch.uint8, zneed))
+
+
+def _int4_weights(op: str, packed, scales, zeros, rows: int, cols: int, group_size: int):
+    """Validated (packed, scales, zeros) of an INT4 layer [rows, cols] in the
+    reference layout: packed [rows, cols/2] u8, scales and zeros as
+    _int4_meta checks them."""
+    import torch
+    ok = rows > 0 and cols > 0 and group_size > 0
+    packed = _arg(f"{op}: packed", packed, torch.uint8, rows * (cols // 2) if ok else None)
+    return (packed,) + _int4_meta(op, scales, zeros, rows, cols, group_size)
 
 
 def _check(name: str, status: Optional[int] = None) -> None:
@@ -443,6 +454,50 @@ def int4_gemm_bf16(packed, scales, zeros, x, rows: int, cols: int, group_size: i
         st = _get_lib().kc_gemm_int4_bf16(_ptr(packed), _ptr(scales), _ptr(zeros), _ptr(x),
                                           _ptr(y), m, rows, cols, group_size, _stream())
     _check("int4_gemm_bf16", st)
+    return y
+
+
+def int4_shuffle_mfma(packed, rows: int, cols: int):
+    """The pre-shuffled layout of packed [rows, cols/2] u8 for the matrix-core
+    kernels (kc_shuffle_int4_mfma): a u8 vector of ceil(rows/16)*16*cols/2
+    bytes.  cols must be a multiple of 128; scales and zeros stay as they are."""
+    import torch
+    nbytes = _get_lib().kc_shuffled_int4_bytes(rows, cols)
+    if nbytes < 0 or rows < 0:
+        raise ValueError(f"int4_shuffle_mfma: rows={rows} cols={cols} (cols must be a multiple of 128)")
+    packed = _arg("int4_shuffle_mfma: packed", packed, torch.uint8, rows * (cols // 2))
+    _on_gpu("int4_shuffle_mfma", packed)
+    out = torch.empty(nbytes, dtype=torch.uint8, device=packed.device)
+    with kernel_span("int4_shuffle_mfma", rows=rows, cols=cols):
+        st = _get_lib().kc_shuffle_int4_mfma(_ptr(packed), _ptr(out), rows, cols, _stream())
+    _check("int4_shuffle_mfma", st)
+    return out
+
+
+def int4_gemm_bf16_shuffled(packed_shuffled, scales, zeros, x, rows: int, cols: int,
+                            group_size: int = 128):
+    """int4_gemm_bf16 on weights in the shuffled layout (int4_shuffle_mfma):
+    Y [m, rows] bf16 for bf16 X [m, cols], 1 <= m <= 64
+    (kc_gemm_int4_bf16_shuffled)."""
+    import torch
+    nbytes = _get_lib().kc_shuffled_int4_bytes(rows, cols)
+    if nbytes < 0 or rows < 0:
+        raise ValueError(f"int4_gemm_bf16_shuffled: rows={rows} cols={cols} (cols must be a "
+                         "multiple of 128)")
+    packed_shuffled = _arg("int4_gemm_bf16_shuffled: packed_shuffled", packed_shuffled, torch.uint8,
+                           nbytes)
+    scales, zeros = _int4_meta("int4_gemm_bf16_shuffled", scales, zeros, rows, cols, group_size)
+    x = _arg("int4_gemm_bf16_shuffled: x", x, torch.bfloat16)
+    if x.dim() != 2 or x.shape[1] != cols:
+        raise ValueError(f"int4_gemm_bf16_shuffled: x must be [m, {cols}], not {list(x.shape)}")
+    _on_gpu("int4_gemm_bf16_shuffled", packed_shuffled, scales, zeros, x)
+    m = x.shape[0]
+    y = torch.empty(m, rows, dtype=torch.bfloat16, device=packed_shuffled.device)
+    with kernel_span("int4_gemm_bf16_shuffled", m=m, rows=rows, cols=cols, group_size=group_size):
+        st = _get_lib().kc_gemm_int4_bf16_shuffled(_ptr(packed_shuffled), _ptr(scales), _ptr(zeros),
+                                                   _ptr(x), _ptr(y), m, rows, cols, group_size,
+                                                   _stream())
+    _check("int4_gemm_bf16_shuffled", st)
     return y
 
 

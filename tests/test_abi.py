@@ -257,6 +257,16 @@ def test_bridge_span_fallback_accepts_attributes(tmp_path):
                                torch.zeros(8, 32, dtype=torch.int8), torch.ones(8)), "share K"),
     (lambda: ops.smooth_factors(torch.ones(8), torch.ones(7)), "elements"),
     (lambda: ops.rmsnorm(torch.zeros(2, 64, dtype=torch.float16), torch.ones(64)), "dtype"),
+    (lambda: ops.int4_shuffle_mfma(torch.zeros(8, 48, dtype=torch.uint8), 8, 96), "multiple of 128"),
+    (lambda: ops.int4_shuffle_mfma(torch.zeros(8, 32, dtype=torch.uint8), 8, 128), "elements"),
+    (lambda: ops.int4_gemm_bf16_shuffled(torch.zeros(8 * 64, dtype=torch.uint8), torch.zeros(8, 1),
+                                         torch.zeros(8, 1, dtype=torch.uint8),
+                                         torch.zeros(4, 128, dtype=torch.bfloat16), 9, 128, 128),
+     "elements"),
+    (lambda: ops.int4_gemm_bf16_shuffled(torch.zeros(16 * 64, dtype=torch.uint8), torch.zeros(16, 1),
+                                         torch.zeros(16, 1, dtype=torch.uint8),
+                                         torch.zeros(4, 128, dtype=torch.float16), 16, 128, 128),
+     "dtype"),
 ])
 def test_bridge_validates_inputs_before_launch(call, match):
     """Wrong dtypes and sizes are rejected on the host with ValueError before

@@ -163,3 +163,25 @@ def test_stub_ops_raise_inside_their_span(gpu):
             ops.flash_attention(Q, Q.clone(), Q.clone(), H_kv=4, causal=True)
     assert spans and spans[0].name == "flash_attention"
     assert spans[0].attributes["causal"] is True and spans[0].attributes["head_dim"] == 64
+
+
+@pytest.mark.parametrize("m,rows,cols", [(4, 300, 2048), (16, 100, 4096), (1, 4096, 4096)])
+def test_bridge_shuffled_gemm(gpu, oracle, m, rows, cols):
+    """int4_shuffle_mfma + int4_gemm_bf16_shuffled: bit for bit the
+    reference-layout int4_gemm_bf16 for m >= 2; m == 1 within the bf16 bar of
+    the fp64 oracle."""
+    torch = gpu
+    gs = 128
+    p, s, z = make_int4(rows, cols, gs, seed=rows + m)
+    xb = np.random.default_rng(m).standard_normal((m, cols)).astype(np.float32)
+    x = torch.from_numpy(xb).cuda().to(torch.bfloat16)
+    dp, ds, dz = _d(torch, p), _d(torch, s), _d(torch, z)
+    sh = ops.int4_shuffle_mfma(dp, rows, cols)
+    assert sh.numel() == (rows + 15) // 16 * 16 * cols // 2
+    y = ops.int4_gemm_bf16_shuffled(sh, ds, dz, x, rows, cols, gs)
+    if m > 1:
+        assert torch.equal(y.view(torch.int16), ops.int4_gemm_bf16(dp, ds, dz, x, rows, cols, gs).view(torch.int16))
+    else:
+        xbits = (x.float().cpu().numpy().view(np.uint32) >> 16).astype(np.uint16)
+        truth = oracle.gemm_int4_bf16_f64(p, s, z.reshape(-1), xbits, 1, rows, cols, gs)
+        assert rel_l2(y.float().cpu().numpy(), truth) < 3e-3
