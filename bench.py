@@ -242,17 +242,26 @@ def counter_probe(args, torch, lib, dev) -> int:
           torch.empty(n, g, device=dev).uniform_(0.005, 0.02, generator=gen),
           torch.randint(0, 256, (n, g // 2), dtype=torch.uint8, device=dev, generator=gen))
          for _ in range(8)]                                                      # 1 GB
-    for m in (4, 16, 64):
-        x = torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16)
-        y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
-        for j in range(10):
-            p, sc, z = w[j % len(w)]
-            st = lib.kc_gemm_int4_bf16(p.data_ptr(), sc.data_ptr(), z.data_ptr(), x.data_ptr(),
-                                       y.data_ptr(), m, n, k, GS, stream)
-            if st:
-                raise RuntimeError(lib.kc_last_error_string().decode())
-        torch.cuda.synchronize()
-    del w
+    ws = []                                                                      # the same, shuffled
+    for p, _, _ in w:
+        sbuf = torch.empty(lib.kc_shuffled_int4_bytes(n, k), dtype=torch.uint8, device=dev)
+        if lib.kc_shuffle_int4_mfma(p.data_ptr(), sbuf.data_ptr(), n, k, stream):
+            raise RuntimeError(lib.kc_last_error_string().decode())
+        ws.append(sbuf)
+    torch.cuda.synchronize()
+    for fn, shuffled in ((lib.kc_gemm_int4_bf16, False), (lib.kc_gemm_int4_bf16_shuffled, True)):
+        for m in (4, 16, 64):
+            x = torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16)
+            y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            for j in range(10):
+                p, sc, z = w[j % len(w)]
+                wp = ws[j % len(ws)] if shuffled else p
+                st = fn(wp.data_ptr(), sc.data_ptr(), z.data_ptr(), x.data_ptr(), y.data_ptr(), m, n,
+                        k, GS, stream)
+                if st:
+                    raise RuntimeError(lib.kc_last_error_string().decode())
+            torch.cuda.synchronize()
+    del w, ws
     # the FP8 W8A8 GEMM at the cfg4 consumer shape
     t4, d4, n4 = 16384, 8192, 28672
     qx = torch.randint(-128, 128, (t4, d4), dtype=torch.int8, device=dev, generator=gen)
@@ -268,8 +277,8 @@ def counter_probe(args, torch, lib, dev) -> int:
         if st:
             raise RuntimeError(lib.kc_last_error_string().decode())
     torch.cuda.synchronize()
-    print("mfma probe done: 10 x cfg3 GEMM at M 4, 16, 64; 3 x FP8 GEMM 16384 x 28672 x 8192",
-          flush=True)
+    print("mfma probe done: 10 x cfg3 GEMM at M 4, 16, 64 on the reference layout, then on the "
+          "shuffled layout; 3 x FP8 GEMM 16384 x 28672 x 8192", flush=True)
     return 0
 
 
@@ -374,7 +383,8 @@ def main() -> int:
                     help="measure only the stream floors (reads of each GEMV's weight bytes, "
                          "quantizer-shaped copies, an empty launch), print them as JSON, exit")
     ap.add_argument("--mfma-probe", action="store_true",
-                    help="for rocprofv3 --pmc: launch the cfg3 GEMMs (M 4, 16, 64) 10 times "
+                    help="for rocprofv3 --pmc: launch the cfg3 GEMMs (M 4, 16, 64; reference, then "
+                         "shuffled layout) 10 times "
                          "each and the FP8 W8A8 GEMM (cfg4 shape) 3 times, then exit")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
