@@ -273,6 +273,20 @@ int kc_col_absmax_f32(const float* d_input, float* d_amax, int64_t rows,
 /* s[c] = max(sqrt(amax_x[c]) / sqrt(max(amax_w[c], 1e-5)), 1e-5) */
 int kc_smooth_factors(const float* d_amax_x, const float* d_amax_w,
                       float* d_smooth, int64_t cols, kc_stream_t stream);
+/* The SmoothQuant statistics of X [tokens, cols] and W [out_features,
+ * cols] in one call: d_amax_x, d_amax_w and d_smooth [cols] get exactly what
+ * kc_col_absmax_* on X, on W and kc_smooth_factors give, in three launches
+ * instead of five (one fill for both maxima, one reduction grid over both
+ * tensors).  No counterpart in the reference, which has no SmoothQuant
+ * statistics (BASELINE cfg4 defines them). */
+int kc_smoothquant_stats_bf16(const uint16_t* d_x, int64_t tokens,
+                              const uint16_t* d_w, int64_t out_features,
+                              int64_t cols, float* d_amax_x, float* d_amax_w,
+                              float* d_smooth, kc_stream_t stream);
+int kc_smoothquant_stats_f32(const float* d_x, int64_t tokens,
+                             const float* d_w, int64_t out_features,
+                             int64_t cols, float* d_amax_x, float* d_amax_w,
+                             float* d_smooth, kc_stream_t stream);
 /* One pass: X / s, per-row absmax, scale, E4M3.  Bit-identical to
  * launch_smoothquant_scale followed by launch_quantize_fp8(per_token). */
 int kc_quantize_fp8_smooth_div_f32(const float* d_input, const float* d_smooth,

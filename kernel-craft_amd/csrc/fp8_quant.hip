@@ -590,15 +590,15 @@ __global__ __launch_bounds__(kThreads) void fill_zero_kernel(float* __restrict__
 // 50-65 us: with few row phases too little is in flight, with many the
 // atomics at the end of the kernel cost more than they save.
 template <bool BF16>
-__global__ __launch_bounds__(kThreads) void col_absmax_kernel(const void* __restrict__ in,
-                                                              float* __restrict__ amax,
-                                                              int64_t rows, int64_t cols,
-                                                              int64_t tiles_per_band, bool vec) {
+__device__ __forceinline__ void col_absmax_block(const void* __restrict__ in,
+                                                 float* __restrict__ amax, int64_t rows,
+                                                 int64_t cols, int64_t tiles_per_band, bool vec,
+                                                 int64_t block) {
     constexpr int kVals = BF16 ? 8 : 4;              // columns per 16-byte slot
     constexpr int kTileCols = 32 * kVals;
     __shared__ float red[8][kTileCols];
-    const int64_t band = blockIdx.x / tiles_per_band;
-    const int64_t tile = blockIdx.x - band * tiles_per_band;
+    const int64_t band = block / tiles_per_band;
+    const int64_t tile = block - band * tiles_per_band;
     const int cg = threadIdx.x & 31, rg = threadIdx.x >> 5;
     const int64_t c = tile * kTileCols + cg * kVals;
     const int64_t r0 = band * kAbsmaxRowsPerBlock;
@@ -661,6 +661,38 @@ __global__ __launch_bounds__(kThreads) void col_absmax_kernel(const void* __rest
 #pragma unroll
         for (int g = 1; g < 8; ++g) v = fmaxf(v, red[g][col]);
         atomicMax(reinterpret_cast<unsigned int*>(amax) + gc, __float_as_uint(v));
+    }
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(kThreads) void col_absmax_kernel(const void* __restrict__ in,
+                                                              float* __restrict__ amax,
+                                                              int64_t rows, int64_t cols,
+                                                              int64_t tiles_per_band, bool vec) {
+    col_absmax_block<BF16>(in, amax, rows, cols, tiles_per_band, vec, blockIdx.x);
+}
+
+// Both column maxima of the SmoothQuant statistics in one grid: the first
+// blocks_a blocks reduce A (rows_a x cols) into amax_a, the rest B into
+// amax_b.  The two tensors' bands share one launch, so B's blocks fill the
+// CUs that A's last blocks leave idle.
+template <bool BF16>
+__global__ __launch_bounds__(kThreads) void col_absmax2_kernel(
+    const void* __restrict__ a, float* __restrict__ amax_a, int64_t rows_a, bool vec_a,
+    int64_t blocks_a, const void* __restrict__ b, float* __restrict__ amax_b, int64_t rows_b,
+    bool vec_b, int64_t cols, int64_t tiles_per_band) {
+    const int64_t blk = blockIdx.x;
+    if (blk < blocks_a) col_absmax_block<BF16>(a, amax_a, rows_a, cols, tiles_per_band, vec_a, blk);
+    else col_absmax_block<BF16>(b, amax_b, rows_b, cols, tiles_per_band, vec_b, blk - blocks_a);
+}
+
+// Zeroes p[0, n) and q[0, n).
+__global__ __launch_bounds__(kThreads) void fill_zero2_kernel(float* __restrict__ p,
+                                                              float* __restrict__ q, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kThreads) {
+        p[i] = 0.0f;
+        q[i] = 0.0f;
     }
 }
 
@@ -897,6 +929,43 @@ int col_absmax(const char* fn, const void* in, float* amax, int64_t rows, int64_
     return kc::check_launch(fn);
 }
 
+// X [tokens, cols] and W [out, cols]: amax_x, amax_w and the smoothing
+// factors in three launches (one fill for both maxima, one reduction grid
+// over both tensors, the factors), with the values of col_absmax on each
+// tensor followed by smooth_factors.
+template <bool BF16>
+int smoothquant_stats(const char* fn, const void* x, int64_t tokens, const void* w, int64_t outs,
+                      int64_t cols, float* amax_x, float* amax_w, float* smooth,
+                      hipStream_t stream) {
+    int st = check_rows(fn, x, amax_x, amax_x, tokens, cols);
+    if (st != KC_SUCCESS) return st;
+    if ((st = check_rows(fn, w, amax_w, amax_w, outs, cols)) != KC_SUCCESS) return st;
+    if (cols == 0) return KC_SUCCESS;
+    if (!amax_x || !amax_w || !smooth)
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: null device pointer", fn);
+    const int64_t fill_blocks = std::min<int64_t>((cols + kThreads - 1) / kThreads, 1024);
+    fill_zero2_kernel<<<static_cast<unsigned>(fill_blocks), kThreads, 0, stream>>>(amax_x, amax_w,
+                                                                                  cols);
+    if ((st = kc::check_launch(fn)) != KC_SUCCESS) return st;
+    constexpr int64_t kCols = 32 * (BF16 ? 8 : 4);  // columns per block
+    const int64_t tiles = (cols + kCols - 1) / kCols;
+    const int64_t blocks_x = (tokens + kAbsmaxRowsPerBlock - 1) / kAbsmaxRowsPerBlock * tiles;
+    const int64_t blocks_w = (outs + kAbsmaxRowsPerBlock - 1) / kAbsmaxRowsPerBlock * tiles;
+    if (blocks_x + blocks_w > INT32_MAX)
+        return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: tensors too large", fn);
+    if (blocks_x + blocks_w > 0) {
+        const bool vec_x = cols % (BF16 ? 8 : 4) == 0 && kc::aligned(x, 16);
+        const bool vec_w = cols % (BF16 ? 8 : 4) == 0 && kc::aligned(w, 16);
+        col_absmax2_kernel<BF16><<<static_cast<unsigned>(blocks_x + blocks_w), kThreads, 0, stream>>>(
+            x, amax_x, tokens, vec_x, blocks_x, w, amax_w, outs, vec_w, cols, tiles);
+        if ((st = kc::check_launch(fn)) != KC_SUCCESS) return st;
+    }
+    const int64_t blocks = std::min<int64_t>((cols + kThreads - 1) / kThreads, 1024);
+    smooth_factor_kernel<<<static_cast<unsigned>(blocks), kThreads, 0, stream>>>(amax_x, amax_w,
+                                                                                smooth, cols);
+    return kc::check_launch(fn);
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -961,6 +1030,20 @@ extern "C" int kc_col_absmax_bf16(const uint16_t* d_input, float* d_amax, int64_
 extern "C" int kc_col_absmax_f32(const float* d_input, float* d_amax, int64_t rows, int64_t cols,
                                  kc_stream_t stream) {
     return col_absmax<false>("kc_col_absmax_f32", d_input, d_amax, rows, cols, stream);
+}
+
+extern "C" int kc_smoothquant_stats_bf16(const uint16_t* d_x, int64_t tokens, const uint16_t* d_w,
+                                         int64_t out_features, int64_t cols, float* d_amax_x,
+                                         float* d_amax_w, float* d_smooth, kc_stream_t stream) {
+    return smoothquant_stats<true>("kc_smoothquant_stats_bf16", d_x, tokens, d_w, out_features, cols,
+                                   d_amax_x, d_amax_w, d_smooth, stream);
+}
+
+extern "C" int kc_smoothquant_stats_f32(const float* d_x, int64_t tokens, const float* d_w,
+                                        int64_t out_features, int64_t cols, float* d_amax_x,
+                                        float* d_amax_w, float* d_smooth, kc_stream_t stream) {
+    return smoothquant_stats<false>("kc_smoothquant_stats_f32", d_x, tokens, d_w, out_features, cols,
+                                    d_amax_x, d_amax_w, d_smooth, stream);
 }
 
 extern "C" int kc_smooth_factors(const float* d_amax_x, const float* d_amax_w, float* d_smooth,

@@ -134,6 +134,8 @@ PROTOTYPES = {
     "kc_col_absmax_bf16": ([_vp, _vp, _i64, _i64, _vp], _i),
     "kc_col_absmax_f32": ([_vp, _vp, _i64, _i64, _vp], _i),
     "kc_smooth_factors": ([_vp, _vp, _vp, _i64, _vp], _i),
+    "kc_smoothquant_stats_bf16": ([_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _vp], _i),
+    "kc_smoothquant_stats_f32": ([_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _vp], _i),
     "kc_quantize_fp8_smooth_div_f32": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp], _i),
     "kc_quantize_fp8_smooth_div_bf16": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp], _i),
     "kc_quantize_fp8_smooth_mul_bf16": ([_vp, _vp, _vp, _vp, _i64, _i64, _vp], _i),
@@ -698,6 +700,31 @@ def smooth_factors(amax_x, amax_w):
                                       _stream())
     _check("smooth_factors", st)
     return s
+
+
+def smoothquant_stats(x, w) -> Tuple:
+    """SmoothQuant statistics of activations x [tokens, cols] and weights
+    w [out_features, cols] (both bf16 or both fp32) in one library call:
+    (amax_x, amax_w, smooth), the values col_absmax(x), col_absmax(w) and
+    smooth_factors give."""
+    import torch
+    x = _arg("smoothquant_stats: x", x, (torch.float32, torch.bfloat16))
+    w = _arg("smoothquant_stats: w", w, x.dtype)
+    if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1]:
+        raise ValueError(f"smoothquant_stats: x {tuple(x.shape)} and w {tuple(w.shape)} must be "
+                         "2-D with the same number of columns")
+    _on_gpu("smoothquant_stats", x, w)
+    cols = x.shape[1]
+    amax_x = torch.empty(cols, dtype=torch.float32, device=x.device)
+    amax_w = torch.empty_like(amax_x)
+    s = torch.empty_like(amax_x)
+    lib = _get_lib()
+    fn = lib.kc_smoothquant_stats_bf16 if x.dtype == torch.bfloat16 else lib.kc_smoothquant_stats_f32
+    with kernel_span("smoothquant_stats", tokens=x.shape[0], out_features=w.shape[0], cols=cols):
+        st = fn(_ptr(x), x.shape[0], _ptr(w), w.shape[0], cols, _ptr(amax_x), _ptr(amax_w), _ptr(s),
+                _stream())
+    _check("smoothquant_stats", st)
+    return amax_x, amax_w, s
 
 
 def fp8_quantize_smooth(x, smooth, mode: str = "div") -> Tuple:

@@ -256,6 +256,12 @@ def test_bridge_span_fallback_accepts_attributes(tmp_path):
     (lambda: ops.fp8_gemm_w8a8(torch.zeros(4, 64, dtype=torch.int8), torch.ones(4),
                                torch.zeros(8, 32, dtype=torch.int8), torch.ones(8)), "share K"),
     (lambda: ops.smooth_factors(torch.ones(8), torch.ones(7)), "elements"),
+    (lambda: ops.smoothquant_stats(torch.zeros(4, 64, dtype=torch.float16),
+                                   torch.zeros(8, 64, dtype=torch.float16)), "dtype"),
+    (lambda: ops.smoothquant_stats(torch.zeros(4, 64, dtype=torch.bfloat16), torch.zeros(8, 64)),
+     "dtype"),
+    (lambda: ops.smoothquant_stats(torch.zeros(4, 64), torch.zeros(8, 32)), "same number of columns"),
+    (lambda: ops.smoothquant_stats(torch.zeros(4, 64), torch.zeros(8, 64)), "GPU only"),
     (lambda: ops.rmsnorm(torch.zeros(2, 64, dtype=torch.float16), torch.ones(64)), "dtype"),
     (lambda: ops.int4_shuffle_mfma(torch.zeros(8, 48, dtype=torch.uint8), 8, 96), "multiple of 128"),
     (lambda: ops.int4_shuffle_mfma(torch.zeros(8, 32, dtype=torch.uint8), 8, 128), "elements"),

@@ -487,6 +487,66 @@ def test_col_absmax_shapes(gpu, oracle, dtype, rows, cols):
     np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), exp.view(np.uint32))
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("T,N,D", [(256, 384, 8192), (1, 1, 8), (130, 257, 4104), (300, 7, 20),
+                                   (0, 64, 2048), (64, 0, 2048), (5, 3, 1000)])
+def test_smoothquant_stats_one_call(gpu, oracle, dtype, T, N, D):
+    """kc_smoothquant_stats_* (both maxima and the factors from one call)
+    equals kc_col_absmax_* on X and on W followed by kc_smooth_factors, bit
+    for bit, and the oracle: band and tile tails, the scalar path (cols not a
+    multiple of the 16-byte slot), empty X or W, NaN, signaling NaN and inf."""
+    torch = gpu
+    L = kc_abi.lib()
+    rng = np.random.default_rng(T * 7 + N * 13 + D)
+    x = (rng.standard_normal((T, D)) * rng.uniform(0.1, 50.0, D)).astype(np.float32)
+    w = (rng.standard_normal((N, D)) * 0.02).astype(np.float32)
+    if T > 2 and D > 4:
+        x[1, 2] = np.nan
+        x[T - 1, 0] = np.array([0x7F800001], np.uint32).view(np.float32)[0]
+        x[0, 3] = -np.inf
+    if N > 1 and D > 5:
+        w[N - 1, 5] = np.array([0xFFA00000], np.uint32).view(np.float32)[0]
+    if dtype == "bf16":
+        xh, wh = f32_to_bf16_bits(x), f32_to_bf16_bits(w)
+        dx, dw = _dev_bf16(torch, xh), _dev_bf16(torch, wh)
+        fused, absmax = L.kc_smoothquant_stats_bf16, L.kc_col_absmax_bf16
+    else:
+        xh, wh = x, w
+        dx, dw = _dev(torch, x), _dev(torch, w)
+        fused, absmax = L.kc_smoothquant_stats_f32, L.kc_col_absmax_f32
+    out = [torch.full((D,), float("nan"), dtype=torch.float32, device="cuda") for _ in range(6)]
+    kc_abi.check("kc_smoothquant_stats", fused(ptr(dx), T, ptr(dw), N, D, ptr(out[0]), ptr(out[1]),
+                                               ptr(out[2]), stream()))
+    for st in (absmax(ptr(dx), ptr(out[3]), T, D, stream()), absmax(ptr(dw), ptr(out[4]), N, D, stream()),
+               L.kc_smooth_factors(ptr(out[3]), ptr(out[4]), ptr(out[5]), D, stream())):
+        kc_abi.check("three-call statistics", st)
+    got = [o.cpu().numpy() for o in out]
+    for a, b in zip(got[:3], got[3:]):
+        np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+    eax = oracle.col_absmax(xh) if T else np.zeros(D, np.float32)
+    eaw = oracle.col_absmax(wh) if N else np.zeros(D, np.float32)
+    np.testing.assert_array_equal(got[0].view(np.uint32), eax.view(np.uint32))
+    np.testing.assert_array_equal(got[1].view(np.uint32), eaw.view(np.uint32))
+    np.testing.assert_array_equal(got[2], oracle.smooth_factors(eax, eaw))
+
+
+def test_smoothquant_stats_cfg4_bridge(gpu):
+    """The bridge op on cfg4's full shapes (X [16384, 8192], W [28672, 8192]
+    bf16) against the three-call statistics on the same device tensors."""
+    torch = gpu
+    import kernel_craft_torch_ops as ops
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4004)
+    X = torch.randn(16384, 8192, device="cuda", generator=g).to(torch.bfloat16)
+    X[:, ::200] *= 100
+    W = (torch.randn(28672, 8192, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    ax, aw, s = ops.smoothquant_stats(X, W)
+    ex, ew = ops.col_absmax(X), ops.col_absmax(W)
+    es = ops.smooth_factors(ex, ew)
+    assert torch.equal(ax, ex) and torch.equal(aw, ew) and torch.equal(s, es)
+    assert torch.equal(ax, X.float().abs().amax(0)) and torch.equal(aw, W.float().abs().amax(0))
+
+
 def test_smoothquant_fused_small(gpu, oracle):
     """cfg4 distributions at a size the oracle runs in seconds; every output
     bit-exact (absmax, factors, codes, scales)."""
