@@ -277,8 +277,15 @@ def counter_probe(args, torch, lib, dev) -> int:
         if st:
             raise RuntimeError(lib.kc_last_error_string().decode())
     torch.cuda.synchronize()
+    # the vendor library on the same codes and scales, for its counters beside ours
+    a8, b8 = qx.view(torch.float8_e4m3fn), qw.view(torch.float8_e4m3fn)
+    for _ in range(3):
+        torch._scaled_mm(a8, b8.t(), scale_a=sx.view(-1, 1), scale_b=sw.view(1, -1),
+                         out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
     print("mfma probe done: 10 x cfg3 GEMM at M 4, 16, 64 on the reference layout, then on the "
-          "shuffled layout; 3 x FP8 GEMM 16384 x 28672 x 8192", flush=True)
+          "shuffled layout; 3 x FP8 GEMM 16384 x 28672 x 8192, then 3 x torch._scaled_mm on the "
+          "same codes", flush=True)
     return 0
 
 
@@ -417,27 +424,39 @@ def main() -> int:
     copies = max(2, math.ceil(ROTATE_BYTES / w_bytes))
     gen = torch.Generator(device=dev)
     gen.manual_seed(2024)
-    layers = []
-    for _ in range(copies):
-        layer = []
-        for _, n, k in LLAMA:
-            g = k // GS
-            packed = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=dev, generator=gen)
-            scales = torch.empty(n, g, device=dev).uniform_(0.005, 0.02, generator=gen)
-            zeros = torch.randint(0, 256, (n, g // 2), dtype=torch.uint8, device=dev, generator=gen)
-            layer.append((packed, scales, zeros))
-        layers.append(layer)
+
+    def new_weights(n: int, k: int) -> tuple:
+        g = k // GS
+        packed = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=dev, generator=gen)
+        scales = torch.empty(n, g, device=dev).uniform_(0.005, 0.02, generator=gen)
+        zeros = torch.randint(0, 256, (n, g // 2), dtype=torch.uint8, device=dev, generator=gen)
+        return packed, scales, zeros
+    layers = [[new_weights(n, k) for _, n, k in LLAMA] for _ in range(copies)]
+    # a timing loop that launches one projection back to back rotates over
+    # that projection's own copies, at least ROTATE_BYTES of them: the layer's
+    # ten copies of QKV (135 MB) or O (90 MB) alone would fit in the cache
+    pools = []
+    for i, (_, n, k) in enumerate(LLAMA):
+        need = max(copies, math.ceil(ROTATE_BYTES / (n * k // 2 + n * (k // GS) * 9 // 2)))
+        pools.append([layers[r][i] for r in range(copies)]
+                     + [new_weights(n, k) for _ in range(need - copies)])
     xs = [torch.randn(k, device=dev, generator=gen).to(torch.bfloat16) for _, _, k in LLAMA]
     ys = [torch.empty(n, dtype=torch.bfloat16, device=dev) for _, n, _ in LLAMA]
     fn = lib.kc_gemv_int4_bf16
 
-    def launch(r: int, i: int) -> None:
+    def launch_w(w: tuple, i: int) -> None:
         _, n, k = LLAMA[i]
-        p, s, z = layers[r][i]
+        p, s, z = w
         st = fn(p.data_ptr(), s.data_ptr(), z.data_ptr(), xs[i].data_ptr(), ys[i].data_ptr(),
                 n, k, GS, torch.cuda.current_stream().cuda_stream)
         if st:
             raise RuntimeError(f"kc_gemv_int4_bf16 failed: {lib.kc_last_error_string().decode()}")
+
+    def launch(r: int, i: int) -> None:         # copy r of the layer
+        launch_w(layers[r][i], i)
+
+    def launch_op(j: int, i: int) -> None:      # the j-th launch of projection i alone
+        launch_w(pools[i][j % len(pools[i])], i)
 
     if args.gemv_probe:
         # every decode shape and the cfg0 fp32 GEMV, 20 launches each over
@@ -459,7 +478,7 @@ def main() -> int:
         y32 = torch.empty(4096, device=dev)
         for i, (name, n, k) in enumerate(LLAMA):
             for j in range(20):
-                launch(j % copies, i)
+                launch_op(j, i)
             torch.cuda.synchronize()
             wb = n * k // 2 + n * (k // GS) * 4 + n * (k // GS) // 2
             wb -= wb % 16
@@ -478,7 +497,7 @@ def main() -> int:
         del fbuf
         o = 1                                    # O projection's weights, fp32 x and y
         for j in range(20):
-            p, s_, z = layers[j % copies][o]
+            p, s_, z = pools[o][j % len(pools[o])]
             st = lib.kc_gemv_int4_f32_async(p.data_ptr(), s_.data_ptr(), z.data_ptr(),
                                             x32.data_ptr(), y32.data_ptr(), 4096, 4096, GS,
                                             torch.cuda.current_stream().cuda_stream)
@@ -497,7 +516,7 @@ def main() -> int:
         src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
         for j in range(20):
-            launch(j % copies, DOMINANT)
+            launch_op(j, DOMINANT)
         torch.cuda.synchronize()
         for _ in range(20):
             dst.copy_(src)
@@ -591,7 +610,7 @@ def main() -> int:
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
         for j in range(reps):
-            launch(j % copies, i)
+            launch_op(j, i)
         e1.record()
         torch.cuda.synchronize()
         kernel_us[name] = e0.elapsed_time(e1) * 1e3 / reps
@@ -600,37 +619,37 @@ def main() -> int:
     # ---- the same GEMVs on the pre-shuffled layout (kc_shuffle_int4_mfma once,
     # then kc_gemm_int4_bf16_shuffled at M = 1): the matrix-core GEMV, which
     # reads each 16-row tile 1 KB at a time; same bytes, same rotation
-    shuf = [[None] * len(LLAMA) for _ in range(copies)]
-    for r in range(copies):
-        for i, (_, n, k) in enumerate(LLAMA):
-            p = layers[r][i][0]
+    ys_sh = [torch.empty(1, n, dtype=torch.bfloat16, device=dev) for _, n, _ in LLAMA]
+    xs2 = [x.view(1, -1) for x in xs]
+    shuffled_us = {}
+    for i, (name, n, k) in enumerate(LLAMA):
+        shuf = []
+        for p, _, _ in pools[i]:
             sbuf = torch.empty(lib.kc_shuffled_int4_bytes(n, k), dtype=torch.uint8, device=dev)
             if lib.kc_shuffle_int4_mfma(p.data_ptr(), sbuf.data_ptr(), n, k,
                                         torch.cuda.current_stream().cuda_stream):
                 raise RuntimeError(f"kc_shuffle_int4_mfma: {lib.kc_last_error_string().decode()}")
-            shuf[r][i] = sbuf
-    ys_sh = [torch.empty(1, n, dtype=torch.bfloat16, device=dev) for _, n, _ in LLAMA]
-    xs2 = [x.view(1, -1) for x in xs]
+            shuf.append(sbuf)
 
-    def launch_shuf(r: int, i: int) -> None:
-        _, n, k = LLAMA[i]
-        _, s_, z = layers[r][i]
-        st = lib.kc_gemm_int4_bf16_shuffled(shuf[r][i].data_ptr(), s_.data_ptr(), z.data_ptr(),
-                                            xs2[i].data_ptr(), ys_sh[i].data_ptr(), 1, n, k, GS,
-                                            torch.cuda.current_stream().cuda_stream)
-        if st:
-            raise RuntimeError(f"kc_gemm_int4_bf16_shuffled: {lib.kc_last_error_string().decode()}")
-    shuffled_us = {}
-    for i, (name, n, k) in enumerate(LLAMA):
-        launch_shuf(0, i)
-        launch(0, i)
+        def launch_shuf(j: int, i=i, n=n, k=k, shuf=shuf) -> None:
+            r = j % len(shuf)
+            _, s_, z = pools[i][r]
+            st = lib.kc_gemm_int4_bf16_shuffled(shuf[r].data_ptr(), s_.data_ptr(), z.data_ptr(),
+                                                xs2[i].data_ptr(), ys_sh[i].data_ptr(), 1, n, k,
+                                                GS, torch.cuda.current_stream().cuda_stream)
+            if st:
+                raise RuntimeError(f"kc_gemm_int4_bf16_shuffled: "
+                                   f"{lib.kc_last_error_string().decode()}")
+        launch_shuf(0)
+        launch_op(0, i)
         torch.cuda.synchronize()
         err = ((ys_sh[i].float().view(-1) - ys[i].float()).norm() / ys[i].float().norm()).item()
         if not err < 3e-3:
             print(f"bench.py: shuffled-layout GEMV disagrees for {name}: rel L2 {err:.3e}",
                   file=sys.stderr)
             return 1
-        shuffled_us[name] = time_launches(torch, lambda j, i=i: launch_shuf(j % copies, i), reps)
+        shuffled_us[name] = time_launches(torch, launch_shuf, reps)
+        del shuf
         log(f"# {name:8s} shuffled layout: {shuffled_us[name]:7.2f} us/launch "
             f"(reference layout {kernel_us[name]:.2f})")
     shuffled = {"kernel_us": {k: round(v, 3) for k, v in shuffled_us.items()},
@@ -639,7 +658,6 @@ def main() -> int:
                 "config": "the decode layer's GEMVs at M = 1 on the pre-shuffled layout "
                           "(kc_shuffle_int4_mfma, kc_gemm_int4_bf16_shuffled), one launch each, "
                           "events as kernel_us"}
-    del shuf
 
     dom_name, dom_n, dom_k = LLAMA[DOMINANT]
     dom_bytes = gemv_bytes(dom_n, dom_k)
@@ -763,11 +781,22 @@ def main() -> int:
 
     # ---- BASELINE cfg4: SmoothQuant + FP8, X bf16 [16384, 8192], W bf16 [28672, 8192]
     T4, D4, N4 = 16384, 8192, 28672
-    X4 = torch.randn(T4, D4, device=dev, generator=gen)
     outl4 = torch.randperm(D4, device=dev, generator=gen)[:D4 // 200]
-    X4[:, outl4] *= 100.0                     # 0.5 % outlier channels x100
-    X4 = X4.to(torch.bfloat16)
-    W4 = (torch.randn(N4, D4, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+
+    def new_x4():
+        x = torch.randn(T4, D4, device=dev, generator=gen)
+        x[:, outl4] *= 100.0                  # 0.5 % outlier channels x100
+        return x.to(torch.bfloat16)
+    # X (268 MB) and W (470 MB) each rotate over at least ROTATE_BYTES of copies
+    X4s = [new_x4() for _ in range(max(2, math.ceil(ROTATE_BYTES / (T4 * D4 * 2))))]
+    W4s = [(torch.randn(N4, D4, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+           for _ in range(max(2, math.ceil(ROTATE_BYTES / (N4 * D4 * 2))))]
+
+    def x4(j: int):
+        return X4s[j % len(X4s)]
+
+    def w4(j: int):
+        return W4s[j % len(W4s)]
     ax, aw, sm = (torch.empty(D4, device=dev) for _ in range(3))
     qx = torch.empty(T4, D4, dtype=torch.int8, device=dev)
     qw = torch.empty(N4, D4, dtype=torch.int8, device=dev)
@@ -775,22 +804,22 @@ def main() -> int:
     sw = torch.empty(N4, device=dev)
 
     def cfg4_stats(j: int) -> None:  # one library call: both column maxima and the factors
-        ck(lib.kc_smoothquant_stats_bf16(X4.data_ptr(), T4, W4.data_ptr(), N4, D4, ax.data_ptr(),
+        ck(lib.kc_smoothquant_stats_bf16(x4(j).data_ptr(), T4, w4(j).data_ptr(), N4, D4, ax.data_ptr(),
                                          aw.data_ptr(), sm.data_ptr(), stream_ptr()),
            "smoothquant stats")
 
     def cfg4_stats_calls(j: int) -> None:  # the same as three calls (five launches)
-        ck(lib.kc_col_absmax_bf16(X4.data_ptr(), ax.data_ptr(), T4, D4, stream_ptr()), "absmax X")
-        ck(lib.kc_col_absmax_bf16(W4.data_ptr(), aw.data_ptr(), N4, D4, stream_ptr()), "absmax W")
+        ck(lib.kc_col_absmax_bf16(x4(j).data_ptr(), ax.data_ptr(), T4, D4, stream_ptr()), "absmax X")
+        ck(lib.kc_col_absmax_bf16(w4(j).data_ptr(), aw.data_ptr(), N4, D4, stream_ptr()), "absmax W")
         ck(lib.kc_smooth_factors(ax.data_ptr(), aw.data_ptr(), sm.data_ptr(), D4, stream_ptr()),
            "smooth factors")
 
     def cfg4_qx(j: int) -> None:
-        ck(lib.kc_quantize_fp8_smooth_div_bf16(X4.data_ptr(), sm.data_ptr(), qx.data_ptr(),
+        ck(lib.kc_quantize_fp8_smooth_div_bf16(x4(j).data_ptr(), sm.data_ptr(), qx.data_ptr(),
                                                sx.data_ptr(), T4, D4, stream_ptr()), "quantize X")
 
     def cfg4_qw(j: int) -> None:
-        ck(lib.kc_quantize_fp8_smooth_mul_bf16(W4.data_ptr(), sm.data_ptr(), qw.data_ptr(),
+        ck(lib.kc_quantize_fp8_smooth_mul_bf16(w4(j).data_ptr(), sm.data_ptr(), qw.data_ptr(),
                                                sw.data_ptr(), N4, D4, stream_ptr()), "quantize W")
     stats_b = T4 * D4 * 2 + N4 * D4 * 2 + 2 * D4 * 4
     qx_b = T4 * D4 * 2 + T4 * D4 + T4 * 4 + D4 * 4
@@ -803,7 +832,8 @@ def main() -> int:
                 "quantize_x": hbm(qx_b, t_qx),
                 "quantize_w": hbm(qw_b, t_qw),
                 "total": hbm(stats_b + qx_b + qw_b, t_stats + t_qx + t_qw),
-                "config": "cfg4: col absmax X and W + smooth factors (alpha 0.5) in one call "
+                "config": "cfg4 (X and W rotating over 4 and 3 copies): col absmax X and W + "
+                          "smooth factors (alpha 0.5) in one call "
                           "(kc_smoothquant_stats_bf16; three_calls_us: col absmax X, col absmax W, "
                           "factors); X/s per-token and W*s per-channel to E4M3, bf16 in"}
     log(f"# cfg4 smoothquant+fp8: stats {t_stats:.1f} us, X {t_qx:.1f} us "
@@ -845,12 +875,12 @@ def main() -> int:
     xn4 = torch.empty(T4, D4, dtype=torch.bfloat16, device=dev)
 
     def prologue_fused(j: int) -> None:
-        ck(lib.kc_rmsnorm_quantize_fp8_bf16(X4.data_ptr(), gam4.data_ptr(), 1e-6, qx.data_ptr(),
+        ck(lib.kc_rmsnorm_quantize_fp8_bf16(x4(j).data_ptr(), gam4.data_ptr(), 1e-6, qx.data_ptr(),
                                             sx.data_ptr(), T4, D4, stream_ptr()),
            "kc_rmsnorm_quantize_fp8_bf16")
 
     def prologue_two(j: int) -> None:
-        ck(lib.kc_rmsnorm_bf16(X4.data_ptr(), gam4.data_ptr(), xn4.data_ptr(), T4, D4, 1e-6,
+        ck(lib.kc_rmsnorm_bf16(x4(j).data_ptr(), gam4.data_ptr(), xn4.data_ptr(), T4, D4, 1e-6,
                                stream_ptr()), "kc_rmsnorm_bf16")
         ck(lib.kc_quantize_fp8_per_token_bf16(xn4.data_ptr(), qx.data_ptr(), sx.data_ptr(), T4,
                                               D4, stream_ptr()), "kc_quantize_fp8_per_token_bf16")
@@ -862,7 +892,7 @@ def main() -> int:
                           "against kc_rmsnorm_bf16 + kc_quantize_fp8_per_token_bf16")
     log(f"# fp8 prologue (rmsnorm -> fp8) cfg4 X: fused {prologue['avg_us']} us "
         f"({prologue['GBps']} GB/s), two launches {prologue['two_launches_us']} us")
-    del X4, W4, qx, qw, Y4, xn4
+    del X4s, W4s, qx, qw, Y4, xn4
 
     # ---- decode fusion: the RMSNorm in front of the QKV and gate/up GEMVs ----
     # (kc_rmsnorm_bf16 then kc_gemv_int4_bf16, against the fused launch)
@@ -877,14 +907,14 @@ def main() -> int:
         yf = torch.empty(n, dtype=torch.bfloat16, device=dev)
 
         def two(j: int, i=i, n=n, k=k, yf=yf) -> None:
-            p, sc, z = layers[j % copies][i]
+            p, sc, z = pools[i][j % len(pools[i])]
             ck(lib.kc_rmsnorm_bf16(h_.data_ptr(), gam.data_ptr(), xn.data_ptr(), 1, k, 1e-5,
                                    stream_ptr()), "kc_rmsnorm_bf16")
             ck(lib.kc_gemv_int4_bf16(p.data_ptr(), sc.data_ptr(), z.data_ptr(), xn.data_ptr(),
                                      yf.data_ptr(), n, k, GS, stream_ptr()), "kc_gemv_int4_bf16")
 
         def fused(j: int, i=i, n=n, k=k, yf=yf) -> None:
-            p, sc, z = layers[j % copies][i]
+            p, sc, z = pools[i][j % len(pools[i])]
             ck(lib.kc_rmsnorm_gemv_int4_bf16(h_.data_ptr(), gam.data_ptr(), 1e-5, p.data_ptr(),
                                              sc.data_ptr(), z.data_ptr(), yf.data_ptr(), n, k, GS,
                                              stream_ptr()), "kc_rmsnorm_gemv_int4_bf16")
@@ -958,6 +988,8 @@ def main() -> int:
         "config": {"workload": "int4_gemv_llama3_8b_decode_layer",
                    "shapes_NK": [[n, k] for _, n, k in LLAMA], "group_size": GS, "M": 1,
                    "bytes_per_step": layer_bytes, "rotation_copies": copies,
+                   "per_kernel_rotation_copies": {nm: len(pools[i])
+                                                  for i, (nm, _, _) in enumerate(LLAMA)},
                    "launch": launch_mode, "launch_modes_GBps": modes_gbs},
         "pct_of_peak": round(100.0 * value / PEAK_HBM_GBS, 2),
         "roofline": roofline,
