@@ -129,7 +129,8 @@ def _host(t):
 
 
 SHAPES = [(256, 64, 128), (4096, 4096, 128), (1024, 136, 32), (512, 72, 64), (896, 24, 64),
-          (4096, 448, 256)]
+          (4096, 448, 256),
+          (208, 136, 8)]  # K/8 = 26 words: the word-by-word stores; a partial 128-column tile
 
 
 @pytest.mark.gpu
