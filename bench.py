@@ -929,7 +929,7 @@ def main() -> int:
     kc_, nc_, gc_ = 4096, 28672, 4096 // GS
     conv_b = (kc_ * nc_ // 2 + gc_ * nc_ // 2 + gc_ * nc_ * 2      # qweight, qzeros, fp16 scales
               + nc_ * kc_ // 2 + nc_ * gc_ * 4 + nc_ * gc_ // 2)   # packed, fp32 scales, zeros
-    cv_copies = 4
+    cv_copies = max(2, math.ceil(ROTATE_BYTES / conv_b))   # sources and outputs, >= 1 GiB
     srcs = [(torch.randint(-2**31, 2**31 - 1, (kc_ // 8, nc_), dtype=torch.int32, device=dev,
                            generator=gen),
              torch.randint(-2**31, 2**31 - 1, (gc_, nc_ // 8), dtype=torch.int32, device=dev,
