@@ -99,13 +99,13 @@ __device__ __forceinline__ void transpose8x8_nibbles(uint32_t (&a)[8]) {
 // per row; every load of a thread issued before the first is used): for the
 // gate/up layer 26.1 -> 23.3 us per launch back to back, but only 32.7 -> 32.4
 // us for a whole conversion call (this kernel, then the scales and zero points).
-template <bool AWQ, bool PERM, int TN = kTile>
-__global__ __launch_bounds__(kThreads) void convert_packed_kernel(
+template <bool AWQ, bool PERM, int TN>
+__device__ __forceinline__ void convert_packed_tile(
     const int32_t* __restrict__ qweight, const int32_t* __restrict__ qzeros,
     const int32_t* __restrict__ perm, int K, int N, int gs, int zero_offset,
-    uint32_t* __restrict__ out, bool vec) {
+    uint32_t* __restrict__ out, bool vec, int b, int nb, uint32_t (*tile)[TN + 1]) {
     static_assert(TN == kTile || (!AWQ && !PERM), "wider tiles for the plain GPTQ source only");
-    __shared__ uint32_t tile[kTile][TN + 1];  // [word kb][column n]
+    // tile: [word kb][column n], kTile x (TN + 1) words of LDS
     const int KW = K >> 3;                       // output words per column
     const int NW = N >> 3;                       // source words per row (AWQ, qzeros)
     // Tiles in column-tile-major order.  AWQ reads 32 bytes of a source row
@@ -115,7 +115,6 @@ __global__ __launch_bounds__(kThreads) void convert_packed_kernel(
     // L2 (56 -> 36 us on the gate/up layer).  GPTQ reads 256 or (plain
     // source) 512 contiguous bytes per row and keeps the plain order (64-column
     // tiles: 35.1 us remapped, 33.5 plain).
-    const int b = blockIdx.x, nb = gridDim.x;
     const int xcd = b % 8, q = nb / 8, r = nb % 8;
     const int tile_id = AWQ ? xcd * q + min(xcd, r) + b / 8 : b;  // a bijection of [0, nb)
     const int ntn = (N + TN - 1) / TN;
@@ -215,12 +214,11 @@ __global__ __launch_bounds__(kThreads) void convert_packed_kernel(
 constexpr int kMetaCols = 64, kMetaGroups = 32;
 
 template <bool AWQ>
-__global__ __launch_bounds__(kThreads) void convert_meta_kernel(
+__device__ __forceinline__ void convert_meta_tile(
     const int32_t* __restrict__ qzeros, const uint16_t* __restrict__ scales16, int N, int G,
-    int zero_offset, float* __restrict__ scales, uint8_t* __restrict__ zeros) {
-    __shared__ float sv[kMetaGroups][kMetaCols + 1];
-    __shared__ uint8_t zv[kMetaGroups][kMetaCols + 4];
-    const int n0 = blockIdx.x * kMetaCols, g0 = blockIdx.y * kMetaGroups;
+    int zero_offset, float* __restrict__ scales, uint8_t* __restrict__ zeros, int bx, int by,
+    float (*sv)[kMetaCols + 1], uint8_t (*zv)[kMetaCols + 4]) {
+    const int n0 = bx * kMetaCols, g0 = by * kMetaGroups;
     const int t = threadIdx.x;
     // read: thread t handles column n0 + t % 64 of groups g0 + t / 64 + 4i
     for (int i = 0; i < kMetaGroups / 4; ++i) {
@@ -261,6 +259,35 @@ __global__ __launch_bounds__(kThreads) void convert_meta_kernel(
     }
 }
 
+// One launch for both parts: blocks [0, meta_blocks) convert scales and zero
+// points (tile (b % mx, b / mx) of 64 columns x 32 groups; blocks past the
+// last tile pad meta_blocks to a multiple of 8 and return), the rest the
+// packed weights, which then start on XCD 0 as in a launch of their own.  The
+// two parts share one LDS buffer.  Against two launches, the short
+// scales/zero-points tiles run beside the weight stream instead of after it.
+template <bool AWQ, bool PERM, int TN>
+__global__ __launch_bounds__(kThreads) void convert_kernel(
+    const int32_t* __restrict__ qweight, const int32_t* __restrict__ qzeros,
+    const int32_t* __restrict__ perm, const uint16_t* __restrict__ scales16, int K, int N, int gs,
+    int zero_offset, uint32_t* __restrict__ out, bool vec, float* __restrict__ scales,
+    uint8_t* __restrict__ zeros, int meta_blocks) {
+    constexpr int kPackedWords = kTile * (TN + 1);
+    constexpr int kMetaWords = kMetaGroups * (kMetaCols + 1) + kMetaGroups * (kMetaCols + 4) / 4;
+    __shared__ uint32_t smem[kPackedWords > kMetaWords ? kPackedWords : kMetaWords];
+    const int b = blockIdx.x;
+    if (b < meta_blocks) {
+        const int G = K / gs, mx = (N + kMetaCols - 1) / kMetaCols, my = (G + kMetaGroups - 1) / kMetaGroups;
+        if (b >= mx * my) return;
+        convert_meta_tile<AWQ>(qzeros, scales16, N, G, zero_offset, scales, zeros, b % mx, b / mx,
+                               reinterpret_cast<float (*)[kMetaCols + 1]>(smem),
+                               reinterpret_cast<uint8_t (*)[kMetaCols + 4]>(smem + kMetaGroups * (kMetaCols + 1)));
+        return;
+    }
+    convert_packed_tile<AWQ, PERM, TN>(qweight, qzeros, perm, K, N, gs, zero_offset, out, vec,
+                                       b - meta_blocks, static_cast<int>(gridDim.x) - meta_blocks,
+                                       reinterpret_cast<uint32_t (*)[TN + 1]>(smem));
+}
+
 int check_convert(const char* fn, const void* qweight, const void* qzeros, const void* scales16,
                   int K, int N, int gs, const void* packed, const void* scales, const void* zeros) {
     if (K <= 0 || N <= 0 || gs <= 0)
@@ -295,17 +322,16 @@ int convert(const char* fn, const int32_t* qweight, const int32_t* qzeros, const
         !kc::aligned(scales16, 2) || !kc::aligned(scales, 16) || (perm && !kc::aligned(perm, 4)))
         return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: misaligned pointer", fn);
     const bool vec = (K / 8) % 4 == 0 && kc::aligned(packed, 16);
-    if (AWQ)
-        convert_packed_kernel<true, false><<<grid, kThreads, 0, stream>>>(qweight, qzeros, nullptr, K, N, gs, 0, out, vec);
-    else if (perm)
-        convert_packed_kernel<false, true><<<grid, kThreads, 0, stream>>>(qweight, qzeros, perm, K, N, gs, zero_offset, out, vec);
-    else
-        convert_packed_kernel<false, false, kWide><<<grid, kThreads, 0, stream>>>(qweight, qzeros, nullptr, K, N, gs, zero_offset, out, vec);
-    if ((st = kc::check_launch(fn)) != KC_SUCCESS) return st;
     const int G = K / gs;
-    const dim3 mgrid((N + kMetaCols - 1) / kMetaCols, (G + kMetaGroups - 1) / kMetaGroups);
-    convert_meta_kernel<AWQ><<<mgrid, kThreads, 0, stream>>>(qzeros, scales16, N, G, zero_offset,
-                                                            scales, zeros);
+    const int meta = ((N + kMetaCols - 1) / kMetaCols) * ((G + kMetaGroups - 1) / kMetaGroups);
+    const int meta_blocks = (meta + 7) / 8 * 8;
+    const unsigned all = grid + static_cast<unsigned>(meta_blocks);
+    if (AWQ)
+        convert_kernel<true, false, kTile><<<all, kThreads, 0, stream>>>(qweight, qzeros, nullptr, scales16, K, N, gs, 0, out, vec, scales, zeros, meta_blocks);
+    else if (perm)
+        convert_kernel<false, true, kTile><<<all, kThreads, 0, stream>>>(qweight, qzeros, perm, scales16, K, N, gs, zero_offset, out, vec, scales, zeros, meta_blocks);
+    else
+        convert_kernel<false, false, kWide><<<all, kThreads, 0, stream>>>(qweight, qzeros, nullptr, scales16, K, N, gs, zero_offset, out, vec, scales, zeros, meta_blocks);
     return kc::check_launch(fn);
 }
 
