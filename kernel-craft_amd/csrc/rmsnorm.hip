@@ -216,23 +216,24 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fp8_wave_kernel(
     const uint16_t* __restrict__ h, const uint16_t* __restrict__ gamma, int8_t* __restrict__ out,
     float* __restrict__ scales, int64_t rows, int D, float eps) {
     using namespace kc::fp8;
+    // gamma, staged once per workgroup (its four rows share it): read from
+    // LDS at its use instead of held in registers across the reduction.
+    __shared__ u32x4 gl[NS * kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
-    if (row >= rows) return;
+    const bool live = row < rows;
     const int nslots = D / 8;
-    const u32x4* hs = reinterpret_cast<const u32x4*>(h + row * D);
+    const u32x4* hs = reinterpret_cast<const u32x4*>(h + (live ? row : 0) * D);
     const u32x4* gs = reinterpret_cast<const u32x4*>(gamma);
-    u32x4 xv[NS], gv[NS];
+    u32x4 xv[NS];
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
         const int s = lane + j * kWave;
         xv[j] = s < nslots ? __builtin_nontemporal_load(hs + s) : u32x4{0u, 0u, 0u, 0u};
     }
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-        const int s = lane + j * kWave;
-        gv[j] = s < nslots ? gs[s] : u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int s = threadIdx.x; s < nslots; s += kThreads) gl[s] = gs[s];
+    __syncthreads();
+    if (!live) return;
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
@@ -242,16 +243,28 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fp8_wave_kernel(
         for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
     }
     ss = kc::wave_sum(ss);
+    // Register fence: without it the compiler keeps the 8 * NS unpacked
+    // values of the sum above alive across the reduction for the
+    // normalization below (and the unpacked y across the next one), which
+    // took this kernel to 251 VGPRs and 2 waves per SIMD; unpacking again
+    // costs one instruction per value (154 VGPRs, 3 waves: 78.4 -> 75.4 us on
+    // 16384 x 8192, with gamma from LDS).
+#pragma unroll
+    for (int j = 0; j < NS; ++j) asm volatile("" : "+v"(xv[j]) :: "memory");
     const float rms_inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
     float m = 0.0f;
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-        // Slots past the row hold h = gamma = 0 and give y = 0: no effect on
-        // the absmax, and they are not stored.
-        xv[j] = norm_slot(xv[j], gv[j], rms_inv);
+        // Slots past the row hold h = 0 and give y = 0: no effect on the
+        // absmax, and they are not stored.
+        const int s = lane + j * kWave;
+        const u32x4 g = s < nslots ? gl[s] : u32x4{0u, 0u, 0u, 0u};
+        xv[j] = norm_slot(xv[j], g, rms_inv);
         m = absmax_bf16x8(m, xv[j]);
     }
     const RowDiv d = row_div(kc::wave_max(m));
+#pragma unroll
+    for (int j = 0; j < NS; ++j) asm volatile("" : "+v"(xv[j]));
     if (lane == 0) scales[row] = d.s;
     u32x2* dst = reinterpret_cast<u32x2*>(out + row * D);
     auto emit = [&](auto fast) {
