@@ -224,10 +224,12 @@ int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
  *   kc_gemm_int4_bf16_shuffled: kc_gemm_int4_bf16 on the shuffled weights.
  *     For m >= 2 the same kernels, reading 1 KB of the layout per wave-wide
  *     load instead of 64 bytes of each of 16 rows: bit-identical results.
- *     m == 1 runs a matrix-core GEMV (cols = 1024 * KW, KW <= 16; other cols
- *     take the m >= 2 kernel), within the bf16 tolerance of the reference
- *     GEMV.  Needs cols % 128 == 0, group_size a power of two >= 128, 16-byte
- *     aligned weights and x. */
+ *     m == 1 runs a matrix-core GEMV when cols = 1024 * KW (KW <= 16), or
+ *     cols = 512 * KW (KW <= 16) with rows <= 8192 (four k-blocks per wave);
+ *     other cols take the m >= 2 kernel.  Within the bf16 tolerance of the
+ *     reference GEMV.  Needs cols % 128 == 0, group_size a power of two
+ *     >= 128, 16-byte aligned weights and x; cols == 0 writes Y = 0 and
+ *     reads no weights. */
 int64_t kc_shuffled_int4_bytes(int64_t rows, int64_t cols);
 int kc_shuffle_int4_mfma(const uint8_t* d_packed, uint8_t* d_packed_shuffled,
                          int rows, int cols, kc_stream_t stream);

@@ -1397,6 +1397,17 @@ int gemm_int4(const char* fn, const uint8_t* d_packed, const float* d_scales,
                       kc::is_pow2(group_size) && kc::aligned(d_packed, 16) &&
                       kc::aligned(d_x, 16);
     if constexpr (SHUF) {
+        // K = 0: Y = 0, as on the reference layout (the per-row GEMV below
+        // writes zeros and reads no weights)
+        if (cols == 0) {
+            for (int i = 0; i < m; ++i) {
+                const int st = kc_gemv_int4_bf16(d_packed, d_scales, d_zeros, d_x,
+                                                 d_y + static_cast<int64_t>(i) * rows, rows, 0,
+                                                 group_size, stream);
+                if (st != KC_SUCCESS) return st;
+            }
+            return KC_SUCCESS;
+        }
         // only the matrix-core kernels read the shuffled layout
         if (!fast)
             return kc::set_error(KC_ERR_INVALID_ARGUMENT,

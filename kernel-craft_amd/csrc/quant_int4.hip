@@ -358,12 +358,32 @@ __device__ __forceinline__ void x_dma16(const void* g, uint32_t lds_base) {
                  : "memory", "m0");
 }
 
+// s_waitcnt vmcnt(n) for n in [0, 7] (a constant once the caller's loop is
+// unrolled).  The wait reads and writes `after` (a value the caller computes
+// just before, e.g. the previous row's sum), so it is not hoisted above that
+// work; an empty asm then reads and writes v, so v counts as produced after
+// the wait and nothing reads its register before it.
+__device__ __forceinline__ void wait_vmcnt_tied(int n, u32x4& v, float& after) {
+    switch (n) {
+        case 0: asm volatile("s_waitcnt vmcnt(0)" : "+v"(after)::"memory"); break;
+        case 1: asm volatile("s_waitcnt vmcnt(1)" : "+v"(after)::"memory"); break;
+        case 2: asm volatile("s_waitcnt vmcnt(2)" : "+v"(after)::"memory"); break;
+        case 3: asm volatile("s_waitcnt vmcnt(3)" : "+v"(after)::"memory"); break;
+        case 4: asm volatile("s_waitcnt vmcnt(4)" : "+v"(after)::"memory"); break;
+        case 5: asm volatile("s_waitcnt vmcnt(5)" : "+v"(after)::"memory"); break;
+        case 6: asm volatile("s_waitcnt vmcnt(6)" : "+v"(after)::"memory"); break;
+        default: asm volatile("s_waitcnt vmcnt(7)" : "+v"(after)::"memory"); break;
+    }
+    asm volatile("" : "+v"(v));
+}
+
 template <int R, int KW, int RGW, bool NORM, bool BF16 = true>
 __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
     const uint8_t* __restrict__ packed, const float* __restrict__ scales,
     const uint8_t* __restrict__ zeros, const void* __restrict__ x, void* __restrict__ y,
     int rows, int cols, int gshift, const uint16_t* __restrict__ gamma, float eps) {
     static_assert(R % 4 == 0, "rows are reduced across the wave four at a time");
+    static_assert(R <= 8, "weight-load waits count up to 7 younger loads");
     static_assert(BF16 || !NORM, "the fused RMSNorm takes bf16 x");
     constexpr int kXQ = BF16 ? 4 : 8;  // 16-byte quads of x per 32-k chunk
     __shared__ float part[RGW][KW][R + 1];  // row sums, then the sum of h^2
@@ -384,17 +404,11 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
     // LDS slot (t, l), t = kw' kXQ + j, holds quad j of chunk 64 kw' + l, so
     // that a wave's reads of quad j are 64 consecutive slots.
     constexpr bool kShare = !NORM && RGW > 1;
+    static_assert(!kShare || (KW * kXQ) % (KW * RGW) == 0, "x copies split evenly over the waves");
     __shared__ u32x4 xsh[kShare ? KW * kXQ * kWave : 1];
     u32x4 xq[kXQ], gq[NORM ? 4 : 1];
     const u32x4* xs = static_cast<const u32x4*>(x) + c * kXQ;
-    if constexpr (kShare) {
-        const uint32_t base = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_void_t*)xsh));
-        for (int t = wave; t < KW * kXQ; t += KW * RGW) {
-            const int kwp = t / kXQ, j = t - kwp * kXQ;
-            x_dma16(static_cast<const u32x4*>(x) + (kwp * kWave + lane) * kXQ + j,
-                    __builtin_amdgcn_readfirstlane(base + t * kWave * 16));
-        }
-    } else {
+    if constexpr (!kShare) {
 #pragma unroll
         for (int q = 0; q < kXQ; ++q) xq[q] = xs[q];
     }
@@ -412,21 +426,41 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
         zb[r] = zeros[rr * (G >> 1) + (g >> 1)];
     }
     u32x4 w[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int64_t rr = min(row0 + r, rows - 1);
-        w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(packed + rr * rbytes) + c);
-    }
-    __builtin_amdgcn_sched_barrier(0);  // every load above issued before any use
     if constexpr (kShare) {
-        // The copies of x are complete once no more than the R scale, R zero
-        // and R weight loads issued after them are outstanding (vector loads
-        // complete in order); the barrier then publishes every wave's part,
-        // while the weights stay in flight.
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * R) : "memory");
+        // x is copied into LDS with direct-to-LDS loads, then the R weight
+        // loads follow; both are written out as instructions here, so that
+        // exactly R vector loads are issued after the last copy.  Vector
+        // loads complete in order: once no more than R are outstanding, every
+        // copy has landed, whatever the compiler emits elsewhere (a load it
+        // added in between would only make the wait stricter).  The barrier
+        // then publishes every wave's part while the weights stay in flight.
+        const uint32_t base = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_void_t*)xsh));
+#pragma unroll
+        for (int t0 = 0; t0 < KW * kXQ; t0 += KW * RGW) {
+            const int t = t0 + wave;
+            const int kwp = t / kXQ, j = t - kwp * kXQ;
+            x_dma16(static_cast<const u32x4*>(x) + (kwp * kWave + lane) * kXQ + j,
+                    __builtin_amdgcn_readfirstlane(base + t * kWave * 16));
+        }
+        const uint32_t voff = static_cast<uint32_t>(c) * 16u;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int64_t rr = min(row0 + r, rows - 1);
+            const uint8_t* prow = packed + rr * rbytes;
+            asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(w[r]) : "v"(voff), "s"(prow)
+                         : "memory");
+        }
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(R) : "memory");
         __builtin_amdgcn_s_barrier();
 #pragma unroll
         for (int q = 0; q < kXQ; ++q) xq[q] = xsh[(kw * kXQ + q) * kWave + lane];
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int64_t rr = min(row0 + r, rows - 1);
+            w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(packed + rr * rbytes) + c);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every load above issued before any use
     }
 
     uint32_t sel_lo, sel_hi;  // v_perm_b32 selectors, in VGPRs
@@ -471,6 +505,11 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
+        // weights loaded by explicit instructions are not tracked by the
+        // compiler's waits: wait until row r's load has landed (at most
+        // R - 1 - r younger loads outstanding) and tie w[r] to that wait, so
+        // that no use of it can be placed before
+        if constexpr (kShare) wait_vmcnt_tied(R - 1 - r, w[r], r == 0 ? xsm : acc[r > 0 ? r - 1 : 0]);
         const uint32_t z = (g & 1) ? (zb[r] >> 4) : (zb[r] & 0xFu);
         const float dot = BF16 ? chunk_dot<true>(w[r], xp, nk) : chunk_dot<false>(w[r], xq, nk);
         acc[r] = fmaf(sv[r], dot, -sv[r] * (kOff + static_cast<float>(z)) * xsm);

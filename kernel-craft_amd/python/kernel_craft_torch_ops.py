@@ -421,9 +421,17 @@ def int4_gemv_bf16_chain(ops) -> None:
     of (packed, scales, zeros, x, y, rows, cols, group_size) with bf16 x and y
     already allocated and contiguous (the op writes into y, so a copy would
     lose the result); an op's x may be an earlier op's y or a contiguous
-    slice of it."""
+    slice of it.
+
+    Weights that are not contiguous are copied first; every copy is held in
+    ``keep`` until the library call has returned, so no op points at memory
+    the caching allocator has handed to a later copy.  The kernels run
+    asynchronously on the current stream, which orders the copies' eventual
+    reuse after them.  A caller that captures this call in a HIP graph must
+    pass contiguous weights: the graph keeps the pointers, not the copies."""
     import torch
     arr = (GemvOp * max(1, len(ops)))()
+    keep = []
     for i, (packed, scales, zeros, x, y, rows, cols, gs) in enumerate(ops):
         name = f"int4_gemv_bf16_chain op {i}"
         if not (x.is_contiguous() and y.is_contiguous()):
@@ -432,12 +440,14 @@ def int4_gemv_bf16_chain(ops) -> None:
         _arg(f"{name}: x", x, torch.bfloat16, cols)
         _arg(f"{name}: y", y, torch.bfloat16, rows)
         _on_gpu(name, packed, scales, zeros, x, y)
+        keep.append((packed, scales, zeros))
         arr[i] = GemvOp(_ptr(packed), _ptr(scales), _ptr(zeros), _ptr(x), _ptr(y), rows, cols,
                         gs, 0)
     with kernel_span("int4_gemv_bf16_chain", ops=len(ops)):
         st = _get_lib().kc_gemv_int4_bf16_chain(ctypes.cast(arr, ctypes.c_void_p), len(ops),
                                                 _stream())
     _check("int4_gemv_bf16_chain", st)
+    del keep
 
 
 def int4_gemm_bf16(packed, scales, zeros, x, rows: int, cols: int, group_size: int = 128):
@@ -649,7 +659,9 @@ def rmsnorm_fp8_quantize(h, gamma, eps: float = 1e-6) -> Tuple:
     gamma = _arg("rmsnorm_fp8_quantize: gamma", gamma, torch.bfloat16, D)
     _on_gpu("rmsnorm_fp8_quantize", h, gamma)
     q = torch.empty(T, D, dtype=torch.int8, device=h.device)
-    s = torch.empty(T, dtype=torch.float32, device=h.device)
+    # an empty row has absmax 0, hence scale 1; the library writes nothing
+    # when D == 0 (as the reference launcher, whose launch has no threads)
+    s = (torch.ones if D == 0 else torch.empty)(T, dtype=torch.float32, device=h.device)
     with kernel_span("rmsnorm_fp8_quantize", rows=T, cols=D):
         st = _get_lib().kc_rmsnorm_quantize_fp8_bf16(_ptr(h), _ptr(gamma), eps, _ptr(q), _ptr(s),
                                                      T, D, _stream())
@@ -665,7 +677,8 @@ def fp8_quantize_rows(x) -> Tuple:
     _on_gpu("fp8_quantize_rows", x)
     rows, cols = x.shape
     q = torch.empty(rows, cols, dtype=torch.int8, device=x.device)
-    s = torch.empty(rows, dtype=torch.float32, device=x.device)
+    # scale 1 for empty rows (absmax 0), which the library does not write
+    s = (torch.ones if cols == 0 else torch.empty)(rows, dtype=torch.float32, device=x.device)
     lib = _get_lib()
     fn = lib.kc_quantize_fp8_per_token_bf16 if x.dtype == torch.bfloat16 \
         else lib.kc_quantize_fp8_per_token_f32

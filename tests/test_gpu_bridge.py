@@ -185,3 +185,35 @@ def test_bridge_shuffled_gemm(gpu, oracle, m, rows, cols):
         xbits = (x.float().cpu().numpy().view(np.uint32) >> 16).astype(np.uint16)
         truth = oracle.gemm_int4_bf16_f64(p, s, z.reshape(-1), xbits, 1, rows, cols, gs)
         assert rel_l2(y.float().cpu().numpy(), truth) < 3e-3
+
+
+def test_gemv_chain_non_contiguous_weights(gpu):
+    """int4_gemv_bf16_chain with weights that are column slices of wider
+    buffers (so the bridge copies them): three ops of one shape and different
+    weights, each output bit-identical to int4_gemv_bf16 on contiguous copies
+    of the same weights.  The copies must all outlive the library call: with
+    same-sized copies freed early, the caching allocator hands op 0's block
+    to op 1's copy and op 0 reads op 1's weights."""
+    torch = gpu
+    from kc_data import normal_bf16
+    rows, cols, gs = 1024, 4096, 128
+    G = cols // gs
+    ops_args, refs = [], []
+    for i in range(3):
+        p, s, z = make_int4(rows, cols, gs, seed=900 + i)
+        wide_p = torch.zeros(rows, cols // 2 + 64, dtype=torch.uint8, device="cuda")
+        wide_s = torch.zeros(rows, G + 3, dtype=torch.float32, device="cuda")
+        wide_z = torch.zeros(rows, z.shape[1] + 5, dtype=torch.uint8, device="cuda")
+        wide_p[:, 32:32 + cols // 2] = _d(torch, p)
+        wide_s[:, 1:1 + G] = _d(torch, s)
+        wide_z[:, 2:2 + z.shape[1]] = _d(torch, z)
+        vp, vs, vz = wide_p[:, 32:32 + cols // 2], wide_s[:, 1:1 + G], wide_z[:, 2:2 + z.shape[1]]
+        assert not (vp.is_contiguous() or vs.is_contiguous() or vz.is_contiguous())
+        x = _d(torch, normal_bf16((cols,), seed=950 + i).view(np.int16)).view(torch.bfloat16)
+        y = torch.empty(rows, dtype=torch.bfloat16, device="cuda")
+        ops_args.append((vp, vs, vz, x, y, rows, cols, gs))
+        refs.append(ops.int4_gemv_bf16(_d(torch, p), _d(torch, s), _d(torch, z), x, rows, cols, gs))
+    ops.int4_gemv_bf16_chain(ops_args)
+    torch.cuda.synchronize()
+    for i, (args, ref) in enumerate(zip(ops_args, refs)):
+        assert torch.equal(args[4].view(torch.int16), ref.view(torch.int16)), f"op {i}"

@@ -161,4 +161,13 @@ def test_shuffle_empty_shapes(gpu):
     assert L.kc_shuffle_int4_mfma(None, None, 0, 128, stream()) == 0
     assert L.kc_shuffle_int4_mfma(None, None, 16, 0, stream()) == 0
     assert L.kc_shuffled_int4_bytes(0, 128) == 0
+    # K = 0: Y = 0 on both layouts, success, no weights read (null pointers)
+    for m in (1, 3, 17):
+        y0 = torch.full((m, 48), 7.0, dtype=torch.bfloat16, device="cuda")
+        y1 = y0.clone()
+        assert L.kc_gemm_int4_bf16(None, None, None, None, ptr(y0), m, 48, 0, 128, stream()) == 0
+        assert L.kc_gemm_int4_bf16_shuffled(None, None, None, None, ptr(y1), m, 48, 0, 128,
+                                            stream()) == 0
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(y0).item() == 0 and torch.count_nonzero(y1).item() == 0
     torch.cuda.synchronize()
