@@ -419,21 +419,17 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
     }
     float sv[R];
     uint32_t zb[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int64_t rr = min(row0 + r, rows - 1);
-        sv[r] = scales[rr * G + g];
-        zb[r] = zeros[rr * (G >> 1) + (g >> 1)];
-    }
     u32x4 w[R];
     if constexpr (kShare) {
-        // x is copied into LDS with direct-to-LDS loads, then the R weight
-        // loads follow; both are written out as instructions here, so that
-        // exactly R vector loads are issued after the last copy.  Vector
-        // loads complete in order: once no more than R are outstanding, every
-        // copy has landed, whatever the compiler emits elsewhere (a load it
-        // added in between would only make the wait stricter).  The barrier
-        // then publishes every wave's part while the weights stay in flight.
+        // x is copied into LDS with direct-to-LDS loads, then come the R
+        // scale, R zero-byte and R weight loads of this wave's rows; all are
+        // written out as instructions here, so that exactly 3R vector loads
+        // are issued after the last copy.  Vector loads complete in order:
+        // once no more than 3R are outstanding, every copy has landed,
+        // whatever the compiler emits elsewhere (a load it added in between
+        // would only make the wait stricter).  The barrier then publishes
+        // every wave's part while the rest stays in flight; the values these
+        // loads produce are tied to explicit waits before their first use.
         const uint32_t base = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_void_t*)xsh));
 #pragma unroll
         for (int t0 = 0; t0 < KW * kXQ; t0 += KW * RGW) {
@@ -441,6 +437,17 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
             const int kwp = t / kXQ, j = t - kwp * kXQ;
             x_dma16(static_cast<const u32x4*>(x) + (kwp * kWave + lane) * kXQ + j,
                     __builtin_amdgcn_readfirstlane(base + t * kWave * 16));
+        }
+        const uint32_t soff = static_cast<uint32_t>(g) * 4u, zoff = static_cast<uint32_t>(g >> 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int64_t rr = min(row0 + r, rows - 1);
+            const float* srow = scales + rr * G;
+            const uint8_t* zrow = zeros + rr * (G >> 1);
+            asm volatile("global_load_dword %0, %1, %2" : "=v"(sv[r]) : "v"(soff), "s"(srow)
+                         : "memory");
+            asm volatile("global_load_ubyte %0, %1, %2" : "=v"(zb[r]) : "v"(zoff), "s"(zrow)
+                         : "memory");
         }
         const uint32_t voff = static_cast<uint32_t>(c) * 16u;
 #pragma unroll
@@ -450,11 +457,17 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
             asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(w[r]) : "v"(voff), "s"(prow)
                          : "memory");
         }
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(R) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * R) : "memory");
         __builtin_amdgcn_s_barrier();
 #pragma unroll
         for (int q = 0; q < kXQ; ++q) xq[q] = xsh[(kw * kXQ + q) * kWave + lane];
     } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int64_t rr = min(row0 + r, rows - 1);
+            sv[r] = scales[rr * G + g];
+            zb[r] = zeros[rr * (G >> 1) + (g >> 1)];
+        }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int64_t rr = min(row0 + r, rows - 1);
@@ -509,7 +522,13 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
         // compiler's waits: wait until row r's load has landed (at most
         // R - 1 - r younger loads outstanding) and tie w[r] to that wait, so
         // that no use of it can be placed before
-        if constexpr (kShare) wait_vmcnt_tied(R - 1 - r, w[r], r == 0 ? xsm : acc[r > 0 ? r - 1 : 0]);
+        if constexpr (kShare) {
+            wait_vmcnt_tied(R - 1 - r, w[r], r == 0 ? xsm : acc[r > 0 ? r - 1 : 0]);
+            if (r == 0) {  // every scale and zero byte is older than the first weight load
+#pragma unroll
+                for (int q = 0; q < R; ++q) asm volatile("" : "+v"(sv[q]), "+v"(zb[q]));
+            }
+        }
         const uint32_t z = (g & 1) ? (zb[r] >> 4) : (zb[r] & 0xFu);
         const float dot = BF16 ? chunk_dot<true>(w[r], xp, nk) : chunk_dot<false>(w[r], xq, nk);
         acc[r] = fmaf(sv[r], dot, -sv[r] * (kOff + static_cast<float>(z)) * xsm);
