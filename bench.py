@@ -9,14 +9,18 @@ N 6144), O (4096, 4096), fused gate/up (4096, 28672), down (14336, 4096).
 nibbles + x + y: 116 858 880 B) times steps over the wall-clock time of the
 timed steps, bracketed by torch.cuda.synchronize().  Inputs are resident in
 HBM and rotate over enough copies (> 1 GiB) that the 256 MB Infinity Cache
-cannot hold them.  A step is timed two ways -- one kc_gemv_int4_bf16_chain
-call (the four launches back to back from native code) and a HIP graph
-replay of the four launches -- and `value` is the faster; both are in
-`config.launch_modes_GBps`.
+cannot hold them.  The four GEMVs read independent inputs, and a step is one
+kc_gemv_int4_bf16_chain call, which runs them as ONE launch of the fused tile
+(gemv_run_kernel); the same call captured in a HIP graph, and the four
+kc_gemv_int4_bf16 launches back to back, are timed beside it, and `value` is
+the fastest of these (all in `config.launch_modes_GBps`).  The same chain
+with each GEMV reading the previous one's output (QKV -> O -> gate/up ->
+down, which the library runs launch by launch) is reported as
+`dependent_chain`.
 
-`roofline` is for the dominant kernel (the gate/up GEMV): its algorithmic
-bytes per launch over its average duration, timed with HIP events on the
-launch stream; `cpu_baseline` times the CPU oracle's scalar GEMV on the same
+`roofline` is for the dominant kernel, the fused launch of the whole layer:
+its algorithmic bytes per launch over its average duration, timed with HIP
+events on the launch stream; `cpu_baseline` times the CPU oracle's scalar GEMV on the same
 inputs on one host thread.  The other BASELINE configurations are reported
 beside it, each as algorithmic bytes over the average launch duration:
 `gemv_cfg0` (fp32 reference-ABI GEMV, 4096 x 4096), `gemm_cfg3` (MFMA
@@ -65,7 +69,7 @@ def fp8_bytes(rows: int, cols: int) -> int:
     return rows * cols * 4 + rows * cols + rows * 4
 
 
-GEMV_SOURCES = ("kernel-craft_amd/csrc/quant_int4.hip", "kernel-craft_amd/csrc/int4_decode.hpp",
+GEMV_SOURCES = ("kernel-craft_amd/csrc/gemv_chain.hip", "kernel-craft_amd/csrc/int4_decode.hpp",
                 "kernel-craft_amd/csrc/kc_common.hpp")
 
 
@@ -377,8 +381,9 @@ def main() -> int:
                     help="bound on the CPU-baseline sample (0 skips it)")
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of HIP graphs")
     ap.add_argument("--traffic-probe", action="store_true",
-                    help="for rocprofv3 --pmc: launch the gate/up GEMV and a plain 64 MiB "
-                         "device copy (the counter calibration) 20 times each, then exit")
+                    help="for rocprofv3 --pmc: launch the decode layer's fused run (one chain "
+                         "call) and a plain 64 MiB device copy (the counter calibration) 20 "
+                         "times each, then exit")
     ap.add_argument("--quant-probe", action="store_true",
                     help="for rocprofv3 --pmc: launch the cfg1 FP8 per-token quantizer 20 "
                          "times over rotating inputs and the 64 MiB copy 20 times, then exit")
@@ -512,17 +517,6 @@ def main() -> int:
         print("gemv probe done: cfg0 x 20, 20 x copy of 67108864 B", flush=True)
         return 0
 
-    if args.traffic_probe:
-        src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        for j in range(20):
-            launch_op(j, DOMINANT)
-        torch.cuda.synchronize()
-        for _ in range(20):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print("traffic probe done: 20 x gate/up GEMV, 20 x copy of 67108864 B", flush=True)
-        return 0
 
     # ---- parity guard: every shape against an fp32 reference --------------
     for i, (name, n, k) in enumerate(LLAMA):
@@ -539,24 +533,79 @@ def main() -> int:
             return 1
         log(f"# parity {name}: rel L2 {err:.2e}")
 
-    # ---- a step: the layer's four GEMVs from one native call ---------------
-    # (kc_gemv_int4_bf16_chain launches them back to back), and the same four
-    # launches replayed from a HIP graph; `value` is the faster of the two.
+    # ---- a step: the layer's four GEMVs from one chain call (one launch of the
+    # fused tile: the inputs are independent), the same call replayed from a
+    # HIP graph, and the four stand-alone launches; `value` is the fastest.
     import ctypes
-    chains = []
-    for r in range(copies):
-        arr = (ops.GemvOp * len(LLAMA))()
-        for i, (_, n, k) in enumerate(LLAMA):
-            p, s, z = layers[r][i]
-            arr[i] = ops.GemvOp(p.data_ptr(), s.data_ptr(), z.data_ptr(), xs[i].data_ptr(),
-                                ys[i].data_ptr(), n, k, GS, 0)
-        chains.append(arr)
 
-    def step_chain(j: int) -> None:
-        st = lib.kc_gemv_int4_bf16_chain(ctypes.cast(chains[j % copies], ctypes.c_void_p),
-                                         len(LLAMA), torch.cuda.current_stream().cuda_stream)
+    def chain_arrays(xs_, ys_):
+        arrs = []
+        for r in range(copies):
+            arr = (ops.GemvOp * len(LLAMA))()
+            for i, (_, n, k) in enumerate(LLAMA):
+                p, s, z = layers[r][i]
+                arr[i] = ops.GemvOp(p.data_ptr(), s.data_ptr(), z.data_ptr(), xs_[i].data_ptr(),
+                                    ys_[i].data_ptr(), n, k, GS, 0)
+            arrs.append(arr)
+        return arrs
+
+    chains = chain_arrays(xs, ys)
+    # the host work of a step is one foreign call with arguments prepared
+    # here (the op array's address, the stream handle), as a native caller's
+    # would be: with ~21 us of GPU work per step, per-step Python overhead
+    # (torch.cuda.current_stream() alone costs microseconds) would otherwise
+    # leave the GPU waiting for the host
+    chain_fn = lib.kc_gemv_int4_bf16_chain
+    n_ops = len(LLAMA)
+    main_stream = torch.cuda.current_stream().cuda_stream
+
+    def chain_ptrs(arrs):
+        return [ctypes.cast(a, ctypes.c_void_p) for a in arrs]
+
+    chain_p = chain_ptrs(chains)
+
+    def step_chain(j: int, arrs=chain_p, stream=None) -> None:
+        st = chain_fn(arrs[j % copies], n_ops, main_stream if stream is None else stream)
         if st:
             raise RuntimeError(f"kc_gemv_int4_bf16_chain failed: {lib.kc_last_error_string().decode()}")
+
+    per_op_args = [[(p.data_ptr(), s_.data_ptr(), z.data_ptr(), xs[i].data_ptr(), ys[i].data_ptr(),
+                     n, k, GS) for i, ((_, n, k), (p, s_, z)) in enumerate(zip(LLAMA, layers[r]))]
+                   for r in range(copies)]
+
+    def step_per_op(j: int) -> None:
+        for a in per_op_args[j % copies]:
+            if fn(*a, main_stream):
+                raise RuntimeError(f"kc_gemv_int4_bf16 failed: {lib.kc_last_error_string().decode()}")
+
+    if args.traffic_probe:
+        src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for j in range(20):
+            step_chain(j)
+        torch.cuda.synchronize()
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print("traffic probe done: 20 x the decode layer's fused run, 20 x copy of 67108864 B",
+              flush=True)
+        return 0
+
+    # parity of the fused run: every projection of the chain's output against
+    # its own stand-alone launch (the chain's tile repeats the per-lane-x
+    # GEMV; gate/up's stand-alone kernel sums in another order)
+    step_chain(0)
+    torch.cuda.synchronize()
+    fused_out = [y.clone() for y in ys]
+    for i, (name, n, k) in enumerate(LLAMA):
+        launch(0, i)
+        torch.cuda.synchronize()
+        err = ((fused_out[i].float() - ys[i].float()).norm() / ys[i].float().norm()).item()
+        if not err < 3e-3:
+            print(f"bench.py: fused run differs from the stand-alone GEMV for {name}: rel L2 "
+                  f"{err:.3e}", file=sys.stderr)
+            return 1
+        log(f"# fused run {name}: rel L2 {err:.2e} against the stand-alone launch")
 
     graphs = None
     if not args.no_graph:
@@ -568,8 +617,7 @@ def main() -> int:
                 for r in range(copies):
                     gph = torch.cuda.CUDAGraph()
                     with torch.cuda.graph(gph, stream=side):
-                        for i in range(len(LLAMA)):
-                            launch(r, i)
+                        step_chain(r, stream=side.cuda_stream)
                     graphs.append(gph)
             torch.cuda.current_stream().wait_stream(side)
         except Exception as e:  # pragma: no cover - depends on the runtime
@@ -590,7 +638,7 @@ def main() -> int:
         torch.cuda.synchronize()
         return time.perf_counter() - t0
 
-    modes = {"native_chain": timed(step_chain)}
+    modes = {"one_launch_chain": timed(step_chain), "per_op_launches": timed(step_per_op)}
     if graphs is not None:
         modes["hip_graph"] = timed(step_graph)
     for m, t in modes.items():
@@ -600,6 +648,34 @@ def main() -> int:
     elapsed = modes[launch_mode]
     value = layer_bytes * args.steps / elapsed / 1e9
     modes_gbs = {m: round(layer_bytes * args.steps / t / 1e9, 1) for m, t in modes.items()}
+
+    # the decode layer wired as in a decoder: each GEMV reads the previous
+    # one's output (O's x from QKV's y, gate/up's from O's, down's from
+    # gate/up's), which the chain runs launch by launch
+    ys_dep = [torch.empty(n, dtype=torch.bfloat16, device=dev) for _, n, _ in LLAMA]
+    xs_dep = [xs[0]] + [ys_dep[i - 1][:k] for i, (_, _, k) in enumerate(LLAMA) if i > 0]
+    chains_dep = chain_arrays(xs_dep, ys_dep)
+    chain_dep_p = chain_ptrs(chains_dep)
+    t_dep = timed(lambda j: step_chain(j, chain_dep_p))
+    dependent = {"GBps": round(layer_bytes * args.steps / t_dep / 1e9, 1),
+                 "us_per_step": round(t_dep * 1e6 / args.steps, 3),
+                 "config": "QKV -> O -> gate/up -> down, each x a slice of the previous y; "
+                           "kc_gemv_int4_bf16_chain runs dependent ops launch by launch"}
+    log(f"# dependent chain: {dependent['us_per_step']} us/step, {dependent['GBps']} GB/s")
+
+    # ---- the fused launch timed alone (events, backlogged, rotating copies)
+    reps = 100
+    enqueue_backlog(torch)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for j in range(reps):
+        step_chain(j)
+    e1.record()
+    torch.cuda.synchronize()
+    run_us = e0.elapsed_time(e1) * 1e3 / reps
+    log(f"# fused run (gemv_run_kernel, the layer in one launch): {run_us:.2f} us/launch, "
+        f"{layer_bytes / run_us / 1e3:.1f} GB/s")
 
     # ---- per-kernel durations with HIP events (launch stream, backlogged) ---
     reps = 100
@@ -659,15 +735,13 @@ def main() -> int:
                           "(kc_shuffle_int4_mfma, kc_gemm_int4_bf16_shuffled), one launch each, "
                           "events as kernel_us"}
 
-    dom_name, dom_n, dom_k = LLAMA[DOMINANT]
-    dom_bytes = gemv_bytes(dom_n, dom_k)
-    achieved = dom_bytes / (kernel_us[dom_name] * 1e-6) / 1e9
-    traffic, traffic_note = read_traffic(ROOT / "profiles" / "gemv_int4_bf16_gate_up_traffic.md")
+    achieved = layer_bytes / (run_us * 1e-6) / 1e9
+    traffic, traffic_note = read_traffic(ROOT / "profiles" / "gemv_run_decode_layer_traffic.md")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                 "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
                 "traffic_source": traffic_note,
-                "kernel": f"gemv_int4_fast_kernel bf16 gate/up N={dom_n} K={dom_k}",
-                "bytes_per_launch": dom_bytes, "avg_us": round(kernel_us[dom_name], 3)}
+                "kernel": "gemv_run_kernel: the decode layer's four GEMVs in one launch",
+                "bytes_per_launch": layer_bytes, "avg_us": round(run_us, 3)}
 
     def stream_ptr() -> int:
         return torch.cuda.current_stream().cuda_stream
@@ -991,6 +1065,7 @@ def main() -> int:
                    "per_kernel_rotation_copies": {nm: len(pools[i])
                                                   for i, (nm, _, _) in enumerate(LLAMA)},
                    "launch": launch_mode, "launch_modes_GBps": modes_gbs},
+        "dependent_chain": dependent,
         "pct_of_peak": round(100.0 * value / PEAK_HBM_GBS, 2),
         "roofline": roofline,
         "kernel_us": {k: round(v, 3) for k, v in kernel_us.items()},

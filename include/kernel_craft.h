@@ -121,10 +121,14 @@ int kc_gemv_int4_bf16(const uint8_t* d_packed, const float* d_scales,
 
 /* A decode step's INT4 GEMVs from one call (no counterpart in the
  * reference, whose decode loop calls launch_gemv_int4 once per projection,
- * quant_int4.cu:221-234).  Each op is one kc_gemv_int4_bf16; the ops are
- * launched back to back on the stream, so an op may read what earlier ops
- * wrote (its x may be an earlier op's y).  Every op is validated before the
- * first launch. */
+ * quant_int4.cu:221-234).  Each op computes what kc_gemv_int4_bf16 computes,
+ * in list order, so an op may read what earlier ops wrote (its x may be an
+ * earlier op's y).  The list is cut into runs at dependencies (an op that
+ * reads an earlier op's y, or writes what it reads or writes, starts a new
+ * run); a run of two or more ops with K = 2048 KW (KW 2..8), a power-of-two
+ * group of at least 32 and 16-byte aligned weights and x is one launch,
+ * every other op its own kc_gemv_int4_bf16 launch.  Every op is validated
+ * before the first launch; ops with rows == 0 are skipped. */
 #define KC_GEMV_CHAIN_MAX_OPS 8
 typedef struct kc_gemv_op {
     const uint8_t* packed;
@@ -135,6 +139,7 @@ typedef struct kc_gemv_op {
     int rows, cols, group_size, reserved;
 } kc_gemv_op;
 int kc_gemv_int4_bf16_chain(const kc_gemv_op* ops, int n_ops, kc_stream_t stream);
+
 
 /* RMSNorm with bf16 input, weight and output (fp32 arithmetic, output
  * rounded to nearest even): the bf16 counterpart of launch_rmsnorm,

@@ -408,3 +408,143 @@ def test_chain_argument_errors(gpu):
     assert L.kc_gemv_int4_bf16_chain(ctypes.cast(arr, ctypes.c_void_p), 1, stream()) == 1  # nulls
     assert L.kc_gemv_int4_bf16_chain(None, 0, stream()) == 0
     L.kc_get_last_error()
+
+
+# ---------------------------------------------------------------------------
+# Runs of independent ops: one launch of the fused tile
+# ---------------------------------------------------------------------------
+
+def _fused_tile_takes(rows, cols, gs):
+    return cols % 2048 == 0 and 2 <= cols // 2048 <= 8 and gs >= 32 and gs & (gs - 1) == 0
+
+
+def _same_as_standalone(rows, cols, gs):
+    """kc_gemv_int4_bf16 takes the per-lane-x kernel, whose per-row
+    arithmetic the fused tile repeats: the outputs are equal bit for bit
+    (at K = 4096 with N > 16384 it takes the LDS-staged kernel, which sums
+    in another order)."""
+    return _fused_tile_takes(rows, cols, gs) and not (cols == 4096 and rows > 16384)
+
+
+def _check_run(torch, oracle, specs, results, tol=3e-3):
+    _check_chain(oracle, specs, results, tol)
+    for (rows, cols, gs), ((packed, scales, zeros), xb, y) in zip(specs, results):
+        if _same_as_standalone(rows, cols, gs):
+            alone = _gemv_bf16(torch, packed, scales, zeros, xb, rows, cols, gs)
+            np.testing.assert_array_equal(y.view(np.uint32), alone.view(np.uint32),
+                                          err_msg=str((rows, cols, gs)))
+
+
+FUSED_RUNS = [
+    # the decode layer with independent inputs (the bench's step): one launch
+    [(6144, 4096, 128), (4096, 4096, 128), (28672, 4096, 128), (4096, 14336, 128)],
+    # every KW, ragged row counts (tiles of 16, 8, 8, 4, 4, 4, 4 rows)
+    [(100, 4096, 128), (37, 6144, 64), (1000, 8192, 32), (5, 10240, 256), (333, 12288, 128),
+     (17, 14336, 128), (64, 16384, 512)],
+    # group sizes 32 .. 2048 at K = 4096, and single rows
+    [(17, 4096, 32), (33, 4096, 64), (65, 4096, 2048), (1, 4096, 128), (1, 14336, 128)],
+    # the fused tile next to ops it does not take (K = 2048, K not 2048 KW,
+    # K above 16384): those launch on their own, the neighbours keep theirs
+    [(100, 4096, 128), (50, 2048, 128), (60, 8192, 128), (70, 8192 + 2048, 128),
+     (40, 5120, 128), (30, 18432, 128), (20, 4096, 128), (10, 6144, 128)],
+]
+
+
+@pytest.mark.parametrize("specs", FUSED_RUNS, ids=["decode_layer", "every_kw", "group_sizes", "mixed"])
+def test_chain_fused_run(gpu, oracle, specs):
+    results = _run_chain(gpu, specs, [-1] * len(specs), seed=4000 + len(specs))
+    _check_run(gpu, oracle, specs, results)
+
+
+def test_chain_runs_cut_at_dependencies(gpu, oracle):
+    """A, B independent; C reads A's y; D independent of C (but after it):
+    the runs are [A, B] and [C, D].  Every op matches its stand-alone GEMV on
+    the x it read."""
+    specs = [(4096, 4096, 128), (300, 8192, 128), (500, 4096, 128), (200, 14336, 128)]
+    _check_run(gpu, oracle, specs, _run_chain(gpu, specs, [-1, -1, 0, -1], seed=4100))
+
+
+def test_chain_write_after_read_is_ordered(gpu, oracle):
+    """Op B overwrites the buffer op A reads its x from: B must run after A
+    (another run), so A sees the original x."""
+    import kernel_craft_torch_ops as ops
+    torch = gpu
+    buf = _dev_bf16(torch, normal_bf16(8192, seed=4200))
+    x_orig = _host_bf16_bits(buf[:4096].clone())
+    pa, sa, za = make_int4(256, 4096, 128, seed=4201)
+    pb, sb, zb = make_int4(8192, 4096, 128, seed=4202)
+    xb_bits = normal_bf16(4096, seed=4203)
+    ya = torch.empty(256, dtype=torch.bfloat16, device="cuda")
+    chain = [(_dev(torch, pa), _dev(torch, sa), _dev(torch, za), buf[:4096], ya, 256, 4096, 128),
+             (_dev(torch, pb), _dev(torch, sb), _dev(torch, zb), _dev_bf16(torch, xb_bits), buf,
+              8192, 4096, 128)]
+    print("chain write-after-read", flush=True)
+    ops.int4_gemv_bf16_chain(chain)
+    torch.cuda.synchronize()
+    got_a = bf16_bits_to_f32(_host_bf16_bits(ya))
+    np.testing.assert_array_equal(got_a.view(np.uint32),
+                                  _gemv_bf16(torch, pa, sa, za, x_orig, 256, 4096, 128).view(np.uint32))
+    got_b = bf16_bits_to_f32(_host_bf16_bits(buf))
+    np.testing.assert_array_equal(got_b.view(np.uint32),
+                                  _gemv_bf16(torch, pb, sb, zb, xb_bits, 8192, 4096, 128).view(np.uint32))
+
+
+def test_chain_zero_row_ops_inside_a_run(gpu, oracle):
+    """Ops with rows == 0 are skipped; the ops around them still form one run."""
+    import kernel_craft_torch_ops as ops
+    torch = gpu
+    specs = [(64, 4096, 128), (0, 4096, 128), (48, 8192, 128), (0, 14336, 128), (32, 14336, 128)]
+    chain, host = [], []
+    for i, (rows, cols, gs) in enumerate(specs):
+        p, s, z = make_int4(max(rows, 1), cols, gs, seed=4300 + i)
+        xbits = normal_bf16(cols, seed=4310 + i)
+        y = torch.full((max(rows, 1),), 7.0, dtype=torch.bfloat16, device="cuda")
+        chain.append((_dev(torch, p), _dev(torch, s), _dev(torch, z), _dev_bf16(torch, xbits), y,
+                      rows, cols, gs))
+        host.append((p, s, z, xbits))
+    print("chain with zero-row ops", flush=True)
+    ops.int4_gemv_bf16_chain(chain)
+    torch.cuda.synchronize()
+    for (rows, cols, gs), (p, s, z, xbits), d in zip(specs, host, chain):
+        got = bf16_bits_to_f32(_host_bf16_bits(d[4]))
+        if rows == 0:
+            assert np.all(got == 7.0), "an op with no rows writes nothing"
+            continue
+        np.testing.assert_array_equal(got.view(np.uint32),
+                                      _gemv_bf16(torch, p, s, z, xbits, rows, cols, gs).view(np.uint32))
+
+
+def test_chain_fused_run_graph_replays(gpu, oracle):
+    """A fused run (the decode layer with independent inputs) captured in a
+    HIP graph: every replay equals the eager call bit for bit, with eager
+    work on the same buffers between replays."""
+    import kernel_craft_torch_ops as ops
+    torch = gpu
+    specs = FUSED_RUNS[0]
+    chain = []
+    for i, (rows, cols, gs) in enumerate(specs):
+        p, s, z = make_int4(rows, cols, gs, seed=4400 + i)
+        chain.append((_dev(torch, p), _dev(torch, s), _dev(torch, z),
+                      _dev_bf16(torch, normal_bf16(cols, seed=4410 + i)),
+                      torch.empty(rows, dtype=torch.bfloat16, device="cuda"), rows, cols, gs))
+    print("fused run: eager", flush=True)
+    ops.int4_gemv_bf16_chain(chain)
+    torch.cuda.synchronize()
+    eager = [d[4].clone() for d in chain]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    print("fused run: capture", flush=True)
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            ops.int4_gemv_bf16_chain(chain)
+    torch.cuda.current_stream().wait_stream(side)
+    for rep in range(3):
+        for d in chain:
+            d[4].fill_(3.0)
+        torch.cuda.synchronize()
+        print(f"fused run: replay {rep}", flush=True)
+        g.replay()
+        torch.cuda.synchronize()
+        for d, e in zip(chain, eager):
+            assert torch.equal(d[4].view(torch.int16), e.view(torch.int16)), rep
