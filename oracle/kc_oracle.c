@@ -37,6 +37,7 @@
 #include "kc_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define E4M3_MAX 448.0f /* fp8_quant.cu:31 */
@@ -241,6 +242,37 @@ void kco_gemm_int4_bf16_f64(const uint8_t* packed, const float* scales,
                 y[i * rows + r] += w * (double)kco_bf16_to_f32(x[i * cols + k]);
         }
     }
+}
+
+/* The same sums as kco_gemm_int4_bf16_f64, rows split over `threads` OpenMP
+ * threads: each output y[i][r] starts at 0.0 and adds w(r, k) * x(i, k) for
+ * k = 0, 1, ... in order, exactly as there (the loops are nested the other
+ * way round so that a row's dequantized weights are formed once and x is
+ * read contiguously). */
+void kco_gemm_int4_bf16_f64_mt(const uint8_t* packed, const float* scales,
+                               const uint8_t* zeros, const uint16_t* x, double* y,
+                               int64_t m, int64_t rows, int64_t cols, int64_t gs,
+                               int threads) {
+    double* xd = (double*)malloc((size_t)(m * cols) * sizeof(double));
+    if (!xd) return;
+    for (int64_t j = 0; j < m * cols; ++j) xd[j] = (double)kco_bf16_to_f32(x[j]);
+#pragma omp parallel num_threads(threads > 0 ? threads : 1)
+    {
+        double* wr = (double*)malloc((size_t)cols * sizeof(double));
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < rows; ++r) {
+            if (!wr) continue;
+            for (int64_t k = 0; k < cols; ++k) wr[k] = (double)wq(packed, scales, zeros, r, k, cols, gs);
+            for (int64_t i = 0; i < m; ++i) {
+                const double* xi = xd + i * cols;
+                double acc = 0.0;
+                for (int64_t k = 0; k < cols; ++k) acc += wr[k] * xi[k];
+                y[i * rows + r] = acc;
+            }
+        }
+        free(wr);
+    }
+    free(xd);
 }
 
 void kco_gemv_int4_bf16_f32(const uint8_t* packed, const float* scales,
@@ -514,6 +546,30 @@ void kco_gemv_int4_bf16_f32_mt(const uint8_t* packed, const float* scales,
         const int64_t r0 = rows * c / chunks, r1 = rows * (c + 1) / chunks;
         kco_gemv_int4_bf16_f32(packed + r0 * (cols / 2), scales + r0 * G,
                                zeros + r0 * (G / 2), x, y + r0, r1 - r0, cols, gs);
+    }
+}
+
+void kco_quantize_fp8_smooth_div_bf16_mt(const uint16_t* in, const float* s, int8_t* out,
+                                         float* scales, int64_t rows, int64_t cols,
+                                         int threads) {
+    const int64_t chunks = threads > 0 ? threads : 1;
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int64_t c = 0; c < chunks; ++c) {
+        const int64_t r0 = rows * c / chunks, r1 = rows * (c + 1) / chunks;
+        kco_quantize_fp8_smooth_div_bf16(in + r0 * cols, s, out + r0 * cols, scales + r0,
+                                         r1 - r0, cols);
+    }
+}
+
+void kco_quantize_fp8_smooth_mul_bf16_mt(const uint16_t* in, const float* s, int8_t* out,
+                                         float* scales, int64_t rows, int64_t cols,
+                                         int threads) {
+    const int64_t chunks = threads > 0 ? threads : 1;
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int64_t c = 0; c < chunks; ++c) {
+        const int64_t r0 = rows * c / chunks, r1 = rows * (c + 1) / chunks;
+        kco_quantize_fp8_smooth_mul_bf16(in + r0 * cols, s, out + r0 * cols, scales + r0,
+                                         r1 - r0, cols);
     }
 }
 

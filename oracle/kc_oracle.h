@@ -112,6 +112,20 @@ void kco_gemv_int4_bf16_f32_mt(const uint8_t* packed, const float* scales,
                                int64_t rows, int64_t cols, int64_t group_size, int threads);
 void kco_quantize_fp8_per_token_mt(const float* in, int8_t* out, float* scales,
                                    int64_t rows, int64_t cols, int threads);
+/* Row splits used by the full-size GPU parity tests: the same rows as
+ * kco_quantize_fp8_smooth_{div,mul}_bf16 and the same sums as
+ * kco_gemm_int4_bf16_f64 (each output's terms added in k order from 0.0),
+ * over `threads` OpenMP threads. */
+void kco_quantize_fp8_smooth_div_bf16_mt(const uint16_t* in, const float* s, int8_t* out,
+                                         float* scales, int64_t rows, int64_t cols,
+                                         int threads);
+void kco_quantize_fp8_smooth_mul_bf16_mt(const uint16_t* in, const float* s, int8_t* out,
+                                         float* scales, int64_t rows, int64_t cols,
+                                         int threads);
+void kco_gemm_int4_bf16_f64_mt(const uint8_t* packed, const float* scales,
+                               const uint8_t* zeros, const uint16_t* x, double* y,
+                               int64_t m, int64_t rows, int64_t cols, int64_t group_size,
+                               int threads);
 
 #ifdef __cplusplus
 }

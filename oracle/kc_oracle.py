@@ -50,6 +50,10 @@ _SIGS = {
     "kco_rmsnorm_bf16": ([_P, _P, _P, _I64, _I64, ctypes.c_float], None),
     "kco_gemv_int4_bf16_f32_mt": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, ctypes.c_int], None),
     "kco_quantize_fp8_per_token_mt": ([_P, _P, _P, _I64, _I64, ctypes.c_int], None),
+    "kco_quantize_fp8_smooth_div_bf16_mt": ([_P, _P, _P, _P, _I64, _I64, ctypes.c_int], None),
+    "kco_quantize_fp8_smooth_mul_bf16_mt": ([_P, _P, _P, _P, _I64, _I64, ctypes.c_int], None),
+    "kco_gemm_int4_bf16_f64_mt": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, ctypes.c_int],
+                                  None),
     "kco_rmsnorm_f32_lanes": ([_P, _P, _P, _I64, _I64, ctypes.c_float], None),
     "kco_rmsnorm_bf16_lanes": ([_P, _P, _P, _I64, _I64, ctypes.c_float, _P], None),
     "kco_rmsnorm_quantize_fp8_bf16": ([_P, _P, ctypes.c_float, _P, _P, _I64, _I64, _P, _P],
@@ -140,13 +144,15 @@ def gemv_int4_refkernel_f32(packed, scales, zeros, x, rows, cols, group_size):
     return y
 
 
-def gemm_int4_bf16_f64(packed, scales, zeros, x_bf16, m, rows, cols, group_size):
-    """Reference GEMV applied to each of the m bf16 activation rows -> [m, rows]."""
+def gemm_int4_bf16_f64(packed, scales, zeros, x_bf16, m, rows, cols, group_size, threads=1):
+    """Reference GEMV applied to each of the m bf16 activation rows -> [m, rows];
+    threads > 1 splits the rows over that many OpenMP threads (same sums)."""
     packed, scales, zeros = _c(packed, np.uint8), _c(scales, np.float32), _c(zeros, np.uint8)
     x_bf16 = _c(x_bf16, np.uint16)
     y = np.empty((m, rows), np.float64)
-    lib().kco_gemm_int4_bf16_f64(_p(packed), _p(scales), _p(zeros), _p(x_bf16),
-                                 _p(y), m, rows, cols, group_size)
+    fn = lib().kco_gemm_int4_bf16_f64_mt if threads > 1 else lib().kco_gemm_int4_bf16_f64
+    args = (_p(packed), _p(scales), _p(zeros), _p(x_bf16), _p(y), m, rows, cols, group_size)
+    fn(*args, int(threads)) if threads > 1 else fn(*args)
     return y
 
 
@@ -279,28 +285,36 @@ def smooth_factors(amax_x, amax_w):
     return s
 
 
-def quantize_fp8_smooth_div(x, s):
-    """x [rows, cols] fp32 or bf16 bits; returns (codes, scales) of (x / s)."""
+def quantize_fp8_smooth_div(x, s, threads=1):
+    """x [rows, cols] fp32 or bf16 bits; returns (codes, scales) of (x / s);
+    threads > 1 (bf16 x) splits the rows over that many OpenMP threads."""
     s = _c(s, np.float32)
+    mt = False
     if x.dtype == np.uint16:
         x = _c(x, np.uint16)
-        fn = lib().kco_quantize_fp8_smooth_div_bf16
+        mt = threads > 1
+        fn = lib().kco_quantize_fp8_smooth_div_bf16_mt if mt else lib().kco_quantize_fp8_smooth_div_bf16
     else:
         x = _c(x, np.float32)
         fn = lib().kco_quantize_fp8_smooth_div_f32
     rows, cols = x.shape
     q = np.empty((rows, cols), np.int8)
     sc = np.empty(rows, np.float32)
-    fn(_p(x), _p(s), _p(q), _p(sc), rows, cols)
+    args = (_p(x), _p(s), _p(q), _p(sc), rows, cols)
+    fn(*args, int(threads)) if mt else fn(*args)
     return q, sc
 
 
-def quantize_fp8_smooth_mul_bf16(w_bf16, s):
+def quantize_fp8_smooth_mul_bf16(w_bf16, s, threads=1):
     w_bf16, s = _c(w_bf16, np.uint16), _c(s, np.float32)
     rows, cols = w_bf16.shape
     q = np.empty((rows, cols), np.int8)
     sc = np.empty(rows, np.float32)
-    lib().kco_quantize_fp8_smooth_mul_bf16(_p(w_bf16), _p(s), _p(q), _p(sc), rows, cols)
+    args = (_p(w_bf16), _p(s), _p(q), _p(sc), rows, cols)
+    if threads > 1:
+        lib().kco_quantize_fp8_smooth_mul_bf16_mt(*args, int(threads))
+    else:
+        lib().kco_quantize_fp8_smooth_mul_bf16(*args)
     return q, sc
 
 

@@ -717,6 +717,40 @@ def test_multithreaded_baselines_equal_scalar(oracle):
         np.testing.assert_array_equal(sc, s1)
 
 
+def test_multithreaded_full_size_oracles_equal_scalar(oracle):
+    """The row splits the full-size GPU tests use (cfg4's SmoothQuant
+    quantizers, cfg3's per-row GEMM) give the single-thread functions' bits:
+    every row, with rows not divisible by the thread count, more threads than
+    rows, special values (zero rows, NaN, infinity, huge and tiny values) and
+    every M of the GEMM's tiles."""
+    rng = np.random.default_rng(61)
+    for rows, cols in ((37, 1024), (5, 256), (300, 2048)):
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        x[:, rng.choice(cols, 4, replace=False)] *= 100.0
+        x[1] = 0.0
+        x[2, 3] = np.nan
+        x[3, 7] = np.inf
+        x[4, :5] = [3e38, -3e38, 1e-38, -1e-40, 6e-8]
+        xb = f32_to_bf16_bits(x)
+        sm = rng.uniform(0.05, 20.0, cols).astype(np.float32)
+        qd1, sd1 = oracle.quantize_fp8_smooth_div(xb, sm)
+        qm1, sm1 = oracle.quantize_fp8_smooth_mul_bf16(xb, sm)
+        for t in (2, 3, 8, 64):
+            qd, sd = oracle.quantize_fp8_smooth_div(xb, sm, threads=t)
+            qm, smm = oracle.quantize_fp8_smooth_mul_bf16(xb, sm, threads=t)
+            np.testing.assert_array_equal(qd, qd1)
+            np.testing.assert_array_equal(sd.view(np.uint32), sd1.view(np.uint32))
+            np.testing.assert_array_equal(qm, qm1)
+            np.testing.assert_array_equal(smm.view(np.uint32), sm1.view(np.uint32))
+    for m, rows, cols, gs in ((1, 37, 256, 128), (5, 100, 512, 64), (17, 33, 1024, 128)):
+        p, s, z = make_int4(rows, cols, gs, seed=62 + m)
+        xb = normal_bf16((m, cols), seed=63 + m)
+        y1 = oracle.gemm_int4_bf16_f64(p, s, z.reshape(-1), xb, m, rows, cols, gs)
+        for t in (2, 5, 64):
+            y = oracle.gemm_int4_bf16_f64(p, s, z.reshape(-1), xb, m, rows, cols, gs, threads=t)
+            np.testing.assert_array_equal(y.view(np.uint64), y1.view(np.uint64))
+
+
 # ---------------------------------------------------------------------------
 # The shuffled INT4 layout (kco_shuffle_int4_mfma)
 # ---------------------------------------------------------------------------
