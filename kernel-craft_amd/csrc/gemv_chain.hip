@@ -68,6 +68,7 @@ constexpr int kMaxRunLds = 4 * kXQ * kWave * 16 + 8 * 4 * 8 * 4;
 
 constexpr int row_groups(int kw) { return kw == 2 ? 4 : (kw <= 4 ? 2 : 1); }
 
+
 // One op of a run: 64 bytes, so that a workgroup fetches all of its fields
 // with one scalar load (s_load_dwordx16).
 struct __attribute__((aligned(64))) RunOp {
@@ -81,6 +82,18 @@ struct __attribute__((aligned(64))) RunOp {
 };
 static_assert(sizeof(RunOp) == 64, "one s_load_dwordx16 per op");
 typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+
+// Pointers read from the op table are generic; loads through them would be
+// flat loads, which count on the LDS counter too and so leave the compiler
+// only full waits.  Every pointer of an op is global memory.
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gbl(const T* p) {
+    return (const __attribute__((address_space(1))) T*)p;
+}
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gbl(T* p) {
+    return (__attribute__((address_space(1))) T*)p;
+}
 
 // The op table.  The first workgroup of ops 1..7 (INT32_MAX for unused ops)
 // and the ops' KW (4 bits each) are passed as scalar arguments ahead of it:
@@ -115,38 +128,68 @@ __device__ __forceinline__ void wait_vm(int n, float& after) {
     }
 }
 
-template <int KW, int R>
-__device__ __forceinline__ void run_tile(const RunOp& o, int tile, char* lds) {
+// An op's fields, from the argument segment with one scalar load; the load
+// is issued where the compiler likes (at the top) and waited for at the
+// first use of a field.
+__device__ __forceinline__ RunOp load_op(const RunOp* op) {
+    const u32x16 d = *reinterpret_cast<const u32x16*>(op);
+    const uint32_t w[16] = {d[0], d[1], d[2],  d[3],  d[4],  d[5],  d[6],  d[7],
+                            d[8], d[9], d[10], d[11], d[12], d[13], d[14], d[15]};
+    RunOp o;
+    __builtin_memcpy(&o, w, sizeof o);
+    return o;
+}
+
+// One tile.  PRE: the op's weight pointer comes in SGPRs that the hardware
+// preloaded (a kernel argument), K = 2048 KW is a constant and every row of
+// the tile exists, so the tile's weight loads go out first, before the op's
+// other fields have arrived; the x copies, scale and zero-byte loads follow.
+// Otherwise the loads go in the order x, scales, zero bytes, weights.
+template <int KW, int R, bool PRE>
+__device__ __forceinline__ void run_tile(const RunOp* op, const uint8_t* pre_packed, int tile,
+                                         char* lds) {
     constexpr int RGW = row_groups(KW);
     constexpr bool kShare = RGW > 1;
     constexpr int kActive = KW * RGW;
+    constexpr int cols = KW * 2048;
+    constexpr int64_t rbytes = cols / 2;
     static_assert(kActive <= kRunWaves && R % 4 == 0 && R <= 8, "tile shape");
     u32x4* xsh = reinterpret_cast<u32x4*>(lds);                                    // [KW kXQ][64]
     float* part = reinterpret_cast<float*>(lds + (kShare ? KW * kXQ * kWave * 16 : 0));  // [RGW][KW][R]
 
+    const RunOp o = load_op(op);
+    const uint8_t* packed = PRE ? pre_packed : o.packed;
+    const int rows = PRE ? INT32_MAX : o.rows;  // the clamp of the row index
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const bool active = wave < kActive;
     const int kw = wave % KW, rg = active ? wave / KW : 0;
-    const int rows = o.rows, cols = o.cols, gshift = o.gshift;
     const int row0 = (tile * RGW + rg) * R;
     const int c = kw * kWave + lane;
-    const int G = cols >> (5 + gshift);
-    const int g = c >> gshift;
-    const int64_t rbytes = cols >> 1;
 
-    // Loads: x (copies into LDS, or this lane's 64 bytes), then R scale, R
+    // Loads: x (copies into LDS, or this lane's 64 bytes), R scale, R
     // zero-byte and R weight loads.  With x in LDS they are written out as
-    // instructions, so that the wait for the copies counts exactly the 3R
-    // loads issued after them (vector loads complete in order, and the
-    // compiler does not count direct-to-LDS loads); with x per lane the
-    // compiler issues and waits for them itself.
+    // instructions, so that the wait for the copies counts exactly the loads
+    // issued after them (vector loads complete in order, and the compiler
+    // does not count direct-to-LDS loads); with x per lane the compiler
+    // issues and waits for them itself.
     u32x4 xq[kXQ];
     float sv[R];
     uint32_t zb[R];
     u32x4 w[R];
+    int gshift = 0;
     if (active) {
         if constexpr (kShare) {
+            const uint32_t voff = static_cast<uint32_t>(c) * 16u;
+            if constexpr (PRE) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int64_t rr = min(row0 + r, rows - 1);
+                    const uint8_t* prow = packed + rr * rbytes;
+                    asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(w[r]) : "v"(voff), "s"(prow)
+                                 : "memory");
+                }
+            }
             const uint32_t base = static_cast<uint32_t>(reinterpret_cast<size_t>(
                 (__attribute__((address_space(3))) void*)xsh));
 #pragma unroll
@@ -156,6 +199,9 @@ __device__ __forceinline__ void run_tile(const RunOp& o, int tile, char* lds) {
                 x_dma16(o.x + ((kwp * kWave + lane) * kXQ + j) * 8,
                         __builtin_amdgcn_readfirstlane(base + t * kWave * 16));
             }
+            gshift = o.gshift;
+            const int G = cols >> (5 + gshift);
+            const int g = c >> gshift;
             const uint32_t soff = static_cast<uint32_t>(g) * 4u, zoff = static_cast<uint32_t>(g >> 1);
 #pragma unroll
             for (int r = 0; r < R; ++r) {
@@ -167,33 +213,54 @@ __device__ __forceinline__ void run_tile(const RunOp& o, int tile, char* lds) {
                 asm volatile("global_load_ubyte %0, %1, %2" : "=v"(zb[r]) : "v"(zoff), "s"(zrow)
                              : "memory");
             }
-            const uint32_t voff = static_cast<uint32_t>(c) * 16u;
+            if constexpr (PRE) {
+                __builtin_amdgcn_s_setprio(0);
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * R) : "memory");  // x (and the weights)
+            } else {
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int64_t rr = min(row0 + r, rows - 1);
-                const uint8_t* prow = o.packed + rr * rbytes;
-                asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(w[r]) : "v"(voff), "s"(prow)
-                             : "memory");
+                for (int r = 0; r < R; ++r) {
+                    const int64_t rr = min(row0 + r, rows - 1);
+                    const uint8_t* prow = packed + rr * rbytes;
+                    asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(w[r]) : "v"(voff), "s"(prow)
+                                 : "memory");
+                }
+                __builtin_amdgcn_s_setprio(0);
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * R) : "memory");  // x has landed
             }
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * R) : "memory");  // x has landed
         } else {
-            const u32x4* xs = reinterpret_cast<const u32x4*>(o.x) + c * kXQ;
+            if constexpr (PRE) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int64_t rr = min(row0 + r, rows - 1);
+                    w[r] = __builtin_nontemporal_load(gbl(reinterpret_cast<const u32x4*>(packed + rr * rbytes)) + c);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // the weight loads first
+            }
+            gshift = o.gshift;
+            const int G = cols >> (5 + gshift);
+            const int g = c >> gshift;
+            const auto xs = gbl(reinterpret_cast<const u32x4*>(o.x)) + c * kXQ;
 #pragma unroll
             for (int q = 0; q < kXQ; ++q) xq[q] = xs[q];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const int64_t rr = min(row0 + r, rows - 1);
-                sv[r] = o.scales[rr * G + g];
-                zb[r] = o.zeros[rr * (G >> 1) + (g >> 1)];
+                sv[r] = gbl(o.scales + rr * G)[g];
+                zb[r] = gbl(o.zeros + rr * (G >> 1))[g >> 1];
             }
+            if constexpr (!PRE) {
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int64_t rr = min(row0 + r, rows - 1);
-                w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(o.packed + rr * rbytes) + c);
+                for (int r = 0; r < R; ++r) {
+                    const int64_t rr = min(row0 + r, rows - 1);
+                    w[r] = __builtin_nontemporal_load(gbl(reinterpret_cast<const u32x4*>(packed + rr * rbytes)) + c);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);  // every load above issued before any use
+            __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
+    __builtin_amdgcn_s_setprio(0);  // the waves that issue no loads
     if constexpr (kShare) {
         __builtin_amdgcn_s_barrier();  // every wave's copies of x, in LDS
         if (active) {
@@ -223,23 +290,57 @@ __device__ __forceinline__ void run_tile(const RunOp& o, int tile, char* lds) {
             xsm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.w), as_bf16x2(ones), xsm, false);
         }
         const NibConsts nk = nib_consts();
+        const int g = c >> gshift;
         float acc[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            // explicit loads: row r's weights have landed once at most
-            // R - 1 - r younger loads are outstanding; the values the loads
-            // produced count as produced by the wait
+        if constexpr (PRE) {
+            // With the weights first, every load has landed once the scale
+            // and zero-byte loads have (the compiler's waits, or one explicit
+            // wait here), so the rows' dot products go dword by dword across
+            // the rows: four independent chains instead of one chain of 16
+            // dot2 per row.  Each row still sums its dwords and pairs in the
+            // same order, so the results are those of the row-by-row loop.
             if constexpr (kShare) {
-                wait_vm(R - 1 - r, r == 0 ? xsm : acc[r > 0 ? r - 1 : 0]);
-                asm volatile("" : "+v"(w[r]));
-                if (r == 0) {
+                wait_vm(0, xsm);
+                static_assert(R == 4, "one tie statement for four rows");
+                asm volatile("" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(sv[0]),
+                             "+v"(sv[1]), "+v"(sv[2]), "+v"(sv[3]), "+v"(zb[0]), "+v"(zb[1]),
+                             "+v"(zb[2]), "+v"(zb[3]));
+            }
+            float dot[R];
 #pragma unroll
-                    for (int q = 0; q < R; ++q) asm volatile("" : "+v"(sv[q]), "+v"(zb[q]));
+            for (int r = 0; r < R; ++r) dot[r] = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const u32x4 wr = w[r];
+                    const uint32_t wd = d == 0 ? wr.x : d == 1 ? wr.y : d == 2 ? wr.z : wr.w;
+                    dot[r] = dot8_bf16(wd, xp[d], dot[r], nk);
                 }
             }
-            const uint32_t z = (g & 1) ? (zb[r] >> 4) : (zb[r] & 0xFu);
-            const float dot = chunk_dot<true>(w[r], xp, nk);
-            acc[r] = fmaf(sv[r], dot, -sv[r] * (136.0f + static_cast<float>(z)) * xsm);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t z = (g & 1) ? (zb[r] >> 4) : (zb[r] & 0xFu);
+                acc[r] = fmaf(sv[r], dot[r], -sv[r] * (136.0f + static_cast<float>(z)) * xsm);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                // explicit loads: row r's weights have landed once at most
+                // R - 1 - r younger loads are outstanding; the values the
+                // loads produced count as produced by the wait
+                if constexpr (kShare) {
+                    wait_vm(R - 1 - r, r == 0 ? xsm : acc[r > 0 ? r - 1 : 0]);
+                    asm volatile("" : "+v"(w[r]));
+                    if (r == 0) {
+#pragma unroll
+                        for (int q = 0; q < R; ++q) asm volatile("" : "+v"(sv[q]), "+v"(zb[q]));
+                    }
+                }
+                const uint32_t z = (g & 1) ? (zb[r] >> 4) : (zb[r] & 0xFu);
+                const float dot = chunk_dot<true>(w[r], xp, nk);
+                acc[r] = fmaf(sv[r], dot, -sv[r] * (136.0f + static_cast<float>(z)) * xsm);
+            }
         }
 #pragma unroll
         for (int r4 = 0; r4 < R; r4 += 4) {
@@ -258,14 +359,35 @@ __device__ __forceinline__ void run_tile(const RunOp& o, int tile, char* lds) {
 #pragma unroll
     for (int k = 1; k < KW; ++k) sum += part[((tr / R) * KW + k) * R + (tr % R)];
     const int row = tile * kTileRows + lane;
-    if (lane < kTileRows && row < rows) o.y[row] = kc::f32_to_bf16(sum);
+    if (lane < kTileRows && row < o.rows) gbl(o.y)[row] = kc::f32_to_bf16(sum);
+    // The op's unused fields stay in their registers until here: otherwise
+    // the compiler reuses them while the scalar load that fills them is still
+    // in flight, and has to wait for it before the first weight load.
+    if constexpr (PRE) asm volatile("" ::"s"(o.packed), "s"(o.cols), "s"(o.kw), "s"(o.pad_[0]), "s"(o.pad_[1]));
 }
 
+template <int R, bool PRE>
+__device__ __forceinline__ void run_dispatch(int kw, const RunOp* op, const uint8_t* pk, int tile,
+                                             char* lds) {
+    switch (kw) {
+        case 2: run_tile<2, R, PRE>(op, pk, tile, lds); break;
+        case 3: run_tile<3, R, PRE>(op, pk, tile, lds); break;
+        case 4: run_tile<4, R, PRE>(op, pk, tile, lds); break;
+        case 5: run_tile<5, R, PRE>(op, pk, tile, lds); break;
+        case 6: run_tile<6, R, PRE>(op, pk, tile, lds); break;
+        case 7: run_tile<7, R, PRE>(op, pk, tile, lds); break;
+        default: run_tile<8, R, PRE>(op, pk, tile, lds); break;
+    }
+}
+
+// Runs of up to 8 ops: the tile starts of ops 1..7 and the KW codes
+// preloaded, the rest of an op from the op table.
 template <int R>
 __global__ __launch_bounds__(kRunThreads) void gemv_run_kernel(int t1, int t2, int t3, int t4,
                                                                int t5, int t6, int t7, uint32_t kws,
                                                                RunParams p) {
     __shared__ __attribute__((aligned(16))) char lds[kMaxRunLds];
+    __builtin_amdgcn_s_setprio(kIssuePrio);  // until this tile's loads are out
     const int b = static_cast<int>(blockIdx.x);
     const int ts[KC_GEMV_CHAIN_MAX_OPS] = {0, t1, t2, t3, t4, t5, t6, t7};
     int i = 0, t0 = 0;
@@ -276,23 +398,33 @@ __global__ __launch_bounds__(kRunThreads) void gemv_run_kernel(int t1, int t2, i
             t0 = ts[j];
         }
     const int kw = (kws >> (4 * i)) & 0xF;
-    const u32x16 d = *reinterpret_cast<const u32x16*>(&p.op[i]);
-    RunOp o;
-    {
-        const uint32_t w[16] = {d[0], d[1], d[2], d[3], d[4], d[5], d[6], d[7],
-                                d[8], d[9], d[10], d[11], d[12], d[13], d[14], d[15]};
-        __builtin_memcpy(&o, w, sizeof o);
-    }
+    run_dispatch<R, false>(kw, &p.op[i], nullptr, b - t0, lds);
+}
+
+// Runs of up to 4 ops: the tile starts of ops 1..3, the KW codes (bits
+// 4i..4i+3) with a flag for an op whose last tile is full (bit 16 + i), the
+// ops' weight pointers and the tile count fill the first 13 argument dwords,
+// which the hardware preloads (14 fit beside the argument-segment pointer), so a
+// workgroup issues its weight loads without waiting for the op table.  The
+// last tile of an op whose row count it does not fill takes the table path.
+template <int R>
+__global__ __launch_bounds__(kRunThreads) void gemv_run4_kernel(
+    int t1, int t2, int t3, uint32_t kws, const uint8_t* pk0, const uint8_t* pk1,
+    const uint8_t* pk2, const uint8_t* pk3, int t_end, RunParams p) {
+    __shared__ __attribute__((aligned(16))) char lds[kMaxRunLds];
+    __builtin_amdgcn_s_setprio(kIssuePrio);  // until this tile's loads are out
+    const int b = static_cast<int>(blockIdx.x);
+    int i = 0, t0 = 0, tn = min(t1, t_end);
+    const uint8_t* pk = pk0;
+    if (b >= t1) { i = 1; t0 = t1; tn = min(t2, t_end); pk = pk1; }
+    if (b >= t2) { i = 2; t0 = t2; tn = min(t3, t_end); pk = pk2; }
+    if (b >= t3) { i = 3; t0 = t3; tn = t_end; pk = pk3; }
+    const int kw = (kws >> (4 * i)) & 0xF;
     const int tile = b - t0;
-    switch (kw) {
-        case 2: run_tile<2, R>(o, tile, lds); break;
-        case 3: run_tile<3, R>(o, tile, lds); break;
-        case 4: run_tile<4, R>(o, tile, lds); break;
-        case 5: run_tile<5, R>(o, tile, lds); break;
-        case 6: run_tile<6, R>(o, tile, lds); break;
-        case 7: run_tile<7, R>(o, tile, lds); break;
-        default: run_tile<8, R>(o, tile, lds); break;
-    }
+    if (b < tn - 1 || ((kws >> (16 + i)) & 1u))
+        run_dispatch<R, true>(kw, &p.op[i], pk, tile, lds);
+    else
+        run_dispatch<R, false>(kw, &p.op[i], nullptr, tile, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -382,8 +514,17 @@ int launch_run(const char* fn, const kc_gemv_op* ops, int first, int last, hipSt
             return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: %lld tiles in one launch", fn,
                                  (long long)tiles);
     }
-    gemv_run_kernel<kRunRows><<<static_cast<unsigned>(tiles), kRunThreads, 0, stream>>>(
-        p.tile0[1], p.tile0[2], p.tile0[3], p.tile0[4], p.tile0[5], p.tile0[6], p.tile0[7], kws, p);
+    if (n <= 4) {
+        for (int k = 0; k < n; ++k)
+            if (p.op[k].rows % (kRunRows * row_groups(p.op[k].kw)) == 0) kws |= 1u << (16 + k);
+        gemv_run4_kernel<kRunRows><<<static_cast<unsigned>(tiles), kRunThreads, 0, stream>>>(
+            p.tile0[1], p.tile0[2], p.tile0[3], kws, p.op[0].packed, p.op[1].packed,
+            p.op[2].packed, p.op[3].packed, static_cast<int>(tiles), p);
+    } else {
+        gemv_run_kernel<kRunRows><<<static_cast<unsigned>(tiles), kRunThreads, 0, stream>>>(
+            p.tile0[1], p.tile0[2], p.tile0[3], p.tile0[4], p.tile0[5], p.tile0[6], p.tile0[7],
+            kws, p);
+    }
     return kc::check_launch(fn);
 }
 

@@ -153,6 +153,7 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_int4_fast_kernel(
     constexpr int kQPT = (kMaxQuads + kThreadsWG - 1) / kThreadsWG;  // x quads per thread
     extern __shared__ u32x4 xl[];                                    // x quads, then chunk sums
 
+    __builtin_amdgcn_s_setprio(kIssuePrio);  // until the loads are out
     const int lane = threadIdx.x & (kWave - 1);
     // wave-uniform: row bases and K offsets stay in SGPRs, so the loads
     // address with a scalar base and one shared lane offset
@@ -207,6 +208,8 @@ __global__ __launch_bounds__(WPB * kWave) void gemv_int4_fast_kernel(
     }
     // keep every load above this point: the compiler otherwise sinks weight
     // loads towards their uses, leaving one row in flight at a time
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_sched_barrier(0);
 
     // 1d. fused RMSNorm: x = bf16(gamma h) is staged in place of h, and each
@@ -387,6 +390,7 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
     static_assert(BF16 || !NORM, "the fused RMSNorm takes bf16 x");
     constexpr int kXQ = BF16 ? 4 : 8;  // 16-byte quads of x per 32-k chunk
     __shared__ float part[RGW][KW][R + 1];  // row sums, then the sum of h^2
+    __builtin_amdgcn_s_setprio(kIssuePrio);  // until the loads are out
     const int lane = threadIdx.x & (kWave - 1);
     // wave-uniform: row bases and K offsets stay in SGPRs, so the loads
     // address with a scalar base and one shared lane offset
@@ -457,6 +461,7 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
             asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(w[r]) : "v"(voff), "s"(prow)
                          : "memory");
         }
+        __builtin_amdgcn_s_setprio(0);
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * R) : "memory");
         __builtin_amdgcn_s_barrier();
 #pragma unroll
@@ -474,6 +479,8 @@ __global__ __launch_bounds__(KW * RGW * kWave) void gemv_int4_xl_kernel(
             w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(packed + rr * rbytes) + c);
         }
         __builtin_amdgcn_sched_barrier(0);  // every load above issued before any use
+        __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     uint32_t sel_lo, sel_hi;  // v_perm_b32 selectors, in VGPRs

@@ -454,10 +454,15 @@ FUSED_RUNS = [
     # K above 16384): those launch on their own, the neighbours keep theirs
     [(100, 4096, 128), (50, 2048, 128), (60, 8192, 128), (70, 8192 + 2048, 128),
      (40, 5120, 128), (30, 18432, 128), (20, 4096, 128), (10, 6144, 128)],
+    # runs of up to four ops (weight pointers passed in preloaded arguments):
+    # full and ragged last tiles side by side, and three ops
+    [(48, 4096, 128), (37, 6144, 64), (1000, 8192, 32), (5, 14336, 128)],
+    [(4100, 10240, 128), (16, 4096, 256), (9, 12288, 128)],
 ]
 
 
-@pytest.mark.parametrize("specs", FUSED_RUNS, ids=["decode_layer", "every_kw", "group_sizes", "mixed"])
+@pytest.mark.parametrize("specs", FUSED_RUNS, ids=["decode_layer", "every_kw", "group_sizes", "mixed",
+                                                   "four_ragged", "three"])
 def test_chain_fused_run(gpu, oracle, specs):
     results = _run_chain(gpu, specs, [-1] * len(specs), seed=4000 + len(specs))
     _check_run(gpu, oracle, specs, results)
