@@ -737,12 +737,18 @@ int device_cus() {
 }
 
 // Rows held by each workgroup of the persistent smoothing quantizer: the one
-// being reduced and kSmoothDepth - 1 in flight.  Its grid is kSmoothWaves
-// times what the device holds at once; with more row slots in flight
-// (depth 3-4) or exactly one resident round the 8192-column cases measured
-// the same or up to 3 % slower.
+// being reduced and kSmoothDepth - 1 in flight.  Its grid is a multiple of
+// what the device holds at once.  Workgroups that share a CU progress at
+// different rates (on cfg4 X the first finished after 22 us, the last after
+// 45 us, with the same row counts), so more, shorter workgroups shorten the
+// tail, at the cost of one setup per workgroup: loading the factors and,
+// for the division, their reciprocals (an IEEE division each).  For the
+// multiplication (cfg4 W, 28672 x 8192: 121.9 -> 113.6 us) eight rounds
+// pay; for the division (cfg4 X 70.5 against 72.2 us at four rounds) and the
+// plain rows (cfg1) two.  More row slots in flight (depth 3-4) measured the
+// same or up to 3 % slower.
 constexpr int kSmoothDepth = 2;
-constexpr int kSmoothWaves = 2;
+constexpr int smooth_rounds(Smooth s) { return s == Smooth::kMul ? 8 : 2; }
 
 template <int NV, bool BF16, Smooth S, bool FULL>
 int launch_smooth(const char* fn, const void* in, const float* smooth, int8_t* out, float* scales,
@@ -754,7 +760,7 @@ int launch_smooth(const char* fn, const void* in, const float* smooth, int8_t* o
             n = 1;
         return n;
     }();
-    const int64_t grid = std::min<int64_t>(rows, int64_t{kSmoothWaves} * per_cu * device_cus());
+    const int64_t grid = std::min<int64_t>(rows, int64_t{smooth_rounds(S)} * per_cu * device_cus());
     kernel<<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(in, smooth, out, scales, rows, cols);
     return kc::check_launch(fn);
 }
