@@ -140,14 +140,11 @@ __device__ __forceinline__ RunOp load_op(const RunOp* op) {
     return o;
 }
 
-// One tile.  PRE: the op's weight pointer comes in SGPRs that the hardware
-// preloaded (a kernel argument), K = 2048 KW is a constant and every row of
-// the tile exists, so the tile's weight loads go out first, before the op's
-// other fields have arrived; the x copies, scale and zero-byte loads follow.
-// Otherwise the loads go in the order x, scales, zero bytes, weights.
-template <int KW, int R, bool PRE>
-__device__ __forceinline__ void run_tile(const RunOp* op, const uint8_t* pre_packed, int tile,
-                                         char* lds) {
+// One tile: loads in the order x (copies into LDS, or this lane's 64 bytes),
+// R scale, R zero-byte and R weight loads.  K = 2048 KW is a constant of the
+// tile code.
+template <int KW, int R>
+__device__ __forceinline__ void run_tile(const RunOp* op, int tile, char* lds) {
     constexpr int RGW = row_groups(KW);
     constexpr bool kShare = RGW > 1;
     constexpr int kActive = KW * RGW;
@@ -158,38 +155,28 @@ __device__ __forceinline__ void run_tile(const RunOp* op, const uint8_t* pre_pac
     float* part = reinterpret_cast<float*>(lds + (kShare ? KW * kXQ * kWave * 16 : 0));  // [RGW][KW][R]
 
     const RunOp o = load_op(op);
-    const uint8_t* packed = PRE ? pre_packed : o.packed;
-    const int rows = PRE ? INT32_MAX : o.rows;  // the clamp of the row index
+    const int rows = o.rows;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const bool active = wave < kActive;
     const int kw = wave % KW, rg = active ? wave / KW : 0;
     const int row0 = (tile * RGW + rg) * R;
     const int c = kw * kWave + lane;
+    const int gshift = o.gshift;
+    const int G = cols >> (5 + gshift);
+    const int g = c >> gshift;
 
-    // Loads: x (copies into LDS, or this lane's 64 bytes), R scale, R
-    // zero-byte and R weight loads.  With x in LDS they are written out as
-    // instructions, so that the wait for the copies counts exactly the loads
-    // issued after them (vector loads complete in order, and the compiler
-    // does not count direct-to-LDS loads); with x per lane the compiler
-    // issues and waits for them itself.
+    // With x in LDS the loads are written out as instructions, so that the
+    // wait for the copies counts exactly the 3R loads issued after them
+    // (vector loads complete in order, and the compiler does not count
+    // direct-to-LDS loads); with x per lane the compiler issues and waits for
+    // them itself.  The op's pointers are read as global-memory pointers.
     u32x4 xq[kXQ];
     float sv[R];
     uint32_t zb[R];
     u32x4 w[R];
-    int gshift = 0;
     if (active) {
         if constexpr (kShare) {
-            const uint32_t voff = static_cast<uint32_t>(c) * 16u;
-            if constexpr (PRE) {
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const int64_t rr = min(row0 + r, rows - 1);
-                    const uint8_t* prow = packed + rr * rbytes;
-                    asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(w[r]) : "v"(voff), "s"(prow)
-                                 : "memory");
-                }
-            }
             const uint32_t base = static_cast<uint32_t>(reinterpret_cast<size_t>(
                 (__attribute__((address_space(3))) void*)xsh));
 #pragma unroll
@@ -199,9 +186,6 @@ __device__ __forceinline__ void run_tile(const RunOp* op, const uint8_t* pre_pac
                 x_dma16(o.x + ((kwp * kWave + lane) * kXQ + j) * 8,
                         __builtin_amdgcn_readfirstlane(base + t * kWave * 16));
             }
-            gshift = o.gshift;
-            const int G = cols >> (5 + gshift);
-            const int g = c >> gshift;
             const uint32_t soff = static_cast<uint32_t>(g) * 4u, zoff = static_cast<uint32_t>(g >> 1);
 #pragma unroll
             for (int r = 0; r < R; ++r) {
@@ -213,32 +197,17 @@ __device__ __forceinline__ void run_tile(const RunOp* op, const uint8_t* pre_pac
                 asm volatile("global_load_ubyte %0, %1, %2" : "=v"(zb[r]) : "v"(zoff), "s"(zrow)
                              : "memory");
             }
-            if constexpr (PRE) {
-                __builtin_amdgcn_s_setprio(0);
-                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * R) : "memory");  // x (and the weights)
-            } else {
+            const uint32_t voff = static_cast<uint32_t>(c) * 16u;
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const int64_t rr = min(row0 + r, rows - 1);
-                    const uint8_t* prow = packed + rr * rbytes;
-                    asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(w[r]) : "v"(voff), "s"(prow)
-                                 : "memory");
-                }
-                __builtin_amdgcn_s_setprio(0);
-                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * R) : "memory");  // x has landed
+            for (int r = 0; r < R; ++r) {
+                const int64_t rr = min(row0 + r, rows - 1);
+                const uint8_t* prow = o.packed + rr * rbytes;
+                asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(w[r]) : "v"(voff), "s"(prow)
+                             : "memory");
             }
+            __builtin_amdgcn_s_setprio(0);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * R) : "memory");  // x has landed
         } else {
-            if constexpr (PRE) {
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const int64_t rr = min(row0 + r, rows - 1);
-                    w[r] = __builtin_nontemporal_load(gbl(reinterpret_cast<const u32x4*>(packed + rr * rbytes)) + c);
-                }
-                __builtin_amdgcn_sched_barrier(0);  // the weight loads first
-            }
-            gshift = o.gshift;
-            const int G = cols >> (5 + gshift);
-            const int g = c >> gshift;
             const auto xs = gbl(reinterpret_cast<const u32x4*>(o.x)) + c * kXQ;
 #pragma unroll
             for (int q = 0; q < kXQ; ++q) xq[q] = xs[q];
@@ -248,12 +217,10 @@ __device__ __forceinline__ void run_tile(const RunOp* op, const uint8_t* pre_pac
                 sv[r] = gbl(o.scales + rr * G)[g];
                 zb[r] = gbl(o.zeros + rr * (G >> 1))[g >> 1];
             }
-            if constexpr (!PRE) {
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const int64_t rr = min(row0 + r, rows - 1);
-                    w[r] = __builtin_nontemporal_load(gbl(reinterpret_cast<const u32x4*>(packed + rr * rbytes)) + c);
-                }
+            for (int r = 0; r < R; ++r) {
+                const int64_t rr = min(row0 + r, rows - 1);
+                w[r] = __builtin_nontemporal_load(gbl(reinterpret_cast<const u32x4*>(o.packed + rr * rbytes)) + c);
             }
             __builtin_amdgcn_sched_barrier(0);  // every load above issued before any use
             __builtin_amdgcn_s_setprio(0);
@@ -290,57 +257,23 @@ __device__ __forceinline__ void run_tile(const RunOp* op, const uint8_t* pre_pac
             xsm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.w), as_bf16x2(ones), xsm, false);
         }
         const NibConsts nk = nib_consts();
-        const int g = c >> gshift;
         float acc[R];
-        if constexpr (PRE) {
-            // With the weights first, every load has landed once the scale
-            // and zero-byte loads have (the compiler's waits, or one explicit
-            // wait here), so the rows' dot products go dword by dword across
-            // the rows: four independent chains instead of one chain of 16
-            // dot2 per row.  Each row still sums its dwords and pairs in the
-            // same order, so the results are those of the row-by-row loop.
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            // explicit loads: row r's weights have landed once at most
+            // R - 1 - r younger loads are outstanding; the values the loads
+            // produced count as produced by the wait
             if constexpr (kShare) {
-                wait_vm(0, xsm);
-                static_assert(R == 4, "one tie statement for four rows");
-                asm volatile("" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(sv[0]),
-                             "+v"(sv[1]), "+v"(sv[2]), "+v"(sv[3]), "+v"(zb[0]), "+v"(zb[1]),
-                             "+v"(zb[2]), "+v"(zb[3]));
-            }
-            float dot[R];
+                wait_vm(R - 1 - r, r == 0 ? xsm : acc[r > 0 ? r - 1 : 0]);
+                asm volatile("" : "+v"(w[r]));
+                if (r == 0) {
 #pragma unroll
-            for (int r = 0; r < R; ++r) dot[r] = 0.0f;
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const u32x4 wr = w[r];
-                    const uint32_t wd = d == 0 ? wr.x : d == 1 ? wr.y : d == 2 ? wr.z : wr.w;
-                    dot[r] = dot8_bf16(wd, xp[d], dot[r], nk);
+                    for (int q = 0; q < R; ++q) asm volatile("" : "+v"(sv[q]), "+v"(zb[q]));
                 }
             }
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const uint32_t z = (g & 1) ? (zb[r] >> 4) : (zb[r] & 0xFu);
-                acc[r] = fmaf(sv[r], dot[r], -sv[r] * (136.0f + static_cast<float>(z)) * xsm);
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                // explicit loads: row r's weights have landed once at most
-                // R - 1 - r younger loads are outstanding; the values the
-                // loads produced count as produced by the wait
-                if constexpr (kShare) {
-                    wait_vm(R - 1 - r, r == 0 ? xsm : acc[r > 0 ? r - 1 : 0]);
-                    asm volatile("" : "+v"(w[r]));
-                    if (r == 0) {
-#pragma unroll
-                        for (int q = 0; q < R; ++q) asm volatile("" : "+v"(sv[q]), "+v"(zb[q]));
-                    }
-                }
-                const uint32_t z = (g & 1) ? (zb[r] >> 4) : (zb[r] & 0xFu);
-                const float dot = chunk_dot<true>(w[r], xp, nk);
-                acc[r] = fmaf(sv[r], dot, -sv[r] * (136.0f + static_cast<float>(z)) * xsm);
-            }
+            const uint32_t z = (g & 1) ? (zb[r] >> 4) : (zb[r] & 0xFu);
+            const float dot = chunk_dot<true>(w[r], xp, nk);
+            acc[r] = fmaf(sv[r], dot, -sv[r] * (136.0f + static_cast<float>(z)) * xsm);
         }
 #pragma unroll
         for (int r4 = 0; r4 < R; r4 += 4) {
@@ -359,29 +292,14 @@ __device__ __forceinline__ void run_tile(const RunOp* op, const uint8_t* pre_pac
 #pragma unroll
     for (int k = 1; k < KW; ++k) sum += part[((tr / R) * KW + k) * R + (tr % R)];
     const int row = tile * kTileRows + lane;
-    if (lane < kTileRows && row < o.rows) gbl(o.y)[row] = kc::f32_to_bf16(sum);
-    // The op's unused fields stay in their registers until here: otherwise
-    // the compiler reuses them while the scalar load that fills them is still
-    // in flight, and has to wait for it before the first weight load.
-    if constexpr (PRE) asm volatile("" ::"s"(o.packed), "s"(o.cols), "s"(o.kw), "s"(o.pad_[0]), "s"(o.pad_[1]));
+    if (lane < kTileRows && row < rows) gbl(o.y)[row] = kc::f32_to_bf16(sum);
 }
 
-template <int R, bool PRE>
-__device__ __forceinline__ void run_dispatch(int kw, const RunOp* op, const uint8_t* pk, int tile,
-                                             char* lds) {
-    switch (kw) {
-        case 2: run_tile<2, R, PRE>(op, pk, tile, lds); break;
-        case 3: run_tile<3, R, PRE>(op, pk, tile, lds); break;
-        case 4: run_tile<4, R, PRE>(op, pk, tile, lds); break;
-        case 5: run_tile<5, R, PRE>(op, pk, tile, lds); break;
-        case 6: run_tile<6, R, PRE>(op, pk, tile, lds); break;
-        case 7: run_tile<7, R, PRE>(op, pk, tile, lds); break;
-        default: run_tile<8, R, PRE>(op, pk, tile, lds); break;
-    }
-}
-
-// Runs of up to 8 ops: the tile starts of ops 1..7 and the KW codes
-// preloaded, the rest of an op from the op table.
+// The run kernel: the tile starts of ops 1..7 (INT32_MAX for unused ops) and
+// the ops' KW (4 bits each) come as scalar arguments, which the hardware
+// preloads into SGPRs, so a workgroup finds its op and its tile code with no
+// memory access; the op's fields then take one scalar load.  A wave issues
+// its tile's loads at a raised priority and computes at the normal one.
 template <int R>
 __global__ __launch_bounds__(kRunThreads) void gemv_run_kernel(int t1, int t2, int t3, int t4,
                                                                int t5, int t6, int t7, uint32_t kws,
@@ -398,33 +316,17 @@ __global__ __launch_bounds__(kRunThreads) void gemv_run_kernel(int t1, int t2, i
             t0 = ts[j];
         }
     const int kw = (kws >> (4 * i)) & 0xF;
-    run_dispatch<R, false>(kw, &p.op[i], nullptr, b - t0, lds);
-}
-
-// Runs of up to 4 ops: the tile starts of ops 1..3, the KW codes (bits
-// 4i..4i+3) with a flag for an op whose last tile is full (bit 16 + i), the
-// ops' weight pointers and the tile count fill the first 13 argument dwords,
-// which the hardware preloads (14 fit beside the argument-segment pointer), so a
-// workgroup issues its weight loads without waiting for the op table.  The
-// last tile of an op whose row count it does not fill takes the table path.
-template <int R>
-__global__ __launch_bounds__(kRunThreads) void gemv_run4_kernel(
-    int t1, int t2, int t3, uint32_t kws, const uint8_t* pk0, const uint8_t* pk1,
-    const uint8_t* pk2, const uint8_t* pk3, int t_end, RunParams p) {
-    __shared__ __attribute__((aligned(16))) char lds[kMaxRunLds];
-    __builtin_amdgcn_s_setprio(kIssuePrio);  // until this tile's loads are out
-    const int b = static_cast<int>(blockIdx.x);
-    int i = 0, t0 = 0, tn = min(t1, t_end);
-    const uint8_t* pk = pk0;
-    if (b >= t1) { i = 1; t0 = t1; tn = min(t2, t_end); pk = pk1; }
-    if (b >= t2) { i = 2; t0 = t2; tn = min(t3, t_end); pk = pk2; }
-    if (b >= t3) { i = 3; t0 = t3; tn = t_end; pk = pk3; }
-    const int kw = (kws >> (4 * i)) & 0xF;
+    const RunOp* op = &p.op[i];
     const int tile = b - t0;
-    if (b < tn - 1 || ((kws >> (16 + i)) & 1u))
-        run_dispatch<R, true>(kw, &p.op[i], pk, tile, lds);
-    else
-        run_dispatch<R, false>(kw, &p.op[i], nullptr, tile, lds);
+    switch (kw) {
+        case 2: run_tile<2, R>(op, tile, lds); break;
+        case 3: run_tile<3, R>(op, tile, lds); break;
+        case 4: run_tile<4, R>(op, tile, lds); break;
+        case 5: run_tile<5, R>(op, tile, lds); break;
+        case 6: run_tile<6, R>(op, tile, lds); break;
+        case 7: run_tile<7, R>(op, tile, lds); break;
+        default: run_tile<8, R>(op, tile, lds); break;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -514,17 +416,8 @@ int launch_run(const char* fn, const kc_gemv_op* ops, int first, int last, hipSt
             return kc::set_error(KC_ERR_INVALID_ARGUMENT, "%s: %lld tiles in one launch", fn,
                                  (long long)tiles);
     }
-    if (n <= 4) {
-        for (int k = 0; k < n; ++k)
-            if (p.op[k].rows % (kRunRows * row_groups(p.op[k].kw)) == 0) kws |= 1u << (16 + k);
-        gemv_run4_kernel<kRunRows><<<static_cast<unsigned>(tiles), kRunThreads, 0, stream>>>(
-            p.tile0[1], p.tile0[2], p.tile0[3], kws, p.op[0].packed, p.op[1].packed,
-            p.op[2].packed, p.op[3].packed, static_cast<int>(tiles), p);
-    } else {
-        gemv_run_kernel<kRunRows><<<static_cast<unsigned>(tiles), kRunThreads, 0, stream>>>(
-            p.tile0[1], p.tile0[2], p.tile0[3], p.tile0[4], p.tile0[5], p.tile0[6], p.tile0[7],
-            kws, p);
-    }
+    gemv_run_kernel<kRunRows><<<static_cast<unsigned>(tiles), kRunThreads, 0, stream>>>(
+        p.tile0[1], p.tile0[2], p.tile0[3], p.tile0[4], p.tile0[5], p.tile0[6], p.tile0[7], kws, p);
     return kc::check_launch(fn);
 }
 
