@@ -11,7 +11,7 @@ timed steps, bracketed by torch.cuda.synchronize().  Inputs are resident in
 HBM and rotate over enough copies (> 1 GiB) that the 256 MB Infinity Cache
 cannot hold them.  The four GEMVs read independent inputs, and a step is one
 kc_gemv_int4_bf16_chain call, which runs them as ONE launch of the fused tile
-(gemv_run4_kernel); the same call captured in a HIP graph, and the four
+(gemv_run_kernel); the same call captured in a HIP graph, and the four
 kc_gemv_int4_bf16 launches back to back, are timed beside it, and `value` is
 the fastest of these (all in `config.launch_modes_GBps`).  The same chain
 with each GEMV reading the previous one's output (QKV -> O -> gate/up ->
@@ -674,7 +674,7 @@ def main() -> int:
     e1.record()
     torch.cuda.synchronize()
     run_us = e0.elapsed_time(e1) * 1e3 / reps
-    log(f"# fused run (gemv_run4_kernel, the layer in one launch): {run_us:.2f} us/launch, "
+    log(f"# fused run (gemv_run_kernel, the layer in one launch): {run_us:.2f} us/launch, "
         f"{layer_bytes / run_us / 1e3:.1f} GB/s")
 
     # ---- per-kernel durations with HIP events (launch stream, backlogged) ---
@@ -740,7 +740,7 @@ def main() -> int:
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                 "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
                 "traffic_source": traffic_note,
-                "kernel": "gemv_run4_kernel: the decode layer's four GEMVs in one launch",
+                "kernel": "gemv_run_kernel: the decode layer's four GEMVs in one launch",
                 "bytes_per_launch": layer_bytes, "avg_us": round(run_us, 3)}
 
     def stream_ptr() -> int:
