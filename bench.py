@@ -500,6 +500,23 @@ def main() -> int:
             torch.cuda.synchronize()
             print(f"gemv probe: {name} x 20, floor read of {wb} B x 20", flush=True)
         del fbuf
+        # the decode layer's four GEMVs in one launch of the fused tile
+        import ctypes
+        arrs = []
+        for r in range(copies):
+            arr = (ops.GemvOp * len(LLAMA))()
+            for i, (_, n, k) in enumerate(LLAMA):
+                p, s_, z = layers[r][i]
+                arr[i] = ops.GemvOp(p.data_ptr(), s_.data_ptr(), z.data_ptr(), xs[i].data_ptr(),
+                                    ys[i].data_ptr(), n, k, GS, 0)
+            arrs.append(arr)
+        for j in range(20):
+            st = lib.kc_gemv_int4_bf16_chain(ctypes.cast(arrs[j % copies], ctypes.c_void_p),
+                                             len(LLAMA), torch.cuda.current_stream().cuda_stream)
+            if st:
+                raise RuntimeError(lib.kc_last_error_string().decode())
+        torch.cuda.synchronize()
+        print("gemv probe: the fused decode layer x 20", flush=True)
         o = 1                                    # O projection's weights, fp32 x and y
         for j in range(20):
             p, s_, z = pools[o][j % len(pools[o])]
