@@ -28,11 +28,13 @@
 // Kernels, by M (kc_gemm_int4_bf16 at the bottom picks one):
 //   M 2..8    gemm_int4_xres_kernel: X resident in LDS, one wave per 16-row
 //             weight tile over all of K;
-//   M 9..64   gemm_int4_kslice_kernel: K split over the four waves of a CU,
-//             X from the cache into registers;
+//   M 9..64   gemm_int4_kslds_kernel: K split over the four waves of a CU,
+//             X and the weights streamed into LDS by direct-to-LDS loads;
+//             gemm_int4_kslice_kernel (X from the cache into registers)
+//             where that kernel's LDS does not fit (K above 8192 at M > 16);
 //   fallbacks gemm_int4_xres_kernel (M 9..16), gemm_int4_xbig_kernel
 //             (M 33..64) and gemm_int4_mfma_kernel (below) when the K-split
-//             kernel's coefficients do not fit in LDS (K above about 20000).
+//             kernels' coefficients do not fit in LDS (K above about 20000).
 //
 // gemm_int4_mfma_kernel work split.  A workgroup of NW waves owns
 // 16*RT*NW consecutive weight rows and the whole K; wave w owns row tiles
@@ -1215,6 +1217,304 @@ int launch_kslice(const char* fn, const uint8_t* packed, const float* scales, co
 }
 
 // ---------------------------------------------------------------------------
+// M 9..64 with both operands streamed through LDS: gemm_int4_kslds_kernel.
+//
+// The work split of gemm_int4_kslice_kernel (four waves per CU, wave w owns
+// K quarter w of RT = 7 row tiles for all MT activation tiles, the four K
+// parts summed through LDS at the end), with the operands brought in by
+// direct-to-LDS loads instead of through registers:
+//   * X: per T-block the wave's 16 MT rows x 256 bytes, in 1-KB blocks of
+//     four rows, each block one load instruction that reads its 1 KB in one
+//     piece (the register kernel's B-operand loads touch 32 cache lines per
+//     instruction).  Lane l of block j carries chunk u of local row
+//     r = l / 16, u = (l - 2 r - (j & 1)) mod 16, so chunk u of row r sits in
+//     slot 16 r + ((u + 2 r + (j & 1)) mod 16): a B-operand read (lane
+//     (i, kb), step s: chunk 4 kb + s of row 16 c + i) gives every eight
+//     consecutive lanes eight different 16-byte bank groups.
+//   * W: per T-block and row tile the wave-wide 1-KB load of the register
+//     kernel, lane l's 16 bytes in slot l.
+// One T-block of each is resident per wave.  X of the next T-block is
+// requested once the current one has been read out, each row tile's next
+// weights right after that tile's decode, so every load has about one
+// T-block to arrive.  The waits are explicit (loads complete in order:
+// vmcnt(7) before X, vmcnt(22) before each weight tile, counting the loads
+// issued since).  With no operand ring in registers, the accumulators, the
+// B operands and the matrix-core results fit the 256 VGPRs.
+// ---------------------------------------------------------------------------
+constexpr int kKlRT = 7;
+// Coefficient table row stride: 112 rows padded to 116 floats, so that the
+// staging writes (64 lanes, T-block fastest: 116 t + r) fall in 64 different
+// banks instead of 4, and a 4-row read stays 16-byte aligned (464 bytes).
+constexpr int kKlCS = 16 * kKlRT + 4;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return static_cast<uint32_t>(reinterpret_cast<size_t>((lds_void_t*)p));
+}
+
+// One global_load_lds_dwordx4: 16 bytes per lane from sbase + voff into LDS
+// at lds_base + 16 lane.  `after` is a register the load is made to depend
+// on (a value computed from the last LDS read of the slot it overwrites), so
+// it is issued after that read has returned.
+__device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t lds_base, uint32_t after) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base),
+                 "v"(after)
+                 : "memory", "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Per-wave LDS: X (4 MT KB), weights (RT KB), fold coefficients of the
+// wave's quarter (ceil(nT / 4) T-blocks x kKlCS x (s, c2)).
+template <int MT>
+__host__ __device__ constexpr size_t kslds_wave_bytes(int nT) {
+    return static_cast<size_t>(4 * MT + kKlRT) * 1024 + static_cast<size_t>((nT + kKsWaves - 1) / kKsWaves) * kKlCS * 8;
+}
+
+template <int MT>
+__host__ __device__ constexpr size_t kslds_lds_bytes(int nT) {
+    const size_t ops = kKsWaves * kslds_wave_bytes<MT>(nT);
+    const size_t red = static_cast<size_t>(kKsWaves) * kKlRT * MT * kWave * 16;
+    return ops > red ? ops : red;
+}
+
+template <int MT, bool SHUF>
+__global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
+    const uint8_t* __restrict__ packed, const float* __restrict__ scales,
+    const uint8_t* __restrict__ zeros, const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
+    int M, int N, int K, int gshift) {
+    extern __shared__ __align__(16) char lds[];
+    constexpr int RT = kKlRT;
+    constexpr int kRows = 16 * RT;
+    constexpr int kCS = kKlCS;  // coefficient row stride (floats per T-block)
+    constexpr int kXB = 4 * MT;  // X blocks of four rows per T-block
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int i = lane & 15, kb = lane >> 4;
+    const int nT = K / kTBlock;
+    const int G = nT >> gshift;
+    const int ntmax = (nT + kKsWaves - 1) / kKsWaves;
+    const int t0 = (wave * nT) / kKsWaves, t1 = ((wave + 1) * nT) / kKsWaves;
+    const int nt = t1 - t0;  // 0 for some waves when nT < 4
+    const int tl = max(t1 - 1, 0);
+    const int row_base = blockIdx.x * kRows;
+    char* xl = lds + static_cast<size_t>(wave) * kslds_wave_bytes<MT>(nT);
+    char* wl = xl + kXB * 1024;
+    float* cs = reinterpret_cast<float*>(wl + RT * 1024);
+    float* cz = cs + ntmax * kCS;
+    const uint32_t x_lds = lds_addr(xl), w_lds = lds_addr(wl);
+
+    // DMA offsets.  X block j, lane l: row 4 j + r (r = l / 16), chunk u.
+    // Rows below 16 (MT - 1) exist (M > 16 (MT - 1)): blocks j < 4 MT - 4
+    // take lane offset xg[j & 1] and 8 K j bytes on the scalar base; the last
+    // tile's four blocks clamp their rows to M - 1 per lane (xe).
+    uint32_t xg[2], xe[4];
+    {
+        const int r = lane >> 4;
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+            xg[p] = static_cast<uint32_t>(r) * static_cast<uint32_t>(2 * K) + 16u * (((lane & 15) - 2 * r - p) & 15);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int j = kXB - 4 + e;
+            const int u = ((lane & 15) - 2 * r - (j & 1)) & 15;
+            xe[e] = static_cast<uint32_t>(min(4 * j + r, M - 1)) * static_cast<uint32_t>(2 * K) + 16u * u;
+        }
+    }
+    uint32_t woff[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+        woff[rt] = SHUF ? static_cast<uint32_t>(min(row_base / 16 + rt, (N + 15) / 16 - 1)) * static_cast<uint32_t>(nT * 1024) + 16u * lane
+                        : static_cast<uint32_t>(min(row_base + 16 * rt + i, N - 1)) * static_cast<uint32_t>(K >> 1) + 16u * kb;
+    const uint8_t* xbytes = reinterpret_cast<const uint8_t*>(X);
+    auto issue_x = [&](int T, uint32_t after) {
+        const uint8_t* base = xbytes + 256 * min(T, tl);
+#pragma unroll
+        for (int j = 0; j < kXB - 4; ++j)
+            dma16(xg[j & 1], base + static_cast<size_t>(8 * j) * K, x_lds + 1024 * j, after);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dma16(xe[e], base, x_lds + 1024 * (kXB - 4 + e), after);
+    };
+    auto issue_w = [&](int rt, int T, uint32_t after) {
+        dma16(woff[rt], packed + 16 * kTStep<SHUF> * min(T, tl), w_lds + 1024 * rt, after);
+    };
+    // B-operand read offsets: lane (i, kb), step s reads chunk 4 kb + s of
+    // row 16 c + i (block 4 c + i / 4, local row i % 4) at xrd[s] + 4096 c.
+    uint32_t xrd[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int r = i & 3, j1 = (i >> 2) & 1;
+        xrd[s] = 1024u * (i >> 2) + 256u * r + 16u * ((4 * kb + s + 2 * r + j1) & 15);
+    }
+
+    issue_x(t0, 0u);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) issue_w(rt, t0, 0u);
+
+    // Fold coefficients of this wave's K range, cs[t][row] = s and
+    // cz[t][row] = -s (136 + z), as in gemm_int4_kslice_kernel.
+    {
+        constexpr int kBatch = 28;  // 16 T-blocks x 112 rows in one pass
+        const int items = nt * kRows;
+        const float inv_nt = 1.0f / static_cast<float>(max(nt, 1));
+        for (int base = 0; base < items; base += kBatch * kWave) {
+            float sv[kBatch];
+            uint32_t zb[kBatch];
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {
+                const int idx = min(base + b * kWave + lane, items - 1);
+                const int r = static_cast<int>((static_cast<float>(idx) + 0.5f) * inv_nt);
+                const int g = (t0 + idx - r * nt) >> gshift;
+                const int64_t row = min(row_base + r, N - 1);
+                sv[b] = scales[row * G + g];
+                zb[b] = zeros[row * (G >> 1) + (g >> 1)];
+            }
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {
+                const int idx = base + b * kWave + lane;
+                if (idx < items) {
+                    const int r = static_cast<int>((static_cast<float>(idx) + 0.5f) * inv_nt);
+                    const int t = idx - r * nt;
+                    const int g = (t0 + t) >> gshift;
+                    const uint32_t z = (g & 1) ? (zb[b] >> 4) : (zb[b] & 0xFu);
+                    cs[t * kCS + r] = sv[b];
+                    cz[t * kCS + r] = -sv[b] * static_cast<float>(136u + z);
+                }
+            }
+        }
+    }
+
+    const NibConsts nk = nib_consts();
+    uint32_t sel_lo, sel_hi;  // v_perm_b32 selectors, in VGPRs
+    asm volatile("v_mov_b32 %0, 0x05040100" : "=v"(sel_lo));
+    asm volatile("v_mov_b32 %0, 0x07060302" : "=v"(sel_hi));
+    const uint32_t ones = 0x3F803F80u;
+    f32x4 acc[RT][MT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int c = 0; c < MT; ++c) acc[rt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int T = t0; T < t1; ++T) {
+        const int tt = T - t0;
+        // X of this T-block: issued before the 7 weight loads of this T-block
+        wait_vmcnt<RT>();
+        bf16x8_t b[MT][4];
+        float xs[MT];
+#pragma unroll
+        for (int c = 0; c < MT; ++c) {
+            float sm = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const u32x4 d = *reinterpret_cast<const u32x4*>(xl + xrd[s] + 4096 * c);
+                u32x4 q;
+                q.x = __builtin_amdgcn_perm(d.z, d.x, sel_lo);  // (x0, x4)
+                q.y = __builtin_amdgcn_perm(d.z, d.x, sel_hi);  // (x1, x5)
+                q.z = __builtin_amdgcn_perm(d.w, d.y, sel_lo);  // (x2, x6)
+                q.w = __builtin_amdgcn_perm(d.w, d.y, sel_hi);  // (x3, x7)
+                b[c][s] = __builtin_bit_cast(bf16x8_t, q);
+                sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.x), as_bf16x2(ones), sm, false);
+                sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.y), as_bf16x2(ones), sm, false);
+                sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.z), as_bf16x2(ones), sm, false);
+                sm = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(d.w), as_bf16x2(ones), sm, false);
+            }
+            xs[c] = swap16_sum(swap32_sum(sm));
+        }
+        // every X read has returned once the sums exist
+        uint32_t xdone = __builtin_bit_cast(uint32_t, xs[0]);
+#pragma unroll
+        for (int c = 1; c < MT; ++c) xdone ^= __builtin_bit_cast(uint32_t, xs[c]);
+        issue_x(T + 1, xdone);
+        // Each tile's weights are read from LDS one tile ahead.  Tile rt's
+        // load was issued before the 6 - rt later tiles of this T-block, the
+        // next T-block's X (kXB) and the rt next-T-block tiles issued before
+        // the read: RT - 1 + kXB younger loads in every case.
+        wait_vmcnt<RT - 1 + kXB>();
+        u32x4 wv = *reinterpret_cast<const u32x4*>(wl + 16 * lane);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const bf16x8_t a0 = a_operand(wv.x, nk), a1 = a_operand(wv.y, nk);
+            const bf16x8_t a2 = a_operand(wv.z, nk), a3 = a_operand(wv.w, nk);
+            issue_w(rt, T + 1, __builtin_bit_cast(u32x4, a3).w ^ __builtin_bit_cast(u32x4, a0).x);
+            if (rt + 1 < RT) {
+                wait_vmcnt<RT - 1 + kXB>();
+                wv = *reinterpret_cast<const u32x4*>(wl + 1024 * (rt + 1) + 16 * lane);
+            }
+            const f32x4 s4 = *reinterpret_cast<const f32x4*>(cs + tt * kCS + 16 * rt + 4 * kb);
+            const f32x4 z4 = *reinterpret_cast<const f32x4*>(cz + tt * kCS + 16 * rt + 4 * kb);
+#pragma unroll
+            for (int c = 0; c < MT; ++c) {
+                f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[c][0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[c][1], d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[c][2], d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b[c][3], d, 0, 0, 0);
+                f32x4& a = acc[rt][c];
+                a.x = fmaf(s4.x, d.x, fmaf(z4.x, xs[c], a.x));
+                a.y = fmaf(s4.y, d.y, fmaf(z4.y, xs[c], a.y));
+                a.z = fmaf(s4.z, d.z, fmaf(z4.z, xs[c], a.z));
+                a.w = fmaf(s4.w, d.w, fmaf(z4.w, xs[c], a.w));
+            }
+            // one weight tile at a time (register demand)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // Sum the four K parts of every output tile through LDS, as in
+    // gemm_int4_kslice_kernel, once the last loads into LDS have landed.
+    wait_vmcnt<0>();
+    __syncthreads();
+    f32x4* red = reinterpret_cast<f32x4*>(lds);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int c = 0; c < MT; ++c) red[((wave * RT + rt) * MT + c) * kWave + lane] = acc[rt][c];
+    __syncthreads();
+    for (int tile = wave; tile < RT * MT; tile += kKsWaves) {
+        const int rt = tile / MT, c = tile - rt * MT;
+        f32x4 v = red[(rt * MT + c) * kWave + lane];
+#pragma unroll
+        for (int w = 1; w < kKsWaves; ++w) {
+            const f32x4 o = red[((w * RT + rt) * MT + c) * kWave + lane];
+            v.x += o.x;
+            v.y += o.y;
+            v.z += o.z;
+            v.w += o.w;
+        }
+        const int m = 16 * c + i;
+        const int n0 = row_base + 16 * rt + 4 * kb;
+        if (m < M) {
+            const float vals[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (n0 + e < N) Y[static_cast<int64_t>(m) * N + n0 + e] = kc::f32_to_bf16(vals[e]);
+        }
+    }
+}
+
+// Returns -1 when the kernel does not apply (LDS or 32-bit offsets).
+template <int MT, bool SHUF>
+int launch_kslds(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
+                 const uint16_t* X, uint16_t* Y, int M, int N, int K, int gshift, hipStream_t stream) {
+    const size_t lds = kslds_lds_bytes<MT>(K / kTBlock);
+    if (lds > 160 * 1024 || static_cast<uint64_t>((N + 15) / 16) * 16 * (K / 2) >= (uint64_t{1} << 32) ||
+        static_cast<uint64_t>(M) * K * 2 >= (uint64_t{1} << 32))
+        return -1;
+    static bool attr_set = [] {
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_int4_kslds_kernel<MT, SHUF>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+    }();
+    if (!attr_set) return kc::set_error(KC_ERR_HIP, "%s: cannot raise the LDS limit", fn);
+    const unsigned grid = static_cast<unsigned>((N + 16 * kKlRT - 1) / (16 * kKlRT));
+    gemm_int4_kslds_kernel<MT, SHUF><<<grid, kKsWaves * kWave, lds, stream>>>(packed, scales, zeros, X, Y, M, N,
+                                                                               K, gshift);
+    return kc::check_launch(fn);
+}
+
+// ---------------------------------------------------------------------------
 // M = 1 on the shuffled layout: x is the A operand, the same 32 values in
 // every row of the 16 x 32 block (a broadcast), the weight tile the B
 // operand, so every row m of D = A B holds the 16 dot products and lane
@@ -1442,13 +1742,21 @@ int gemm_int4(const char* fn, const uint8_t* d_packed, const float* d_scales,
             return launch_xres<kXresW, kXresD, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols,
                                                gshift, P, stream);
     }
-    // M 9..64: the K-split kernel (K 8192, N 28672, MI355X: M 16 / 32 / 48 /
-    // 64 in 37 / 47 / 57 / 68 us, against 41 / 77 / 95 / 101 us for the
-    // kernels below, which remain for shapes it does not take: K above about
-    // 20000, where its coefficient stage does not fit in LDS, or operands of
-    // 4 GiB).
+    // M 9..64: the K-split kernels, operands through LDS where they fit,
+    // else through registers (K 8192, N 28672, MI355X, reference layout:
+    // M 16 / 32 / 48 / 64 in 34 / 40 / 48 / 59 us through LDS, 37 / 48 / 58 /
+    // 69 us through registers, 41 / 77 / 95 / 101 us for the kernels below,
+    // which remain for shapes neither takes: K above about 20000, where the
+    // coefficient stage does not fit in LDS, or operands of 4 GiB).
     if (m > kXresBestM) {
         int st = -1;
+        switch ((m + 15) / 16) {
+            case 1: st = launch_kslds<1, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+            case 2: st = launch_kslds<2, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+            case 3: st = launch_kslds<3, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+            default: st = launch_kslds<4, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+        }
+        if (st >= 0) return st;
         switch ((m + 15) / 16) {
             case 1: st = launch_kslice<1, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
             case 2: st = launch_kslice<2, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
