@@ -50,6 +50,7 @@
 // Each B operand read from LDS serves RT row tiles, each decoded A operand
 // MT activation tiles.
 #include <algorithm>
+#include <type_traits>
 
 #include "kc_common.hpp"
 
@@ -1227,19 +1228,20 @@ int launch_kslice(const char* fn, const uint8_t* packed, const float* scales, co
 //     four rows, each block one load instruction that reads its 1 KB in one
 //     piece (the register kernel's B-operand loads touch 32 cache lines per
 //     instruction).  Lane l of block j carries chunk u of local row
-//     r = l / 16, u = (l - 2 r - (j & 1)) mod 16, so chunk u of row r sits in
-//     slot 16 r + ((u + 2 r + (j & 1)) mod 16): a B-operand read (lane
-//     (i, kb), step s: chunk 4 kb + s of row 16 c + i) gives every eight
-//     consecutive lanes eight different 16-byte bank groups.
+//     r = l / 16, u = (l - 4 (j mod 4) - r) mod 16, so chunk u of row r sits
+//     in slot 16 r + ((u + 4 (j mod 4) + r) mod 16): a B-operand read (lane
+//     (i, kb), step s: chunk 4 kb + s of row 16 c + i, rotated by i) gives
+//     the 16 lanes of each kb 16 different 16-byte bank groups.
 //   * W: per T-block and row tile the wave-wide 1-KB load of the register
 //     kernel, lane l's 16 bytes in slot l.
 // One T-block of each is resident per wave.  X of the next T-block is
 // requested once the current one has been read out, each row tile's next
 // weights right after that tile's decode, so every load has about one
-// T-block to arrive.  The waits are explicit (loads complete in order:
-// vmcnt(7) before X, vmcnt(22) before each weight tile, counting the loads
-// issued since).  With no operand ring in registers, the accumulators, the
-// B operands and the matrix-core results fit the 256 VGPRs.
+// T-block to arrive; the last T-block requests nothing.  The waits are
+// explicit (loads complete in order: vmcnt(7) before X, vmcnt(22) before
+// each weight tile, counting the loads issued since).  With no operand ring
+// in registers, the accumulators, the B operands and the matrix-core results
+// fit the 256 VGPRs.
 // ---------------------------------------------------------------------------
 constexpr int kKlRT = 7;
 // Coefficient table row stride: 112 rows padded to 116 floats, so that the
@@ -1266,6 +1268,20 @@ __device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// s_waitcnt vmcnt(n), n a constant once the caller's loop is unrolled.
+__device__ __forceinline__ void wait_vmcnt_n(int n) {
+    switch (n) {
+        case 0: wait_vmcnt<0>(); break;
+        case 1: wait_vmcnt<1>(); break;
+        case 2: wait_vmcnt<2>(); break;
+        case 3: wait_vmcnt<3>(); break;
+        case 4: wait_vmcnt<4>(); break;
+        case 5: wait_vmcnt<5>(); break;
+        case 6: wait_vmcnt<6>(); break;
+        default: wait_vmcnt<0>(); break;
+    }
 }
 
 // Per-wave LDS: X (4 MT KB), weights (RT KB), fold coefficients of the
@@ -1310,19 +1326,19 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
 
     // DMA offsets.  X block j, lane l: row 4 j + r (r = l / 16), chunk u.
     // Rows below 16 (MT - 1) exist (M > 16 (MT - 1)): blocks j < 4 MT - 4
-    // take lane offset xg[j & 1] and 8 K j bytes on the scalar base; the last
+    // take lane offset xg[j & 3] and 8 K j bytes on the scalar base; the last
     // tile's four blocks clamp their rows to M - 1 per lane (xe).
-    uint32_t xg[2], xe[4];
+    uint32_t xg[4], xe[4];
     {
         const int r = lane >> 4;
 #pragma unroll
-        for (int p = 0; p < 2; ++p)
-            xg[p] = static_cast<uint32_t>(r) * static_cast<uint32_t>(2 * K) + 16u * (((lane & 15) - 2 * r - p) & 15);
+        for (int q = 0; q < 4; ++q)
+            xg[q] = static_cast<uint32_t>(r) * static_cast<uint32_t>(2 * K) + 16u * (((lane & 15) - 4 * q - r) & 15);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int j = kXB - 4 + e;
-            const int u = ((lane & 15) - 2 * r - (j & 1)) & 15;
-            xe[e] = static_cast<uint32_t>(min(4 * j + r, M - 1)) * static_cast<uint32_t>(2 * K) + 16u * u;
+        for (int q = 0; q < 4; ++q) {
+            const int j = kXB - 4 + q;
+            xe[q] = static_cast<uint32_t>(min(4 * j + r, M - 1)) * static_cast<uint32_t>(2 * K) +
+                    16u * (((lane & 15) - 4 * q - r) & 15);
         }
     }
     uint32_t woff[RT];
@@ -1335,7 +1351,7 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
         const uint8_t* base = xbytes + 256 * min(T, tl);
 #pragma unroll
         for (int j = 0; j < kXB - 4; ++j)
-            dma16(xg[j & 1], base + static_cast<size_t>(8 * j) * K, x_lds + 1024 * j, after);
+            dma16(xg[j & 3], base + static_cast<size_t>(8 * j) * K, x_lds + 1024 * j, after);
 #pragma unroll
         for (int e = 0; e < 4; ++e) dma16(xe[e], base, x_lds + 1024 * (kXB - 4 + e), after);
     };
@@ -1343,21 +1359,103 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
         dma16(woff[rt], packed + 16 * kTStep<SHUF> * min(T, tl), w_lds + 1024 * rt, after);
     };
     // B-operand read offsets: lane (i, kb), step s reads chunk 4 kb + s of
-    // row 16 c + i (block 4 c + i / 4, local row i % 4) at xrd[s] + 4096 c.
+    // row 16 c + i (block 4 c + i / 4, local row i % 4, rotation
+    // 4 (i / 4) + i % 4 = i) at xrd[s] + 4096 c.
     uint32_t xrd[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        const int r = i & 3, j1 = (i >> 2) & 1;
-        xrd[s] = 1024u * (i >> 2) + 256u * r + 16u * ((4 * kb + s + 2 * r + j1) & 15);
-    }
+    for (int s = 0; s < 4; ++s) xrd[s] = 1024u * (i >> 2) + 256u * (i & 3) + 16u * ((4 * kb + s + i) & 15);
 
-    issue_x(t0, 0u);
+    auto issue_first = [&]() {
+        issue_x(t0, 0u);
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) issue_w(rt, t0, 0u);
+        for (int rt = 0; rt < RT; ++rt) issue_w(rt, t0, 0u);
+    };
 
     // Fold coefficients of this wave's K range, cs[t][row] = s and
-    // cz[t][row] = -s (136 + z), as in gemm_int4_kslice_kernel.
-    {
+    // cz[t][row] = -s (136 + z).
+    //
+    // One group per T-block, whole quads of T-blocks and aligned tables (the
+    // usual case, e.g. K 8192 with groups of 128): lane item (row, quad q)
+    // reads the four scales of T-blocks 4 q .. 4 q + 3 with one 16-byte load
+    // and their four zero points with one 2-byte load; the first pass (all of
+    // a 16-T-block quarter) is requested before this T-block's operand loads
+    // and waited for with them still in flight.  Otherwise one item per
+    // (row, T-block), as in gemm_int4_kslice_kernel.
+    const bool quad = gshift == 0 && (nT & 15) == 0 && (reinterpret_cast<uintptr_t>(scales) & 15) == 0 &&
+                      (reinterpret_cast<uintptr_t>(zeros) & 1) == 0;
+    if (quad) {
+        constexpr int kQB = 7;  // 112 rows x 4 quads in one pass
+        const int nq = nt >> 2;
+        const int items = kRows * nq;
+        const float inv_nq = 1.0f / static_cast<float>(max(nq, 1));
+        const float* srow = scales + static_cast<size_t>(row_base) * G + t0;
+        const uint8_t* zrow = zeros + static_cast<size_t>(row_base) * (G >> 1) + (t0 >> 1);
+        auto item = [&](int idx, int& r, int& q) {
+            r = static_cast<int>((static_cast<float>(idx) + 0.5f) * inv_nq);
+            q = idx - r * nq;
+        };
+        auto store = [&](int base, const u32x4 (&sq)[kQB], const uint32_t (&zq)[kQB]) {
+#pragma unroll
+            for (int b = 0; b < kQB; ++b) {
+                const int idx = base + b * kWave + lane;
+                if (idx < items) {
+                    int r, q;
+                    item(idx, r, q);
+                    // the whole vector is cast: this compiler reads component 0
+                    // for a bit cast of any single component of an ext-vector
+                    const f32x4 sf = __builtin_bit_cast(f32x4, sq[b]);
+                    const float sv[4] = {sf.x, sf.y, sf.z, sf.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t z = (zq[b] >> (4 * e)) & 0xFu;
+                        cs[(4 * q + e) * kCS + r] = sv[e];
+                        cz[(4 * q + e) * kCS + r] = -sv[e] * static_cast<float>(136u + z);
+                    }
+                }
+            }
+        };
+        // 32-bit offsets from the workgroup's first row (rows past N - 1 read row N - 1)
+        auto offsets = [&](int base, int b, uint32_t& so, uint32_t& zo) {
+            int r, q;
+            item(min(base + b * kWave + lane, items - 1), r, q);
+            const uint32_t rr = static_cast<uint32_t>(min(row_base + r, N - 1) - row_base);
+            so = (rr * static_cast<uint32_t>(G) + 4u * q) * 4u;
+            zo = rr * static_cast<uint32_t>(G >> 1) + 2u * q;
+        };
+        {
+            u32x4 sq[kQB];
+            uint32_t zq[kQB];
+#pragma unroll
+            for (int b = 0; b < kQB; ++b) {
+                uint32_t so, zo;
+                offsets(0, b, so, zo);
+                asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(sq[b]) : "v"(so), "s"(srow));
+                asm volatile("global_load_ushort %0, %1, %2" : "=v"(zq[b]) : "v"(zo), "s"(zrow));
+            }
+            issue_first();
+            // the 2 kQB loads above have landed once only this T-block's
+            // kXB + RT operand loads can remain
+            asm volatile("s_waitcnt vmcnt(%14)"
+                         : "+v"(sq[0]), "+v"(sq[1]), "+v"(sq[2]), "+v"(sq[3]), "+v"(sq[4]), "+v"(sq[5]), "+v"(sq[6]),
+                           "+v"(zq[0]), "+v"(zq[1]), "+v"(zq[2]), "+v"(zq[3]), "+v"(zq[4]), "+v"(zq[5]), "+v"(zq[6])
+                         : "n"(kXB + RT)
+                         : "memory");
+            store(0, sq, zq);
+        }
+        for (int base = kQB * kWave; base < items; base += kQB * kWave) {
+            u32x4 sq[kQB];
+            uint32_t zq[kQB];
+#pragma unroll
+            for (int b = 0; b < kQB; ++b) {
+                uint32_t so, zo;
+                offsets(base, b, so, zo);
+                sq[b] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(srow) + so);
+                zq[b] = *reinterpret_cast<const uint16_t*>(zrow + zo);
+            }
+            store(base, sq, zq);
+        }
+    } else {
+        issue_first();
         constexpr int kBatch = 28;  // 16 T-blocks x 112 rows in one pass
         const int items = nt * kRows;
         const float inv_nt = 1.0f / static_cast<float>(max(nt, 1));
@@ -1399,10 +1497,21 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
 #pragma unroll
         for (int c = 0; c < MT; ++c) acc[rt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int T = t0; T < t1; ++T) {
+    // One T-block; the last one issues no loads for a next one, so its
+    // waits count only its own remaining weight tiles.
+    auto tblock = [&](int T, auto last_tag) {
+        constexpr bool kLast = decltype(last_tag)::value;
         const int tt = T - t0;
         // X of this T-block: issued before the 7 weight loads of this T-block
         wait_vmcnt<RT>();
+        // all X reads in flight at once (the previous T-block's B operands
+        // are dead), then the permutation and sums as they return
+        u32x4 xr[MT][4];
+#pragma unroll
+        for (int c = 0; c < MT; ++c)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) xr[c][s] = *reinterpret_cast<const u32x4*>(xl + xrd[s] + 4096 * c);
+        __builtin_amdgcn_sched_barrier(0);
         bf16x8_t b[MT][4];
         float xs[MT];
 #pragma unroll
@@ -1410,7 +1519,7 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
             float sm = 0.0f;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                const u32x4 d = *reinterpret_cast<const u32x4*>(xl + xrd[s] + 4096 * c);
+                const u32x4 d = xr[c][s];
                 u32x4 q;
                 q.x = __builtin_amdgcn_perm(d.z, d.x, sel_lo);  // (x0, x4)
                 q.y = __builtin_amdgcn_perm(d.z, d.x, sel_hi);  // (x1, x5)
@@ -1424,24 +1533,29 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
             }
             xs[c] = swap16_sum(swap32_sum(sm));
         }
-        // every X read has returned once the sums exist
-        uint32_t xdone = __builtin_bit_cast(uint32_t, xs[0]);
+        if constexpr (!kLast) {
+            // every X read has returned once the sums exist
+            uint32_t xdone = __builtin_bit_cast(uint32_t, xs[0]);
 #pragma unroll
-        for (int c = 1; c < MT; ++c) xdone ^= __builtin_bit_cast(uint32_t, xs[c]);
-        issue_x(T + 1, xdone);
+            for (int c = 1; c < MT; ++c) xdone ^= __builtin_bit_cast(uint32_t, xs[c]);
+            issue_x(T + 1, xdone);
+        }
         // Each tile's weights are read from LDS one tile ahead.  Tile rt's
-        // load was issued before the 6 - rt later tiles of this T-block, the
-        // next T-block's X (kXB) and the rt next-T-block tiles issued before
-        // the read: RT - 1 + kXB younger loads in every case.
-        wait_vmcnt<RT - 1 + kXB>();
+        // load was issued before the 6 - rt later tiles of this T-block and,
+        // unless this is the last T-block, the next T-block's X (kXB) and the
+        // rt next-T-block tiles issued before the read: RT - 1 + kXB younger
+        // loads, or RT - 1 - rt in the last T-block.
+        if constexpr (kLast) wait_vmcnt<RT - 1>();
+        else wait_vmcnt<RT - 1 + kXB>();
         u32x4 wv = *reinterpret_cast<const u32x4*>(wl + 16 * lane);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             const bf16x8_t a0 = a_operand(wv.x, nk), a1 = a_operand(wv.y, nk);
             const bf16x8_t a2 = a_operand(wv.z, nk), a3 = a_operand(wv.w, nk);
-            issue_w(rt, T + 1, __builtin_bit_cast(u32x4, a3).w ^ __builtin_bit_cast(u32x4, a0).x);
+            if constexpr (!kLast) issue_w(rt, T + 1, __builtin_bit_cast(u32x4, a3).w ^ __builtin_bit_cast(u32x4, a0).x);
             if (rt + 1 < RT) {
-                wait_vmcnt<RT - 1 + kXB>();
+                if constexpr (kLast) wait_vmcnt_n(RT - 2 - rt);
+                else wait_vmcnt<RT - 1 + kXB>();
                 wv = *reinterpret_cast<const u32x4*>(wl + 1024 * (rt + 1) + 16 * lane);
             }
             const f32x4 s4 = *reinterpret_cast<const f32x4*>(cs + tt * kCS + 16 * rt + 4 * kb);
@@ -1461,7 +1575,9 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
             // one weight tile at a time (register demand)
             __builtin_amdgcn_sched_barrier(0);
         }
-    }
+    };
+    for (int T = t0; T + 1 < t1; ++T) tblock(T, std::false_type{});
+    if (nt > 0) tblock(t1 - 1, std::true_type{});
 
     // Sum the four K parts of every output tile through LDS, as in
     // gemm_int4_kslice_kernel, once the last loads into LDS have landed.
@@ -1473,6 +1589,7 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
 #pragma unroll
         for (int c = 0; c < MT; ++c) red[((wave * RT + rt) * MT + c) * kWave + lane] = acc[rt][c];
     __syncthreads();
+    const bool y8 = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(Y) & 7) == 0;
     for (int tile = wave; tile < RT * MT; tile += kKsWaves) {
         const int rt = tile / MT, c = tile - rt * MT;
         f32x4 v = red[(rt * MT + c) * kWave + lane];
@@ -1487,10 +1604,18 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
         const int m = 16 * c + i;
         const int n0 = row_base + 16 * rt + 4 * kb;
         if (m < M) {
-            const float vals[4] = {v.x, v.y, v.z, v.w};
+            uint16_t* yp = Y + static_cast<int64_t>(m) * N + n0;
+            if (y8 && n0 + 3 < N) {
+                // four consecutive outputs, 8-byte aligned: one store
+                const uint32_t lo = kc::f32_to_bf16(v.x) | (static_cast<uint32_t>(kc::f32_to_bf16(v.y)) << 16);
+                const uint32_t hi = kc::f32_to_bf16(v.z) | (static_cast<uint32_t>(kc::f32_to_bf16(v.w)) << 16);
+                *reinterpret_cast<uint2*>(yp) = make_uint2(lo, hi);
+            } else {
+                const float vals[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (n0 + e < N) Y[static_cast<int64_t>(m) * N + n0 + e] = kc::f32_to_bf16(vals[e]);
+                for (int e = 0; e < 4; ++e)
+                    if (n0 + e < N) yp[e] = kc::f32_to_bf16(vals[e]);
+            }
         }
     }
 }
