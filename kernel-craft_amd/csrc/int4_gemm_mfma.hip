@@ -1241,7 +1241,9 @@ int launch_kslice(const char* fn, const uint8_t* packed, const float* scales, co
 // explicit (loads complete in order: vmcnt(7) before X, vmcnt(22) before
 // each weight tile, counting the loads issued since).  With no operand ring
 // in registers, the accumulators, the B operands and the matrix-core results
-// fit the 256 VGPRs.
+// fit the 256 VGPRs.  With three or four activation tiles the fold keeps only
+// its scale FMA per T-block; the zero-point terms of four T-blocks at a time
+// go through one fp32 MFMA (16 x 16 x 4) per output tile.
 // ---------------------------------------------------------------------------
 constexpr int kKlRT = 7;
 // Coefficient table row stride: 112 rows padded to 116 floats, so that the
@@ -1496,6 +1498,15 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int c = 0; c < MT; ++c) acc[rt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // With three or four activation tiles the zero-point half of the fold,
+    // cz[t][n] xs[t][m], is left to the fp32 matrix core, four T-blocks at a
+    // time: xsb[c] holds xs of T-block g0 + kb of the current group of four.
+    constexpr bool kZmf = MT >= 3;
+    float xsb[kZmf ? MT : 1];
+    if constexpr (kZmf) {
+#pragma unroll
+        for (int c = 0; c < MT; ++c) xsb[c] = 0.0f;
+    }
 
     // One T-block; the last one issues no loads for a next one, so its
     // waits count only its own remaining weight tiles.
@@ -1533,6 +1544,10 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
             }
             xs[c] = swap16_sum(swap32_sum(sm));
         }
+        if constexpr (kZmf) {
+#pragma unroll
+            for (int c = 0; c < MT; ++c) xsb[c] = kb == (tt & 3) ? xs[c] : xsb[c];
+        }
         if constexpr (!kLast) {
             // every X read has returned once the sums exist
             uint32_t xdone = __builtin_bit_cast(uint32_t, xs[0]);
@@ -1559,21 +1574,52 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
                 wv = *reinterpret_cast<const u32x4*>(wl + 1024 * (rt + 1) + 16 * lane);
             }
             const f32x4 s4 = *reinterpret_cast<const f32x4*>(cs + tt * kCS + 16 * rt + 4 * kb);
-            const f32x4 z4 = *reinterpret_cast<const f32x4*>(cz + tt * kCS + 16 * rt + 4 * kb);
+            if constexpr (kZmf) {
 #pragma unroll
-            for (int c = 0; c < MT; ++c) {
-                f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[c][0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[c][1], d, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[c][2], d, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b[c][3], d, 0, 0, 0);
-                f32x4& a = acc[rt][c];
-                a.x = fmaf(s4.x, d.x, fmaf(z4.x, xs[c], a.x));
-                a.y = fmaf(s4.y, d.y, fmaf(z4.y, xs[c], a.y));
-                a.z = fmaf(s4.z, d.z, fmaf(z4.z, xs[c], a.z));
-                a.w = fmaf(s4.w, d.w, fmaf(z4.w, xs[c], a.w));
+                for (int c = 0; c < MT; ++c) {
+                    f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[c][0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[c][1], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[c][2], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b[c][3], d, 0, 0, 0);
+                    f32x4& a = acc[rt][c];
+                    a.x = fmaf(s4.x, d.x, a.x);
+                    a.y = fmaf(s4.y, d.y, a.y);
+                    a.z = fmaf(s4.z, d.z, a.z);
+                    a.w = fmaf(s4.w, d.w, a.w);
+                }
+            } else {
+                const f32x4 z4 = *reinterpret_cast<const f32x4*>(cz + tt * kCS + 16 * rt + 4 * kb);
+#pragma unroll
+                for (int c = 0; c < MT; ++c) {
+                    f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[c][0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[c][1], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[c][2], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b[c][3], d, 0, 0, 0);
+                    f32x4& a = acc[rt][c];
+                    a.x = fmaf(s4.x, d.x, fmaf(z4.x, xs[c], a.x));
+                    a.y = fmaf(s4.y, d.y, fmaf(z4.y, xs[c], a.y));
+                    a.z = fmaf(s4.z, d.z, fmaf(z4.z, xs[c], a.z));
+                    a.w = fmaf(s4.w, d.w, fmaf(z4.w, xs[c], a.w));
+                }
             }
             // one weight tile at a time (register demand)
             __builtin_amdgcn_sched_barrier(0);
+        }
+        // zero points of the group of four T-blocks ending here, on the fp32
+        // matrix core: acc[n][m] += sum_kb cz[g0 + kb][n] xs[g0 + kb][m]
+        if constexpr (kZmf) {
+            if ((tt & 3) == 3 || kLast) {
+                const int g0 = tt & ~3;
+                const int tz = min(g0 + kb, nt - 1);  // lanes past the range hold xs = 0
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    const float av = cz[tz * kCS + 16 * rt + i];
+#pragma unroll
+                    for (int c = 0; c < MT; ++c) acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, xsb[c], acc[rt][c], 0, 0, 0);
+                }
+#pragma unroll
+                for (int c = 0; c < MT; ++c) xsb[c] = 0.0f;
+            }
         }
     };
     for (int T = t0; T + 1 < t1; ++T) tblock(T, std::false_type{});
