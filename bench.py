@@ -813,7 +813,7 @@ def main() -> int:
         r["TFLOPs"] = round(2.0 * m * n3 * k3 / (r["avg_us"] * 1e-6) / 1e12, 2)
         cfg3[f"M{m}"] = r
         log(f"# cfg3 MFMA GEMM M={m:2d}: {r['avg_us']} us, {r['GBps']} GB/s, {r['TFLOPs']} TFLOP/s")
-    # the same GEMMs on the pre-shuffled layout: bit-identical outputs
+    # the same GEMMs on the pre-shuffled layout
     c3s = []
     for p, _, _ in c3:
         sbuf = torch.empty(lib.kc_shuffled_int4_bytes(n3, k3), dtype=torch.uint8, device=dev)
@@ -836,7 +836,15 @@ def main() -> int:
                                  y3r.data_ptr(), m, n3, k3, GS, stream_ptr()), "kc_gemm_int4_bf16")
         launch_cfg3s(0)
         torch.cuda.synchronize()
-        if not torch.equal(y3.view(torch.int16), y3r.view(torch.int16)):
+        if m >= 9:
+            # the same kernels read both layouts: bit-identical outputs
+            same = torch.equal(y3.view(torch.int16), y3r.view(torch.int16))
+        else:
+            # M 2..8: the K-split kernel on the shuffled layout, the
+            # X-resident one on the reference layout (other summation orders)
+            a, b = y3.float(), y3r.float()
+            same = bool(torch.isfinite(a).all()) and float((a - b).norm() / b.norm()) < 1e-2
+        if not same:
             print(f"bench.py: shuffled-layout GEMM differs at M={m}", file=sys.stderr)
             return 1
         nbytes = w3_bytes + m * k3 * 2 + m * n3 * 2

@@ -26,13 +26,15 @@
 // per activation row.
 //
 // Kernels, by M (kc_gemm_int4_bf16 at the bottom picks one):
-//   M 2..8    gemm_int4_xres_kernel: X resident in LDS, one wave per 16-row
-//             weight tile over all of K;
-//   M 9..64   gemm_int4_kslds_kernel: K split over the four waves of a CU,
-//             X and the weights streamed into LDS by direct-to-LDS loads;
-//             gemm_int4_kslice_kernel (X from the cache into registers)
-//             where that kernel's LDS does not fit (K above 8192 at M > 16);
-//   fallbacks gemm_int4_xres_kernel (M 9..16), gemm_int4_xbig_kernel
+//   M 2..8    gemm_int4_xres_kernel (reference layout): X resident in LDS,
+//             one wave per 16-row weight tile over all of K;
+//   M 9..64   gemm_int4_kslds_kernel (M 2..64 on the shuffled layout): K
+//             split over the four waves of a CU, X and the weights streamed
+//             into LDS by direct-to-LDS loads; gemm_int4_kslice_kernel (X
+//             from the cache into registers) where that kernel's LDS does not
+//             fit (K above 16384 / 13824 / 11776 / 9216 at M <= 16 / 32 / 48
+//             / 64);
+//   fallbacks gemm_int4_xres_kernel (M 2..16), gemm_int4_xbig_kernel
 //             (M 33..64) and gemm_int4_mfma_kernel (below) when the K-split
 //             kernels' coefficients do not fit in LDS (K above about 20000).
 //
@@ -1905,9 +1907,12 @@ int gemm_int4(const char* fn, const uint8_t* d_packed, const float* d_scales,
         return KC_SUCCESS;
     }
     const int gshift = kc::ilog2(group_size) - 7;
-    // M <= 8: the X-resident kernel when its LDS fits in some number of
-    // phases of K.
-    if (m <= kXresBestM) {
+    // M <= 8 on the reference layout: the X-resident kernel when its LDS fits
+    // in some number of phases of K.  On the shuffled layout the K-split
+    // kernel below is faster from M = 2 (K 8192, N 28672: M 2 / 4 / 8 in
+    // 26.0 / 25.1 / 25.2 us against 27.5 / 27.3 / 28.2; on the reference
+    // layout 31.4 / 31.4 / 32.6 against 32.2 / 31.5 / 32.7, the same).
+    if (m <= kXresBestM && !SHUF) {
         const int P = xres_phases(m, cols, (cols / kTBlock) >> gshift);
         if (P > 0)
             return launch_xres<kXresW, kXresD, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols,
@@ -1919,7 +1924,7 @@ int gemm_int4(const char* fn, const uint8_t* d_packed, const float* d_scales,
     // 69 us through registers, 41 / 77 / 95 / 101 us for the kernels below,
     // which remain for shapes neither takes: K above about 20000, where the
     // coefficient stage does not fit in LDS, or operands of 4 GiB).
-    if (m > kXresBestM) {
+    if (m > kXresBestM || SHUF) {
         int st = -1;
         switch ((m + 15) / 16) {
             case 1: st = launch_kslds<1, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
