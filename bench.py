@@ -836,14 +836,9 @@ def main() -> int:
                                  y3r.data_ptr(), m, n3, k3, GS, stream_ptr()), "kc_gemm_int4_bf16")
         launch_cfg3s(0)
         torch.cuda.synchronize()
-        if m >= 9:
-            # the same kernels read both layouts: bit-identical outputs
-            same = torch.equal(y3.view(torch.int16), y3r.view(torch.int16))
-        else:
-            # M 2..8: the K-split kernel on the shuffled layout, the
-            # X-resident one on the reference layout (other summation orders)
-            a, b = y3.float(), y3r.float()
-            same = bool(torch.isfinite(a).all()) and float((a - b).norm() / b.norm()) < 1e-2
+        # the same K-split kernel reads both layouts at K 8192 (on the
+        # reference layout in pairs of T-blocks): bit-identical outputs
+        same = torch.equal(y3.view(torch.int16), y3r.view(torch.int16))
         if not same:
             print(f"bench.py: shuffled-layout GEMM differs at M={m}", file=sys.stderr)
             return 1

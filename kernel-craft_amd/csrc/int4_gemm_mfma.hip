@@ -26,14 +26,19 @@
 // per activation row.
 //
 // Kernels, by M (kc_gemm_int4_bf16 at the bottom picks one):
-//   M 2..8    gemm_int4_xres_kernel (reference layout): X resident in LDS,
-//             one wave per 16-row weight tile over all of K;
-//   M 9..64   gemm_int4_kslds_kernel (M 2..64 on the shuffled layout): K
-//             split over the four waves of a CU, X and the weights streamed
-//             into LDS by direct-to-LDS loads; gemm_int4_kslice_kernel (X
-//             from the cache into registers) where that kernel's LDS does not
-//             fit (K above 16384 / 13824 / 11776 / 9216 at M <= 16 / 32 / 48
-//             / 64);
+//   M 2..64   gemm_int4_kslds_kernel: K split over the four waves of a CU, X
+//             and the weights streamed into LDS by direct-to-LDS loads; on
+//             the reference layout at M <= 32 with K a multiple of 1024 the
+//             weights come in pairs of T-blocks (whole 128-byte rows; K up to
+//             12288 at M <= 16, 9216 at M <= 32), otherwise one T-block at a
+//             time (K up to 16384 / 13824 / 11776 / 9216 at M <= 16 / 32 /
+//             48 / 64), and on the reference layout at M <= 8 only in the
+//             pair form;
+//   M 2..8    gemm_int4_xres_kernel (reference layout, where the pair form
+//             does not apply): X resident in LDS, one wave per 16-row weight
+//             tile over all of K;
+//   M 9..64   gemm_int4_kslice_kernel (X from the cache into registers)
+//             where gemm_int4_kslds_kernel's LDS does not fit;
 //   fallbacks gemm_int4_xres_kernel (M 2..16), gemm_int4_xbig_kernel
 //             (M 33..64) and gemm_int4_mfma_kernel (below) when the K-split
 //             kernels' coefficients do not fit in LDS (K above about 20000).
@@ -1235,8 +1240,15 @@ int launch_kslice(const char* fn, const uint8_t* packed, const float* scales, co
 //     (i, kb), step s: chunk 4 kb + s of row 16 c + i, rotated by i) gives
 //     the 16 lanes of each kb 16 different 16-byte bank groups.
 //   * W: per T-block and row tile the wave-wide 1-KB load of the register
-//     kernel, lane l's 16 bytes in slot l.
-// One T-block of each is resident per wave.  X of the next T-block is
+//     kernel, lane l's 16 bytes in slot l.  On the reference layout that
+//     load reads 64 bytes from each of 16 rows, and 16 neighbouring lanes
+//     touch 16 cache lines; with K a multiple of 1024 (and the LDS for
+//     2-KB slots, M <= 32) the weights instead come per pair of T-blocks,
+//     two loads per tile of 8 whole 128-byte rows each (8 lanes per row).
+//     The first T-block of the pair reads both halves of every tile and
+//     keeps the second T-block's in registers; it then requests the next
+//     pair's rows 0-7 of the tile and the second T-block its rows 8-15.
+// One T-block (pair) of each is resident per wave.  X of the next T-block is
 // requested once the current one has been read out, each row tile's next
 // weights right after that tile's decode, so every load has about one
 // T-block to arrive; the last T-block requests nothing.  The waits are
@@ -1284,25 +1296,48 @@ __device__ __forceinline__ void wait_vmcnt_n(int n) {
         case 4: wait_vmcnt<4>(); break;
         case 5: wait_vmcnt<5>(); break;
         case 6: wait_vmcnt<6>(); break;
+        case 7: wait_vmcnt<7>(); break;
+        case 8: wait_vmcnt<8>(); break;
+        case 9: wait_vmcnt<9>(); break;
+        case 10: wait_vmcnt<10>(); break;
+        case 11: wait_vmcnt<11>(); break;
+        case 12: wait_vmcnt<12>(); break;
+        case 13: wait_vmcnt<13>(); break;
+        case 14: wait_vmcnt<14>(); break;
+        case 15: wait_vmcnt<15>(); break;
+        case 16: wait_vmcnt<16>(); break;
+        case 17: wait_vmcnt<17>(); break;
+        case 18: wait_vmcnt<18>(); break;
+        case 19: wait_vmcnt<19>(); break;
+        case 20: wait_vmcnt<20>(); break;
+        case 21: wait_vmcnt<21>(); break;
+        case 22: wait_vmcnt<22>(); break;
+        case 23: wait_vmcnt<23>(); break;
+        case 24: wait_vmcnt<24>(); break;
+        case 25: wait_vmcnt<25>(); break;
+        case 26: wait_vmcnt<26>(); break;
+        case 27: wait_vmcnt<27>(); break;
         default: wait_vmcnt<0>(); break;
     }
 }
 
-// Per-wave LDS: X (4 MT KB), weights (RT KB), fold coefficients of the
-// wave's quarter (ceil(nT / 4) T-blocks x kKlCS x (s, c2)).
-template <int MT>
+// Per-wave LDS: X (4 MT KB), weights (RT KB, or 2 RT KB for a pair of
+// T-blocks), fold coefficients of the wave's quarter (ceil(nT / 4) T-blocks
+// x kKlCS x (s, c2)).
+template <int MT, bool PAIR>
 __host__ __device__ constexpr size_t kslds_wave_bytes(int nT) {
-    return static_cast<size_t>(4 * MT + kKlRT) * 1024 + static_cast<size_t>((nT + kKsWaves - 1) / kKsWaves) * kKlCS * 8;
+    return static_cast<size_t>(4 * MT + (PAIR ? 2 : 1) * kKlRT) * 1024 +
+           static_cast<size_t>((nT + kKsWaves - 1) / kKsWaves) * kKlCS * 8;
 }
 
-template <int MT>
+template <int MT, bool PAIR>
 __host__ __device__ constexpr size_t kslds_lds_bytes(int nT) {
-    const size_t ops = kKsWaves * kslds_wave_bytes<MT>(nT);
+    const size_t ops = kKsWaves * kslds_wave_bytes<MT, PAIR>(nT);
     const size_t red = static_cast<size_t>(kKsWaves) * kKlRT * MT * kWave * 16;
     return ops > red ? ops : red;
 }
 
-template <int MT, bool SHUF>
+template <int MT, bool SHUF, bool PAIR>
 __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
     const uint8_t* __restrict__ packed, const float* __restrict__ scales,
     const uint8_t* __restrict__ zeros, const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
@@ -1322,9 +1357,9 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
     const int nt = t1 - t0;  // 0 for some waves when nT < 4
     const int tl = max(t1 - 1, 0);
     const int row_base = blockIdx.x * kRows;
-    char* xl = lds + static_cast<size_t>(wave) * kslds_wave_bytes<MT>(nT);
+    char* xl = lds + static_cast<size_t>(wave) * kslds_wave_bytes<MT, PAIR>(nT);
     char* wl = xl + kXB * 1024;
-    float* cs = reinterpret_cast<float*>(wl + RT * 1024);
+    float* cs = reinterpret_cast<float*>(wl + (PAIR ? 2 : 1) * RT * 1024);
     float* cz = cs + ntmax * kCS;
     const uint32_t x_lds = lds_addr(xl), w_lds = lds_addr(wl);
 
@@ -1346,10 +1381,29 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
         }
     }
     uint32_t woff[RT];
+    if constexpr (!PAIR) {
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-        woff[rt] = SHUF ? static_cast<uint32_t>(min(row_base / 16 + rt, (N + 15) / 16 - 1)) * static_cast<uint32_t>(nT * 1024) + 16u * lane
-                        : static_cast<uint32_t>(min(row_base + 16 * rt + i, N - 1)) * static_cast<uint32_t>(K >> 1) + 16u * kb;
+        for (int rt = 0; rt < RT; ++rt)
+            woff[rt] = SHUF ? static_cast<uint32_t>(min(row_base / 16 + rt, (N + 15) / 16 - 1)) * static_cast<uint32_t>(nT * 1024) + 16u * lane
+                            : static_cast<uint32_t>(min(row_base + 16 * rt + i, N - 1)) * static_cast<uint32_t>(K >> 1) + 16u * kb;
+    }
+    // Pairs of T-blocks (reference layout): tile rt's 16 rows x 128 bytes
+    // (T-blocks 2 p and 2 p + 1) in two loads of 8 whole rows, h = 0 / 1 for
+    // rows 8 h .. 8 h + 7.  Lane l = 8 r + pos of load h carries chunk
+    // c = (pos - (r xor h)) mod 8 of row 8 h + r into slot
+    // 2048 rt + 1024 h + 16 l, so chunk c of that row sits at position
+    // (c + (r xor h)) mod 8 of its 128 bytes: the 16 rows of one chunk fall
+    // in 16 different 16-byte bank groups, each 8 of them in 8.
+    uint32_t woffp[PAIR ? RT : 1][2];
+    if constexpr (PAIR) {
+        const int r = lane >> 3, pos = lane & 7;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                woffp[rt][h] = static_cast<uint32_t>(min(row_base + 16 * rt + 8 * h + r, N - 1)) * static_cast<uint32_t>(K >> 1) +
+                               16u * static_cast<uint32_t>((pos - (r ^ h)) & 7);
+    }
     const uint8_t* xbytes = reinterpret_cast<const uint8_t*>(X);
     auto issue_x = [&](int T, uint32_t after) {
         const uint8_t* base = xbytes + 256 * min(T, tl);
@@ -1362,6 +1416,23 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
     auto issue_w = [&](int rt, int T, uint32_t after) {
         dma16(woff[rt], packed + 16 * kTStep<SHUF> * min(T, tl), w_lds + 1024 * rt, after);
     };
+    // load h of tile rt for the pair of T-blocks 2 p, 2 p + 1
+    auto issue_wh = [&](int rt, int p, int h, uint32_t after) {
+        dma16(woffp[rt][h], packed + 128 * min(p, tl >> 1), w_lds + 2048 * rt + 1024 * h, after);
+    };
+    auto issue_wp = [&](int rt, int p, uint32_t after) {
+        issue_wh(rt, p, 0, after);
+        issue_wh(rt, p, 1, after);
+    };
+    // A-operand read offsets in a pair slot: lane (i, kb) of T-block parity t
+    // reads chunk 4 t + kb of row i (h = i / 8, r = i % 8).
+    uint32_t wrd[PAIR ? 2 : 1];
+    if constexpr (PAIR) {
+        const int h = i >> 3, r = i & 7;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+            wrd[t] = 1024u * h + 16u * static_cast<uint32_t>(8 * r + ((4 * t + kb + (r ^ h)) & 7));
+    }
     // B-operand read offsets: lane (i, kb), step s reads chunk 4 kb + s of
     // row 16 c + i (block 4 c + i / 4, local row i % 4, rotation
     // 4 (i / 4) + i % 4 = i) at xrd[s] + 4096 c.
@@ -1369,10 +1440,14 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
 #pragma unroll
     for (int s = 0; s < 4; ++s) xrd[s] = 1024u * (i >> 2) + 256u * (i & 3) + 16u * ((4 * kb + s + i) & 15);
 
+    constexpr int kWL = (PAIR ? 2 : 1) * RT;  // weight loads per T-block, per pair when PAIR
     auto issue_first = [&]() {
         issue_x(t0, 0u);
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) issue_w(rt, t0, 0u);
+        for (int rt = 0; rt < RT; ++rt) {
+            if constexpr (PAIR) issue_wp(rt, t0 >> 1, 0u);
+            else issue_w(rt, t0, 0u);
+        }
     };
 
     // Fold coefficients of this wave's K range, cs[t][row] = s and
@@ -1438,11 +1513,11 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
             }
             issue_first();
             // the 2 kQB loads above have landed once only this T-block's
-            // kXB + RT operand loads can remain
+            // kXB + kWL operand loads can remain
             asm volatile("s_waitcnt vmcnt(%14)"
                          : "+v"(sq[0]), "+v"(sq[1]), "+v"(sq[2]), "+v"(sq[3]), "+v"(sq[4]), "+v"(sq[5]), "+v"(sq[6]),
                            "+v"(zq[0]), "+v"(zq[1]), "+v"(zq[2]), "+v"(zq[3]), "+v"(zq[4]), "+v"(zq[5]), "+v"(zq[6])
-                         : "n"(kXB + RT)
+                         : "n"(kXB + kWL)
                          : "memory");
             store(0, sq, zq);
         }
@@ -1510,13 +1585,35 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
         for (int c = 0; c < MT; ++c) xsb[c] = 0.0f;
     }
 
+    // Pairs of T-blocks: the first T-block of a pair reads both halves of
+    // every tile and keeps the second T-block's half here, so the slot is
+    // free once it has been read: the first T-block requests the next pair's
+    // rows 0-7 of the tile, the second T-block its rows 8-15 (seven loads per
+    // T-block, each with one or two T-blocks to arrive), and the second
+    // T-block reads no weights from LDS.
+    u32x4 wv1[PAIR ? RT : 1];
+
     // One T-block; the last one issues no loads for a next one, so its
-    // waits count only its own remaining weight tiles.
-    auto tblock = [&](int T, auto last_tag) {
+    // waits count only its own remaining weight tiles.  kPar < 0: one
+    // T-block per weight slot; else bit 0: second T-block of a pair, bit 1:
+    // the first pair (the prologue's loads), bit 2: the last pair (no
+    // weights for a next pair).
+    auto tblock = [&](int T, auto last_tag, auto par_tag) {
         constexpr bool kLast = decltype(last_tag)::value;
+        constexpr int kPar = decltype(par_tag)::value;
+        constexpr bool kPair = kPar >= 0;
+        constexpr bool kSecond = kPair && (kPar & 1) != 0;
+        constexpr bool kFirstPair = kPair && (kPar & 2) != 0;
+        constexpr bool kLastPair = kPair && (kPar & 4) != 0;
+        constexpr bool kEnd = kPair ? kSecond && kLastPair : kLast;  // no X for a next T-block
         const int tt = T - t0;
-        // X of this T-block: issued before the 7 weight loads of this T-block
-        wait_vmcnt<RT>();
+        // X of this T-block: issued before the 7 weight loads of this
+        // T-block (in a pair, the previous T-block's 7), the prologue's 14,
+        // or none (second T-block of the last pair).
+        if constexpr (!kPair) wait_vmcnt<RT>();
+        else if constexpr (!kSecond && kFirstPair) wait_vmcnt<2 * RT>();
+        else if constexpr (kSecond && kLastPair) wait_vmcnt<0>();
+        else wait_vmcnt<RT>();
         // all X reads in flight at once (the previous T-block's B operands
         // are dead), then the permutation and sums as they return
         u32x4 xr[MT][4];
@@ -1550,7 +1647,7 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
 #pragma unroll
             for (int c = 0; c < MT; ++c) xsb[c] = kb == (tt & 3) ? xs[c] : xsb[c];
         }
-        if constexpr (!kLast) {
+        if constexpr (!kEnd) {
             // every X read has returned once the sums exist
             uint32_t xdone = __builtin_bit_cast(uint32_t, xs[0]);
 #pragma unroll
@@ -1562,18 +1659,52 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
         // unless this is the last T-block, the next T-block's X (kXB) and the
         // rt next-T-block tiles issued before the read: RT - 1 + kXB younger
         // loads, or RT - 1 - rt in the last T-block.
-        if constexpr (kLast) wait_vmcnt<RT - 1>();
-        else wait_vmcnt<RT - 1 + kXB>();
-        u32x4 wv = *reinterpret_cast<const u32x4*>(wl + 16 * lane);
+        // In a pair, tile rt's rows 8-15 were followed by the rows 8-15 of
+        // the 6 - rt later tiles (the rows 0-7 and 8-15 of each, in the
+        // prologue's first pair), the kXB of X(T + 1) and the rows 0-7 of
+        // the next pair's tiles requested so far.
+        u32x4 wv;
+        if constexpr (!kPair) {
+            if constexpr (kLast) wait_vmcnt<RT - 1>();
+            else wait_vmcnt<RT - 1 + kXB>();
+            wv = *reinterpret_cast<const u32x4*>(wl + 16 * lane);
+        } else if constexpr (!kSecond) {
+            if constexpr (kFirstPair) wait_vmcnt<2 * (RT - 1) + kXB>();
+            else wait_vmcnt<RT - 1 + kXB>();
+            wv = *reinterpret_cast<const u32x4*>(wl + wrd[0]);
+            wv1[0] = *reinterpret_cast<const u32x4*>(wl + wrd[1]);
+        } else {
+            wv = wv1[0];
+        }
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             const bf16x8_t a0 = a_operand(wv.x, nk), a1 = a_operand(wv.y, nk);
             const bf16x8_t a2 = a_operand(wv.z, nk), a3 = a_operand(wv.w, nk);
-            if constexpr (!kLast) issue_w(rt, T + 1, __builtin_bit_cast(u32x4, a3).w ^ __builtin_bit_cast(u32x4, a0).x);
-            if (rt + 1 < RT) {
-                if constexpr (kLast) wait_vmcnt_n(RT - 2 - rt);
-                else wait_vmcnt<RT - 1 + kXB>();
-                wv = *reinterpret_cast<const u32x4*>(wl + 1024 * (rt + 1) + 16 * lane);
+            if constexpr (!kPair) {
+                if constexpr (!kLast) issue_w(rt, T + 1, __builtin_bit_cast(u32x4, a3).w ^ __builtin_bit_cast(u32x4, a0).x);
+                if (rt + 1 < RT) {
+                    if constexpr (kLast) wait_vmcnt_n(RT - 2 - rt);
+                    else wait_vmcnt<RT - 1 + kXB>();
+                    wv = *reinterpret_cast<const u32x4*>(wl + 1024 * (rt + 1) + 16 * lane);
+                }
+            } else if constexpr (!kSecond) {
+                // both halves of slot rt have been read: the next pair's rows
+                // 0-7 of the tile
+                if constexpr (!kLastPair)
+                    issue_wh(rt, (T >> 1) + 1, 0,
+                             __builtin_bit_cast(u32x4, a3).w ^ __builtin_bit_cast(u32x4, a0).x ^ wv1[rt].x);
+                if (rt + 1 < RT) {
+                    constexpr int kNext = kLastPair ? 0 : 1;
+                    if constexpr (kFirstPair) wait_vmcnt_n(kXB + 2 * (RT - 2 - rt) + kNext * (rt + 1));
+                    else wait_vmcnt_n(kXB + (RT - 2 - rt) + kNext * (rt + 1));
+                    wv = *reinterpret_cast<const u32x4*>(wl + 2048 * (rt + 1) + wrd[0]);
+                    wv1[rt + 1] = *reinterpret_cast<const u32x4*>(wl + 2048 * (rt + 1) + wrd[1]);
+                }
+            } else {
+                // the next pair's rows 8-15 of tile rt
+                if constexpr (!kLastPair)
+                    issue_wh(rt, (T >> 1) + 1, 1, __builtin_bit_cast(u32x4, a3).w ^ __builtin_bit_cast(u32x4, a0).x);
+                if (rt + 1 < RT) wv = wv1[rt + 1];
             }
             const f32x4 s4 = *reinterpret_cast<const f32x4*>(cs + tt * kCS + 16 * rt + 4 * kb);
             if constexpr (kZmf) {
@@ -1610,7 +1741,7 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
         // zero points of the group of four T-blocks ending here, on the fp32
         // matrix core: acc[n][m] += sum_kb cz[g0 + kb][n] xs[g0 + kb][m]
         if constexpr (kZmf) {
-            if ((tt & 3) == 3 || kLast) {
+            if ((tt & 3) == 3 || kEnd) {
                 const int g0 = tt & ~3;
                 const int tz = min(g0 + kb, nt - 1);  // lanes past the range hold xs = 0
 #pragma unroll
@@ -1624,8 +1755,33 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
             }
         }
     };
-    for (int T = t0; T + 1 < t1; ++T) tblock(T, std::false_type{});
-    if (nt > 0) tblock(t1 - 1, std::true_type{});
+    if constexpr (PAIR) {
+        // t0 and nt even, nt >= 2 (the launch requires nT a multiple of 8)
+        using F = std::false_type;
+        using first = std::integral_constant<int, 0>;
+        using second = std::integral_constant<int, 1>;
+        using first_of_first = std::integral_constant<int, 2>;
+        using first_of_last = std::integral_constant<int, 4>;
+        using second_of_last = std::integral_constant<int, 5>;
+        using first_of_only = std::integral_constant<int, 6>;
+        if (nt == 2) {
+            tblock(t0, F{}, first_of_only{});
+            tblock(t0 + 1, F{}, second_of_last{});
+        } else {
+            tblock(t0, F{}, first_of_first{});
+            tblock(t0 + 1, F{}, second{});
+            for (int T = t0 + 2; T + 2 < t1; T += 2) {
+                tblock(T, F{}, first{});
+                tblock(T + 1, F{}, second{});
+            }
+            tblock(t1 - 2, F{}, first_of_last{});
+            tblock(t1 - 1, F{}, second_of_last{});
+        }
+    } else {
+        using single = std::integral_constant<int, -1>;
+        for (int T = t0; T + 1 < t1; ++T) tblock(T, std::false_type{}, single{});
+        if (nt > 0) tblock(t1 - 1, std::true_type{}, single{});
+    }
 
     // Sum the four K parts of every output tile through LDS, as in
     // gemm_int4_kslice_kernel, once the last loads into LDS have landed.
@@ -1668,22 +1824,25 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
     }
 }
 
-// Returns -1 when the kernel does not apply (LDS or 32-bit offsets).
-template <int MT, bool SHUF>
+// Returns -1 when the kernel does not apply (LDS or 32-bit offsets; for the
+// pair form, the shuffled layout or K not a multiple of 1024).
+template <int MT, bool SHUF, bool PAIR>
 int launch_kslds(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
                  const uint16_t* X, uint16_t* Y, int M, int N, int K, int gshift, hipStream_t stream) {
-    const size_t lds = kslds_lds_bytes<MT>(K / kTBlock);
+    const int nT = K / kTBlock;
+    if (PAIR && (SHUF || nT % (2 * kKsWaves) != 0)) return -1;
+    const size_t lds = kslds_lds_bytes<MT, PAIR>(nT);
     if (lds > 160 * 1024 || static_cast<uint64_t>((N + 15) / 16) * 16 * (K / 2) >= (uint64_t{1} << 32) ||
         static_cast<uint64_t>(M) * K * 2 >= (uint64_t{1} << 32))
         return -1;
     static bool attr_set = [] {
-        return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_int4_kslds_kernel<MT, SHUF>),
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_int4_kslds_kernel<MT, SHUF, PAIR>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
     }();
     if (!attr_set) return kc::set_error(KC_ERR_HIP, "%s: cannot raise the LDS limit", fn);
     const unsigned grid = static_cast<unsigned>((N + 16 * kKlRT - 1) / (16 * kKlRT));
-    gemm_int4_kslds_kernel<MT, SHUF><<<grid, kKsWaves * kWave, lds, stream>>>(packed, scales, zeros, X, Y, M, N,
-                                                                               K, gshift);
+    gemm_int4_kslds_kernel<MT, SHUF, PAIR><<<grid, kKsWaves * kWave, lds, stream>>>(packed, scales, zeros, X, Y,
+                                                                                     M, N, K, gshift);
     return kc::check_launch(fn);
 }
 
@@ -1907,30 +2066,44 @@ int gemm_int4(const char* fn, const uint8_t* d_packed, const float* d_scales,
         return KC_SUCCESS;
     }
     const int gshift = kc::ilog2(group_size) - 7;
-    // M <= 8 on the reference layout: the X-resident kernel when its LDS fits
-    // in some number of phases of K.  On the shuffled layout the K-split
-    // kernel below is faster from M = 2 (K 8192, N 28672: M 2 / 4 / 8 in
-    // 26.0 / 25.1 / 25.2 us against 27.5 / 27.3 / 28.2; on the reference
-    // layout 31.4 / 31.4 / 32.6 against 32.2 / 31.5 / 32.7, the same).
+    // M <= 8 on the reference layout: the K-split kernel below in its pair
+    // form where that applies (K a multiple of 1024, up to 12288), else the
+    // X-resident kernel when its LDS fits in some number of phases of K.  On
+    // the shuffled layout the K-split kernel below from M = 2.  (K 8192,
+    // N 28672, MI355X: M 2 / 4 / 8 in 25.3 / 25.1 / 25.3 us on the reference
+    // layout against 30.3 / 30.6 / 32.0 for the X-resident kernel; 25.4 /
+    // 25.4 / 25.2 on the shuffled layout against 27.5 / 27.3 / 28.2.)
     if (m <= kXresBestM && !SHUF) {
+        const int st = launch_kslds<1, SHUF, true>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift,
+                                                  stream);
+        if (st >= 0) return st;
         const int P = xres_phases(m, cols, (cols / kTBlock) >> gshift);
         if (P > 0)
             return launch_xres<kXresW, kXresD, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols,
                                                gshift, P, stream);
     }
-    // M 9..64: the K-split kernels, operands through LDS where they fit,
+    // M 9..64: the K-split kernels, operands through LDS where they fit (on
+    // the reference layout in pairs of T-blocks up to M 32 where K allows),
     // else through registers (K 8192, N 28672, MI355X, reference layout:
-    // M 16 / 32 / 48 / 64 in 34 / 40 / 48 / 59 us through LDS, 37 / 48 / 58 /
+    // M 16 / 32 / 48 / 64 in 26 / 31 / 42 / 48 us through LDS, 37 / 48 / 58 /
     // 69 us through registers, 41 / 77 / 95 / 101 us for the kernels below,
     // which remain for shapes neither takes: K above about 20000, where the
     // coefficient stage does not fit in LDS, or operands of 4 GiB).
     if (m > kXresBestM || SHUF) {
         int st = -1;
+        if constexpr (!SHUF) {
+            switch ((m + 15) / 16) {
+                case 1: st = launch_kslds<1, SHUF, true>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+                case 2: st = launch_kslds<2, SHUF, true>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+                default: break;
+            }
+            if (st >= 0) return st;
+        }
         switch ((m + 15) / 16) {
-            case 1: st = launch_kslds<1, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
-            case 2: st = launch_kslds<2, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
-            case 3: st = launch_kslds<3, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
-            default: st = launch_kslds<4, SHUF>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+            case 1: st = launch_kslds<1, SHUF, false>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+            case 2: st = launch_kslds<2, SHUF, false>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+            case 3: st = launch_kslds<3, SHUF, false>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+            default: st = launch_kslds<4, SHUF, false>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
         }
         if (st >= 0) return st;
         switch ((m + 15) / 16) {

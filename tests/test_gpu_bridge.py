@@ -168,9 +168,9 @@ def test_stub_ops_raise_inside_their_span(gpu):
 @pytest.mark.parametrize("m,rows,cols", [(4, 300, 2048), (16, 100, 4096), (1, 4096, 4096)])
 def test_bridge_shuffled_gemm(gpu, oracle, m, rows, cols):
     """int4_shuffle_mfma + int4_gemm_bf16_shuffled: bit for bit the
-    reference-layout int4_gemm_bf16 for m >= 9 (the same kernels); m 2..8 (the
-    K-split kernel on the shuffled layout, the X-resident one on the
-    reference layout) and m == 1 within the bf16 bar of the fp64 oracle."""
+    reference-layout int4_gemm_bf16 for m >= 2 at these K (multiples of 1024
+    up to 12288: the same K-split kernel reads both layouts); m == 1 (a
+    GEMV of its own on each layout) within the bf16 bar of the fp64 oracle."""
     torch = gpu
     gs = 128
     p, s, z = make_int4(rows, cols, gs, seed=rows + m)
@@ -180,7 +180,7 @@ def test_bridge_shuffled_gemm(gpu, oracle, m, rows, cols):
     sh = ops.int4_shuffle_mfma(dp, rows, cols)
     assert sh.numel() == (rows + 15) // 16 * 16 * cols // 2
     y = ops.int4_gemm_bf16_shuffled(sh, ds, dz, x, rows, cols, gs)
-    if m >= 9:
+    if m >= 2:
         assert torch.equal(y.view(torch.int16), ops.int4_gemm_bf16(dp, ds, dz, x, rows, cols, gs).view(torch.int16))
     else:
         xbits = (x.float().cpu().numpy().view(np.uint32) >> 16).astype(np.uint16)

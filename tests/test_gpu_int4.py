@@ -325,7 +325,15 @@ def test_gemm_cfg3(gpu, oracle, m):
                                             (26, 130, 1152, 128), (40, 200, 4096, 512),
                                             # M 33..64 whose coefficients do not fit
                                             # in LDS: the X-resident fallback
-                                            (64, 50, 24576, 128)])
+                                            (64, 50, 24576, 128),
+                                            # reference layout in pairs of T-blocks:
+                                            # one pair per wave, three and five pairs
+                                            # with groups of 256 / 512, ragged rows, and
+                                            # K at the pair form's LDS limit for one and
+                                            # two activation tiles
+                                            (3, 200, 1024, 128), (2, 77, 3072, 256),
+                                            (5, 1000, 5120, 512), (8, 130, 12288, 128),
+                                            (32, 100, 9216, 128), (20, 60, 10240, 128)])
 def test_gemm_shapes(gpu, oracle, m, rows, cols, gs):
     packed, scales, zeros = make_int4(rows, cols, gs, seed=m * 1000 + rows)
     xb = normal_bf16((m, cols), seed=m + rows)

@@ -1,13 +1,15 @@
 """The shuffled INT4 layout of the matrix-core kernels (kc_shuffle_int4_mfma,
 kc_gemm_int4_bf16_shuffled): the weight-format bridge's optional
 "MFMA-friendly" layout.  Bars: the conversion bit for bit against the oracle
-(kco_shuffle_int4_mfma, itself pinned in test_oracle.py); for m >= 9 the
+(kco_shuffle_int4_mfma, itself pinned in test_oracle.py); where both layouts
+run the same kernel (m >= 9, and m 2..8 with K a multiple of 1024 up to
+12288, where the reference layout takes the K-split kernel's pair form) the
 GEMM on the shuffled layout bit for bit against kc_gemm_int4_bf16 on the
-reference layout (the same kernels and arithmetic, other addresses); for
-m 2..8 (the K-split kernel on the shuffled layout, the X-resident kernel on
-the reference layout: other summation orders) and m == 1 (a matrix-core GEMV
-of its own) within the bf16 tolerance of the fp64 oracle, as the other bf16
-GEMM and GEMV tests."""
+reference layout (the same arithmetic, other addresses); for the other
+m 2..8 shapes (the K-split kernel on the shuffled layout, the X-resident
+kernel on the reference layout: other summation orders) and m == 1 (a
+matrix-core GEMV of its own) within the bf16 tolerance of the fp64 oracle, as
+the other bf16 GEMM and GEMV tests."""
 import ctypes
 
 import numpy as np
@@ -81,12 +83,19 @@ GEMM_SHAPES = [(3, 64, 256, 128), (17, 130, 2048, 256), (33, 48, 640, 128), (64,
                (48, 200, 8192, 128), (20, 224, 4096, 128), (32, 1000, 4096, 128),
                (40, 113, 16384, 128), (17, 7, 256, 256), (63, 1, 512, 128), (26, 130, 1152, 128),
                (40, 200, 4096, 512), (64, 50, 24576, 128), (4, 28672, 8192, 128),
-               (16, 28672, 8192, 128), (64, 28672, 8192, 128)]
+               (16, 28672, 8192, 128), (64, 28672, 8192, 128),
+               # the reference layout's pair form: one and three pairs per wave,
+               # K at its limit for M <= 16; past its limit for M <= 32
+               (3, 200, 1024, 128), (2, 77, 3072, 256), (8, 130, 12288, 128),
+               (20, 60, 10240, 128)]
 
 
-# below this M the two layouts run different kernels (shuffled: K-split,
-# reference: X-resident)
-SAME_KERNELS_FROM_M = 9
+def same_kernels(m, cols):
+    """Whether both layouts run the same GEMM kernel: the K-split kernel from
+    m = 9, and from m = 2 where the reference layout takes its pair form (K a
+    multiple of 1024, up to 12288); other m 2..8 shapes run the X-resident
+    kernel on the reference layout."""
+    return m >= 9 or (m >= 2 and cols % 1024 == 0 and cols <= 12288)
 
 
 @pytest.mark.parametrize("m,rows,cols,gs", GEMM_SHAPES)
@@ -98,7 +107,7 @@ def test_gemm_shuffled_equals_reference_layout(gpu, oracle, m, rows, cols, gs):
     ref = _gemm(torch, "kc_gemm_int4_bf16", dp, ds, dz, dx, m, rows, cols, gs)
     sh = _shuffle(torch, dp, rows, cols)
     y = _gemm(torch, "kc_gemm_int4_bf16_shuffled", sh, ds, dz, dx, m, rows, cols, gs)
-    if m >= SAME_KERNELS_FROM_M:
+    if same_kernels(m, cols):
         assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
     else:
         truth = oracle.gemm_int4_bf16_f64(packed, scales, zeros.reshape(-1), xb, m, rows, cols, gs,
