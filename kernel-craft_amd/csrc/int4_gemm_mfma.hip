@@ -28,9 +28,9 @@
 // Kernels, by M (kc_gemm_int4_bf16 at the bottom picks one):
 //   M 2..64   gemm_int4_kslds_kernel: K split over the four waves of a CU, X
 //             and the weights streamed into LDS by direct-to-LDS loads; on
-//             the reference layout at M <= 32 with K a multiple of 1024 the
+//             the reference layout at M <= 48 with K a multiple of 1024 the
 //             weights come in pairs of T-blocks (whole 128-byte rows; K up to
-//             12288 at M <= 16, 9216 at M <= 32), otherwise one T-block at a
+//             12288 / 9216 / 12288 at M <= 16 / 32 / 48), otherwise one T-block at a
 //             time (K up to 16384 / 13824 / 11776 / 9216 at M <= 16 / 32 /
 //             48 / 64), and on the reference layout at M <= 8 only in the
 //             pair form;
@@ -1242,8 +1242,9 @@ int launch_kslice(const char* fn, const uint8_t* packed, const float* scales, co
 //   * W: per T-block and row tile the wave-wide 1-KB load of the register
 //     kernel, lane l's 16 bytes in slot l.  On the reference layout that
 //     load reads 64 bytes from each of 16 rows, and 16 neighbouring lanes
-//     touch 16 cache lines; with K a multiple of 1024 (and the LDS for
-//     2-KB slots, M <= 32) the weights instead come per pair of T-blocks,
+//     touch 16 cache lines; with K a multiple of 1024 and M <= 48 (the LDS
+//     for 2-KB slots; at M 33..48 the zero points kept as bytes) the weights
+//     instead come per pair of T-blocks,
 //     two loads per tile of 8 whole 128-byte rows each (8 lanes per row).
 //     The first T-block of the pair reads both halves of every tile and
 //     keeps the second T-block's in registers; it then requests the next
@@ -1321,13 +1322,20 @@ __device__ __forceinline__ void wait_vmcnt_n(int n) {
     }
 }
 
+// Zero points kept as bytes (c2 = -s (136 + z) formed where it is read):
+// pairs of T-blocks with three activation tiles, where only the zero-point
+// pass on the fp32 matrix core reads them, once per four T-blocks.
+template <int MT, bool PAIR>
+constexpr bool kKslZBytes = PAIR && MT >= 3;
+
 // Per-wave LDS: X (4 MT KB), weights (RT KB, or 2 RT KB for a pair of
 // T-blocks), fold coefficients of the wave's quarter (ceil(nT / 4) T-blocks
-// x kKlCS x (s, c2)).
+// x kKlCS x (s, c2), or (s, z) with z a byte, the byte table rounded to 16).
 template <int MT, bool PAIR>
 __host__ __device__ constexpr size_t kslds_wave_bytes(int nT) {
-    return static_cast<size_t>(4 * MT + (PAIR ? 2 : 1) * kKlRT) * 1024 +
-           static_cast<size_t>((nT + kKsWaves - 1) / kKsWaves) * kKlCS * 8;
+    const size_t nq = static_cast<size_t>((nT + kKsWaves - 1) / kKsWaves);
+    const size_t coef = kKslZBytes<MT, PAIR> ? nq * kKlCS * 4 + (nq * kKlCS + 15) / 16 * 16 : nq * kKlCS * 8;
+    return static_cast<size_t>(4 * MT + (PAIR ? 2 : 1) * kKlRT) * 1024 + coef;
 }
 
 template <int MT, bool PAIR>
@@ -1361,6 +1369,8 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
     char* wl = xl + kXB * 1024;
     float* cs = reinterpret_cast<float*>(wl + (PAIR ? 2 : 1) * RT * 1024);
     float* cz = cs + ntmax * kCS;
+    constexpr bool kZB = kKslZBytes<MT, PAIR>;
+    uint8_t* czb = reinterpret_cast<uint8_t*>(cz);  // zero points, when kZB
     const uint32_t x_lds = lds_addr(xl), w_lds = lds_addr(wl);
 
     // DMA offsets.  X block j, lane l: row 4 j + r (r = l / 16), chunk u.
@@ -1488,7 +1498,8 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
                     for (int e = 0; e < 4; ++e) {
                         const uint32_t z = (zq[b] >> (4 * e)) & 0xFu;
                         cs[(4 * q + e) * kCS + r] = sv[e];
-                        cz[(4 * q + e) * kCS + r] = -sv[e] * static_cast<float>(136u + z);
+                        if constexpr (kZB) czb[(4 * q + e) * kCS + r] = static_cast<uint8_t>(z);
+                        else cz[(4 * q + e) * kCS + r] = -sv[e] * static_cast<float>(136u + z);
                     }
                 }
             }
@@ -1559,7 +1570,8 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
                     const int g = (t0 + t) >> gshift;
                     const uint32_t z = (g & 1) ? (zb[b] >> 4) : (zb[b] & 0xFu);
                     cs[t * kCS + r] = sv[b];
-                    cz[t * kCS + r] = -sv[b] * static_cast<float>(136u + z);
+                    if constexpr (kZB) czb[t * kCS + r] = static_cast<uint8_t>(z);
+                    else cz[t * kCS + r] = -sv[b] * static_cast<float>(136u + z);
                 }
             }
         }
@@ -1746,7 +1758,11 @@ __global__ __launch_bounds__(kKsWaves * kWave) void gemm_int4_kslds_kernel(
                 const int tz = min(g0 + kb, nt - 1);  // lanes past the range hold xs = 0
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt) {
-                    const float av = cz[tz * kCS + 16 * rt + i];
+                    float av;
+                    if constexpr (kZB)  // the staging's c2, formed the same way
+                        av = -cs[tz * kCS + 16 * rt + i] * static_cast<float>(136u + czb[tz * kCS + 16 * rt + i]);
+                    else
+                        av = cz[tz * kCS + 16 * rt + i];
 #pragma unroll
                     for (int c = 0; c < MT; ++c) acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, xsb[c], acc[rt][c], 0, 0, 0);
                 }
@@ -1830,7 +1846,7 @@ template <int MT, bool SHUF, bool PAIR>
 int launch_kslds(const char* fn, const uint8_t* packed, const float* scales, const uint8_t* zeros,
                  const uint16_t* X, uint16_t* Y, int M, int N, int K, int gshift, hipStream_t stream) {
     const int nT = K / kTBlock;
-    if (PAIR && (SHUF || nT % (2 * kKsWaves) != 0)) return -1;
+    if (PAIR && (SHUF || MT > 3 || nT % (2 * kKsWaves) != 0)) return -1;
     const size_t lds = kslds_lds_bytes<MT, PAIR>(nT);
     if (lds > 160 * 1024 || static_cast<uint64_t>((N + 15) / 16) * 16 * (K / 2) >= (uint64_t{1} << 32) ||
         static_cast<uint64_t>(M) * K * 2 >= (uint64_t{1} << 32))
@@ -2083,9 +2099,9 @@ int gemm_int4(const char* fn, const uint8_t* d_packed, const float* d_scales,
                                                gshift, P, stream);
     }
     // M 9..64: the K-split kernels, operands through LDS where they fit (on
-    // the reference layout in pairs of T-blocks up to M 32 where K allows),
+    // the reference layout in pairs of T-blocks up to M 48 where K allows),
     // else through registers (K 8192, N 28672, MI355X, reference layout:
-    // M 16 / 32 / 48 / 64 in 26 / 31 / 42 / 48 us through LDS, 37 / 48 / 58 /
+    // M 16 / 32 / 48 / 64 in 26 / 31 / 38 / 47 us through LDS, 37 / 48 / 58 /
     // 69 us through registers, 41 / 77 / 95 / 101 us for the kernels below,
     // which remain for shapes neither takes: K above about 20000, where the
     // coefficient stage does not fit in LDS, or operands of 4 GiB).
@@ -2095,7 +2111,8 @@ int gemm_int4(const char* fn, const uint8_t* d_packed, const float* d_scales,
             switch ((m + 15) / 16) {
                 case 1: st = launch_kslds<1, SHUF, true>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
                 case 2: st = launch_kslds<2, SHUF, true>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
-                default: break;
+                case 3: st = launch_kslds<3, SHUF, true>(fn, d_packed, d_scales, d_zeros, d_x, d_y, m, rows, cols, gshift, stream); break;
+                default: break;  // four activation tiles: one T-block at a time (faster there)
             }
             if (st >= 0) return st;
         }

@@ -329,11 +329,21 @@ def test_gemm_cfg3(gpu, oracle, m):
                                             # reference layout in pairs of T-blocks:
                                             # one pair per wave, three and five pairs
                                             # with groups of 256 / 512, ragged rows, and
-                                            # K at the pair form's LDS limit for one and
-                                            # two activation tiles
+                                            # K at the pair form's LDS limit for one to
+                                            # four activation tiles; three pairs with a
+                                            # last group of two T-blocks for the
+                                            # zero-point pass
                                             (3, 200, 1024, 128), (2, 77, 3072, 256),
                                             (5, 1000, 5120, 512), (8, 130, 12288, 128),
-                                            (32, 100, 9216, 128), (20, 60, 10240, 128)])
+                                            (32, 100, 9216, 128), (20, 60, 10240, 128),
+                                            (36, 90, 12288, 128), (64, 100, 8192, 128),
+                                            (50, 77, 3072, 256),
+                                            # four activation tiles, one T-block at a
+                                            # time: tiles past the last row, two
+                                            # T-blocks per wave, K at the pair form's
+                                            # limit for one tile fewer
+                                            (50, 80, 3072, 256), (49, 224, 1024, 128),
+                                            (64, 96, 8192, 128)])
 def test_gemm_shapes(gpu, oracle, m, rows, cols, gs):
     packed, scales, zeros = make_int4(rows, cols, gs, seed=m * 1000 + rows)
     xb = normal_bf16((m, cols), seed=m + rows)
