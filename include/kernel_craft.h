@@ -226,10 +226,12 @@ int kc_gemm_int4_bf16(const uint8_t* d_packed, const float* d_scales,
  *     multiple of 128.
  *   kc_shuffle_int4_mfma: packed [rows, cols/2] -> that buffer (16-byte
  *     aligned, not overlapping).
- *   kc_gemm_int4_bf16_shuffled: kc_gemm_int4_bf16 on the shuffled weights.
- *     For m >= 2 the same kernels, reading 1 KB of the layout per wave-wide
- *     load instead of 64 bytes of each of 16 rows: bit-identical results.
- *     m == 1 runs a matrix-core GEMV when cols = 1024 * KW (KW <= 16), or
+ *   kc_gemm_int4_bf16_shuffled: kc_gemm_int4_bf16 on the shuffled weights,
+ *     each wave-wide load reading 1 KB of the layout.  For m >= 9, and for
+ *     m 2..8 with cols a multiple of 1024 up to 12288, the same kernel as
+ *     kc_gemm_int4_bf16 on the same values: bit-identical results.  Other
+ *     m 2..8 shapes run the K-split kernel here and the X-resident kernel
+ *     on the reference layout (another summation order).  m == 1 runs a matrix-core GEMV when cols = 1024 * KW (KW <= 16), or
  *     cols = 512 * KW (KW <= 16) with rows <= 8192 (four k-blocks per wave);
  *     other cols take the m >= 2 kernel.  Within the bf16 tolerance of the
  *     reference GEMV.  Needs cols % 128 == 0, group_size a power of two
