@@ -343,7 +343,10 @@ def test_gemm_cfg3(gpu, oracle, m):
                                             # T-blocks per wave, K at the pair form's
                                             # limit for one tile fewer
                                             (50, 80, 3072, 256), (49, 224, 1024, 128),
-                                            (64, 96, 8192, 128)])
+                                            (64, 96, 8192, 128),
+                                            # the pair form with fewer rows than one
+                                            # 16-row tile (every row clamped to N - 1)
+                                            (9, 5, 2048, 128), (2, 1, 1024, 128)])
 def test_gemm_shapes(gpu, oracle, m, rows, cols, gs):
     packed, scales, zeros = make_int4(rows, cols, gs, seed=m * 1000 + rows)
     xb = normal_bf16((m, cols), seed=m + rows)
