@@ -718,10 +718,10 @@ bool launch_fast_cpl(int slot, const GemvArgs& a, int rows, int cols, int gshift
 }
 
 // The per-lane-x kernel for GEMVs whose K is 2048 x KW (KW 2..8):
-// R = 4 rows per wave (8 for KW >= 3 with N >= 16384), two row groups per
-// workgroup at KW = 2; at KW = 2 only up to N = 16384 (the staged kernel is
-// as fast or faster on the larger K = 4096 shapes).  False when it does not
-// apply.
+// R = 4 rows per wave (8 for KW >= 3 with at least 24 MiB of packed
+// weights), two row groups per workgroup at KW = 2; at KW = 2 only up to
+// N = 16384 (the staged kernel is as fast or faster on the larger K = 4096
+// shapes).  False when it does not apply.
 template <bool NORM, bool BF16>
 bool launch_xl(const GemvArgs& a, int64_t rows, int64_t cols, int gshift, hipStream_t stream) {
     if (cols % 2048 != 0 || rows > INT32_MAX) return false;
@@ -732,7 +732,11 @@ bool launch_xl(const GemvArgs& a, int64_t rows, int64_t cols, int gshift, hipStr
     // N = 14336 (the staged kernel's 4 rows per wave)
     if (!BF16 && rows >= 8192) return false;
     const int r = static_cast<int>(rows), c = static_cast<int>(cols);
-    const bool wide = kw >= 3 && rows >= 16384;
+    // Eight rows per wave halve the waves and the x loads per weight byte:
+    // faster from about 24 MiB of weights (N 4096: K 14336 7.60 -> 7.45 us,
+    // K 16384 8.21 -> 7.99; N 8192 K 8192 8.23 -> 8.00), even at 14-16 MiB,
+    // slower below (N 4096 K 6144 4.39 -> 4.60).  Same outputs either way.
+    const bool wide = kw >= 3 && static_cast<int64_t>(rows) * (cols / 2) >= (int64_t{24} << 20);
 #define KC_XL(KWV, RV, RGWV)                                                                     \
     gemv_int4_xl_kernel<RV, KWV, RGWV, NORM, BF16><<<static_cast<unsigned>((r + RV * RGWV - 1) / (RV * RGWV)), \
                                                KWV * RGWV * kWave, 0, stream>>>(                 \
