@@ -346,7 +346,11 @@ def test_gemm_cfg3(gpu, oracle, m):
                                             (64, 96, 8192, 128),
                                             # the pair form with fewer rows than one
                                             # 16-row tile (every row clamped to N - 1)
-                                            (9, 5, 2048, 128), (2, 1, 1024, 128)])
+                                            (9, 5, 2048, 128), (2, 1, 1024, 128),
+                                            # M 33..64 with fewer rows than a workgroup's
+                                            # 112, K 2048-6144
+                                            (40, 40, 2048, 128), (64, 16, 4096, 128),
+                                            (35, 200, 6144, 128), (57, 1000, 2048, 128)])
 def test_gemm_shapes(gpu, oracle, m, rows, cols, gs):
     packed, scales, zeros = make_int4(rows, cols, gs, seed=m * 1000 + rows)
     xb = normal_bf16((m, cols), seed=m + rows)
