@@ -25,7 +25,7 @@ import pytest
 
 import kc_abi
 from kc_abi import ptr, stream
-from kc_data import bf16_bits_to_f32, normal_bf16, rel_l2
+from kc_data import bf16_bits_to_f32, f32_to_bf16_bits, normal_bf16, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -67,24 +67,66 @@ SHAPES = [(128, 128, 128), (1, 1, 16), (16, 16, 128), (200, 300, 272), (37, 513,
           (256, 1024, 4096), (1000, 130, 48), (129, 129, 144), (512, 384, 8192)]
 
 
-@pytest.mark.parametrize("M,N,K", SHAPES)
-def test_integer_codes_bit_exact(gpu, oracle, M, N, K):
-    torch = gpu
-    rng = np.random.default_rng(M * 7 + N * 3 + K)
+def _integer_case(rng, oracle, M, N, K):
+    """Integer-valued codes and the output they must give bit for bit in fp32."""
     table = oracle.e4m3_decode_table()
     qx = _integer_codes(rng, (M, K), table)
     qw = _integer_codes(rng, (N, K), table)
     sx = rng.uniform(0.001, 2.0, M).astype(np.float32)
     sw = rng.uniform(0.001, 2.0, N).astype(np.float32)
-    y = _gemm(torch, qx, sx, qw, sw, bf16=False)
     acc = table[qx.view(np.uint8)].astype(np.float64) @ table[qw.view(np.uint8)].astype(np.float64).T
     assert np.abs(acc).max() < 2 ** 24
     want = (acc.astype(np.float32) * sx[:, None]) * sw[None, :]
+    return qx, sx, qw, sw, want
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("bf16", [False, True])
+def test_integer_codes_bit_exact(gpu, oracle, M, N, K, bf16):
+    """fp32 Y equals the exact sum scaled as (acc * sx) * sw; bf16 Y is that
+    value rounded to nearest even.  N covers every output path: N % 8 == 0
+    (bf16 rows staged through LDS), N % 4 == 0 (four columns per lane) and
+    the rest (one column at a time)."""
+    torch = gpu
+    rng = np.random.default_rng(M * 7 + N * 3 + K)
+    qx, sx, qw, sw, want = _integer_case(rng, oracle, M, N, K)
+    y = _gemm(torch, qx, sx, qw, sw, bf16=bf16)
+    if bf16:
+        want = bf16_bits_to_f32(f32_to_bf16_bits(want))
     if not np.array_equal(y.view(np.uint32), want.view(np.uint32)):
         bad = np.argwhere(y.view(np.uint32) != want.view(np.uint32))
         m, n = bad[0]
         raise AssertionError(f"{len(bad)} mismatches; first at {(m, n)}: gpu {y[m, n]!r} "
                              f"want {want[m, n]!r}")
+
+
+@pytest.mark.parametrize("bf16,offset", [(True, 0), (True, 1), (True, 4), (False, 1), (False, 2),
+                                          (False, 4)])
+def test_output_alignment(gpu, oracle, bf16, offset):
+    """Y at an element offset inside a larger buffer (N % 8 == 0): the
+    16-byte row stores need 16-byte alignment, the four-column stores 8 (bf16)
+    or 16 (fp32) bytes; other offsets take the one-column path.  Bit-exact on
+    integer codes, and nothing outside Y is written."""
+    torch = gpu
+    M, N, K = 200, 256, 272
+    rng = np.random.default_rng(offset * 13 + bf16)
+    qx, sx, qw, sw, want = _integer_case(rng, oracle, M, N, K)
+    dqx, dsx, dqw, dsw = _dev(torch, qx), _dev(torch, sx), _dev(torch, qw), _dev(torch, sw)
+    if bf16:
+        buf = torch.full((M * N + 16,), -7, dtype=torch.int16, device="cuda")
+        fn = kc_abi.lib().kc_gemm_fp8_w8a8_bf16
+        want = f32_to_bf16_bits(want).view(np.int16)
+    else:
+        buf = torch.full((M * N + 16,), -7.0, dtype=torch.float32, device="cuda")
+        fn = kc_abi.lib().kc_gemm_fp8_w8a8_f32
+    print(f"kc_gemm_fp8_w8a8 {'bf16' if bf16 else 'f32'} M={M} N={N} K={K} y offset {offset}", flush=True)
+    st = fn(ptr(dqx), ptr(dsx), ptr(dqw), ptr(dsw), buf.data_ptr() + offset * buf.element_size(), M, N, K,
+            stream())
+    kc_abi.check("kc_gemm_fp8_w8a8", st)
+    out = buf.cpu().numpy()
+    assert np.all(out[:offset] == -7) and np.all(out[offset + M * N:] == -7)
+    got = out[offset:offset + M * N].reshape(M, N)
+    assert np.array_equal(got.view(np.uint16 if bf16 else np.uint32), want.view(np.uint16 if bf16 else np.uint32))
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
