@@ -77,7 +77,8 @@ constexpr int kThreads = 512;
 constexpr int kBM = 256, kBN = 256, kBK = 128;
 constexpr int kTileBytes = kBM * kBK;            // one operand, one step
 constexpr int kStageBytes = 2 * kTileBytes;      // qx rows then qw rows
-constexpr int kLdsBytes = 2 * kStageBytes;       // double buffer: 128 KB
+constexpr int kScaleOff = 2 * kStageBytes;       // double buffer: 128 KB
+constexpr int kLdsBytes = kScaleOff + (kBM + kBN) * 4;  // + the tile's sx and sw
 constexpr int kGroupM = 4;
 constexpr int kE8M0One = 127;                    // block scale 2^0
 // instruction classes of __builtin_amdgcn_sched_group_barrier
@@ -222,32 +223,43 @@ __global__ __launch_bounds__(kThreads) void gemm_fp8_kernel(
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // One barrier per step: after it, every wave's loads of step s are in
-    // LDS and every wave has finished reading step s - 1's buffer, which then
-    // receives step s + 1 while step s is multiplied.  Full steps run in the
-    // loop, a partial last step (K % 128 != 0) after it, so that the loop
-    // body has one code path for the accumulators and ends in the MFMAs.
+    // One barrier per step, at its end: after it, every wave's loads of step
+    // s + 1 are in LDS and every wave has finished reading step s's buffer,
+    // which then receives step s + 2 while step s + 1 is multiplied.  Full
+    // steps run in the loop, a partial last step (K % 128 != 0) after it, so
+    // that the loop body has one code path for the accumulators.
     // Settle the scalar loads of the epilogue's pointers here: a scalar load
     // still in flight in the loop would make every LDS wait a full drain
     // (scalar loads return out of order on the same counter).
     asm volatile("" ::"s"(y), "s"(sx), "s"(sw));
     const int full = static_cast<int>(K / kBK);
     const int steps = static_cast<int>((K + kBK - 1) / kBK);
+    // The tile's row and column scales wait in LDS for the epilogue: thread
+    // t < 256 loads sx of row m0 + t, the others sw of column n0 + t - 256 (0
+    // past the end), ahead of the first operand loads, and stores the value
+    // once those have landed.
+    float* scl = reinterpret_cast<float*>(lds + kScaleOff);  // [kBM sx][kBN sw]
+    const int tt = static_cast<int>(threadIdx.x);
+    const int64_t si = tt < kBM ? m0 + tt : n0 + (tt - kBM);
+    const float sval = tt < kBM ? (si < M ? sx[si] : 0.0f) : (si < N ? sw[si] : 0.0f);
     load_stage(qx, qw, M, N, K, m0, n0, 0, lds, wave, lane);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    scl[tt] = sval;
     for (int s = 0; s < full; ++s) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
         if (s + 1 < steps)
             load_stage(qx, qw, M, N, K, m0, n0, static_cast<int64_t>(s + 1) * kBK,
                        lds + ((s + 1) & 1) * kStageBytes, wave, lane);
         mfma_step_full(lds + (s & 1) * kStageBytes, wm, wn, lane, acc);
-    }
-    if (full < steps) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+    }
+    if (full < steps) {
         mfma_step<true>(lds + (full & 1) * kStageBytes, wm, wn, lane,
                         static_cast<int>(K - static_cast<int64_t>(full) * kBK), acc);
+        __syncthreads();
     }
+    // Here every wave has read its last operands and the scales are in LDS.
 
     // D layout of a 16 x 16 tile (the qw block as A, the qx block as B):
     // lane (j, g) holds columns n = 4g + v (v < 4) of row m = j, so each lane
@@ -258,17 +270,14 @@ __global__ __launch_bounds__(kThreads) void gemm_fp8_kernel(
             // Each wave stages its 128 x 64 bf16 block in its own 16 KB of LDS
             // (128-byte rows, 16-byte chunks XOR-swizzled by row % 8), then
             // writes whole 128-byte row pieces, 16 bytes per lane, nontemporal.
-            __syncthreads();  // every wave has read its last operands: the LDS is free
             uint8_t* wl = lds + wave * (kBM / 2) * (kBN / 4) * 2;
 #pragma unroll
             for (int mi = 0; mi < 8; ++mi) {
                 const int row = 16 * mi + j;
-                const int64_t m = m0 + 128 * wm + row;
-                const float sxm = m < M ? sx[m] : 0.0f;
+                const float sxm = scl[128 * wm + row];
 #pragma unroll
                 for (int ni = 0; ni < 4; ++ni) {
-                    const int64_t n = n0 + 64 * wn + 16 * ni + 4 * g;
-                    const f32x4 s4 = n < N ? *reinterpret_cast<const f32x4*>(sw + n) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    const f32x4 s4 = *reinterpret_cast<const f32x4*>(scl + kBM + 64 * wn + 16 * ni + 4 * g);
                     const uint32_t lo = kc::f32_to_bf16((acc[mi][ni][0] * sxm) * s4.x) |
                                         static_cast<uint32_t>(kc::f32_to_bf16((acc[mi][ni][1] * sxm) * s4.y)) << 16;
                     const uint32_t hi = kc::f32_to_bf16((acc[mi][ni][2] * sxm) * s4.z) |
@@ -293,12 +302,13 @@ __global__ __launch_bounds__(kThreads) void gemm_fp8_kernel(
     for (int mi = 0; mi < 8; ++mi) {
         const int64_t m = m0 + 128 * wm + 16 * mi + j;
         if (m >= M) continue;
-        const float sxm = sx[m];
+        const float sxm = scl[128 * wm + 16 * mi + j];
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) {
-            const int64_t n = n0 + 64 * wn + 16 * ni + 4 * g;
+            const int nl = 64 * wn + 16 * ni + 4 * g;
+            const int64_t n = n0 + nl;
             if (vec && n + 3 < N) {
-                const f32x4 s4 = *reinterpret_cast<const f32x4*>(sw + n);
+                const f32x4 s4 = *reinterpret_cast<const f32x4*>(scl + kBM + nl);
                 const float r0 = (acc[mi][ni][0] * sxm) * s4.x, r1 = (acc[mi][ni][1] * sxm) * s4.y;
                 const float r2 = (acc[mi][ni][2] * sxm) * s4.z, r3 = (acc[mi][ni][3] * sxm) * s4.w;
                 if constexpr (YBF16) {
@@ -312,7 +322,7 @@ __global__ __launch_bounds__(kThreads) void gemm_fp8_kernel(
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     if (n + v >= N) break;
-                    const float rv = (acc[mi][ni][v] * sxm) * sw[n + v];
+                    const float rv = (acc[mi][ni][v] * sxm) * scl[kBM + nl + v];
                     if constexpr (YBF16) static_cast<uint16_t*>(y)[m * N + n + v] = kc::f32_to_bf16(rv);
                     else static_cast<float*>(y)[m * N + n + v] = rv;
                 }
@@ -364,8 +374,7 @@ int gemm_fp8(const char* fn, const int8_t* qx, const float* sx, const int8_t* qw
     if (!attr_set) return kc::set_error(KC_ERR_HIP, "%s: cannot raise the LDS limit", fn);
     gemm_fp8_kernel<YBF16><<<static_cast<unsigned>(tm * tn), kThreads, kLdsBytes, stream>>>(
         qx, sx, qw, sw, y, M, N, K, static_cast<int>(tm), static_cast<int>(tn),
-        N % 4 == 0 && kc::aligned(sw, 16) && kc::aligned(y, YBF16 ? 8 : 16),
-        YBF16 && N % 8 == 0 && kc::aligned(sw, 16) && kc::aligned(y, 16));
+        N % 4 == 0 && kc::aligned(y, YBF16 ? 8 : 16), YBF16 && N % 8 == 0 && kc::aligned(y, 16));
     return kc::check_launch(fn);
 }
 
