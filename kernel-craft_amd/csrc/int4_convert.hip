@@ -31,15 +31,6 @@
 // nibble p = weight k = base + p, the same order as a GPTQ word: a GPTQ
 // word becomes an output word by one XOR, and the conversion is a transpose
 // of [K/8, N] words into [N, K/8] words through LDS tiles.
-//
-// The 16-byte stores of the outputs (packed words, scales, and the shuffled
-// layout below) are nontemporal: the outputs are not read again by the call,
-// and stores that allocate in L2 held the write stream back (gate/up layer,
-// 124 MB read + written per call: GPTQ 27.0 -> 22.0 us, AWQ 31.0 -> 21.8 us;
-// the shuffle of its packed weights 22.5 -> 18.9 us).  The zero-point bytes
-// and the scalar fallbacks keep ordinary stores, which L2 merges into whole
-// lines (nontemporal byte stores: GPTQ 23.3 against 21.8 us), and the source
-// loads ordinary loads (nontemporal: GPTQ 25.1 against 24.2 us).
 #include <algorithm>
 
 #include "kc_common.hpp"
@@ -210,8 +201,7 @@ __device__ __forceinline__ void convert_packed_tile(
         if (n >= N) continue;
         uint32_t* dst = out + static_cast<int64_t>(n) * KW + kb;
         if (vec && kb + 4 <= KW) {
-            __builtin_nontemporal_store(u32x4{tile[kbl][nl], tile[kbl + 1][nl], tile[kbl + 2][nl], tile[kbl + 3][nl]},
-                                        reinterpret_cast<u32x4*>(dst));
+            *reinterpret_cast<u32x4*>(dst) = u32x4{tile[kbl][nl], tile[kbl + 1][nl], tile[kbl + 2][nl], tile[kbl + 3][nl]};
         } else {
             for (int c = 0; c < 4 && kb + c < KW; ++c) dst[c] = tile[kbl + c][nl];
         }
@@ -251,9 +241,8 @@ __device__ __forceinline__ void convert_meta_tile(
         if (n < N) {
             float* dst = scales + static_cast<int64_t>(n) * G + g0 + gb;
             if ((G & 3) == 0 && g0 + gb + 8 <= G) {  // 16-byte aligned: G % 4 == 0
-                f32x4* d4 = reinterpret_cast<f32x4*>(dst);
-                __builtin_nontemporal_store(f32x4{sv[gb][nl], sv[gb + 1][nl], sv[gb + 2][nl], sv[gb + 3][nl]}, d4);
-                __builtin_nontemporal_store(f32x4{sv[gb + 4][nl], sv[gb + 5][nl], sv[gb + 6][nl], sv[gb + 7][nl]}, d4 + 1);
+                reinterpret_cast<f32x4*>(dst)[0] = f32x4{sv[gb][nl], sv[gb + 1][nl], sv[gb + 2][nl], sv[gb + 3][nl]};
+                reinterpret_cast<f32x4*>(dst)[1] = f32x4{sv[gb + 4][nl], sv[gb + 5][nl], sv[gb + 6][nl], sv[gb + 7][nl]};
             } else {
                 for (int e = 0; e < 8 && g0 + gb + e < G; ++e) dst[e] = sv[gb + e][nl];
             }
@@ -370,7 +359,7 @@ __global__ __launch_bounds__(kThreads) void shuffle_mfma_kernel(const u32x4* __r
         const int64_t row = tile * 16 + (l & 15);
         u32x4 v = u32x4{0u, 0u, 0u, 0u};
         if (row < rows) v = in[row * row_units + T * 4 + (l >> 4)];
-        __builtin_nontemporal_store(v, out + u);
+        out[u] = v;
     }
 }
 
