@@ -64,7 +64,7 @@ def _gemm(torch, qx, sx, qw, sw, bf16):
 
 
 SHAPES = [(128, 128, 128), (1, 1, 16), (16, 16, 128), (200, 300, 272), (37, 513, 1040),
-          (256, 1024, 4096), (1000, 130, 48), (129, 129, 144), (512, 384, 8192)]
+          (256, 1024, 4096), (1000, 130, 48), (129, 129, 144), (512, 384, 8192), (300, 520, 400)]
 
 
 def _integer_case(rng, oracle, M, N, K):
