@@ -100,6 +100,33 @@ def test_integer_codes_bit_exact(gpu, oracle, M, N, K, bf16):
                              f"want {want[m, n]!r}")
 
 
+def _random_shapes(n, seed=2024):
+    """Seeded shapes over every output path: N a multiple of 8 (bf16 rows
+    staged through LDS), of 4 (four columns per lane) or neither, with M, N
+    and K tails of every size."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        M = int(rng.integers(1, 700))
+        N = int(rng.integers(1, 90)) * (8, 4, 1)[i % 3] + (0, 0, int(rng.integers(0, 8)))[i % 3]
+        K = 16 * int(rng.integers(1, 70))
+        out.append((M, max(N, 1), K))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K", _random_shapes(12))
+def test_random_shapes_bit_exact(gpu, oracle, M, N, K):
+    """bf16 and fp32 Y on integer-valued codes, bit for bit, at seeded random
+    shapes."""
+    torch = gpu
+    rng = np.random.default_rng(M * 131 + N * 17 + K)
+    qx, sx, qw, sw, want = _integer_case(rng, oracle, M, N, K)
+    for bf16 in (True, False):
+        y = _gemm(torch, qx, sx, qw, sw, bf16=bf16)
+        w = bf16_bits_to_f32(f32_to_bf16_bits(want)) if bf16 else want
+        assert np.array_equal(y.view(np.uint32), w.view(np.uint32)), (M, N, K, bf16)
+
+
 @pytest.mark.parametrize("bf16,offset", [(True, 0), (True, 1), (True, 4), (False, 1), (False, 2),
                                           (False, 4)])
 def test_output_alignment(gpu, oracle, bf16, offset):
